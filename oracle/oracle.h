@@ -1,0 +1,89 @@
+/*
+ * CPU oracle for the quantized GGUF matrix product — TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load this library, and only as the checker. The product (charlotte_amd/)
+ * never links, loads or calls it.
+ *
+ * Each function restates one piece of plainsight-systems/charlotte's
+ * algorithm for this path, citing the reference file:line it follows.
+ * Pinning, per function (the checks live in tests/test_oracle.py):
+ *   orc_fp16_to_fp32        known answers of tests/quant_q4_0_test.cpp:41-65;
+ *                           all 65,536 inputs against numpy's float16 and
+ *                           against oracle/_ref (the reference's own code).
+ *   orc_dequantize_q4_0     known answers of tests/quant_q4_0_test.cpp:87-145;
+ *                           closed form; oracle/_ref on the edge-scale blocks
+ *                           of tests/gpu/unpack_q4_0_test.cpp:24-37.
+ *   orc_dequantize_q6_k     closed form (6-bit code, int8 scale, fp16 d) built
+ *                           from the stored fields independently in the test;
+ *                           oracle/_ref on tests/gpu/unpack_q6_k_test.cpp:24-41.
+ *   orc_repack_q6_k /
+ *   orc_lay_out             the placement invariant of
+ *                           tests/formats_q6_k_repack_test.cpp:24-69; byte
+ *                           equality with oracle/_ref's repack_q6_k.
+ *   orc_unpack_group        equality with the file-order dequant over every
+ *                           group (the device layout is lossless).
+ *   orc_matmul_f32          order of addition pinned by hand-built cases whose
+ *                           bits differ between orders (test_oracle.py), plus
+ *                           within gamma(2K) of orc_matmul_f64.
+ *   orc_matmul_f64          brute force against numpy float64 dot products.
+ *   orc_fill_unit           the hash of tests/gpu/support/fill.h:24-29, pinned
+ *                           by its range and by recomputation in numpy.
+ *   orc_activate            against math.exp/tanh within its stated bound.
+ * Nothing here is "parity unpinned".
+ */
+#ifndef CHARLOTTE_ORACLE_H
+#define CHARLOTTE_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGUF tensor types (src/core/gguf/types.h:41-43). */
+enum { ORC_F32 = 0, ORC_Q4_0 = 2, ORC_Q6_K = 14 };
+
+float orc_fp16_to_fp32(uint16_t h);
+
+/* File-order blocks -> f32 weights, flat. */
+void orc_dequantize_q4_0(const uint8_t* blocks, uint64_t nblocks, float* out);
+void orc_dequantize_q6_k(const uint8_t* blocks, uint64_t nblocks, float* out);
+/* Weights [first, first + count) of a tensor stored as `type` blocks. */
+int orc_dequantize_range(uint32_t type, const uint8_t* blocks, uint64_t first, uint64_t count, float* out);
+
+/* Device layout: bytes of a piece of `nblocks` blocks, rounded up to 4. */
+uint64_t orc_layout_bytes(uint32_t type, uint64_t nblocks);
+/* File-order blocks -> the piece's streams (SoA; Q6_K repacked). */
+int orc_lay_out(uint32_t type, const uint8_t* blocks, uint64_t nblocks, uint8_t* device);
+void orc_repack_q6_k(const uint8_t* blocks, uint64_t nblocks, uint8_t* lo, uint8_t* hi, uint8_t* scales,
+                     uint8_t* d);
+/* The 32 weights of `group` read from a piece's streams. */
+int orc_unpack_group(uint32_t type, const uint8_t* device, uint64_t blocks_in_piece, uint64_t group, float* out);
+
+/* The canonical range of a row of G groups: groups [lo(r), lo(r + 1)). */
+uint64_t orc_range_lo(uint64_t r, uint64_t groups);
+
+/* y[t * rows + o] over file-order blocks, in the reference's order of
+ * addition (32 ranges, each an fma chain from zero, added in order). */
+int orc_matmul_f32(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t columns, const float* x,
+                   uint32_t tokens, float* y, uint32_t threads);
+/* The same in f64, and each output's bound gamma(2K) * sum |w x|. */
+int orc_matmul_f64(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t columns, const float* x,
+                   uint32_t tokens, double* y, double* bound);
+
+/* tests/gpu/support/fill.h:24-29: a value in [-1, 1) for index i. */
+float orc_fill_unit(uint32_t i);
+void orc_fill(uint32_t seed, uint64_t count, float amplitude, float* out);
+
+/* matmul.wgsl:169-205: 0 SiLU, 1 GELU (tanh form), 2 sigmoid. */
+float orc_exp_nonpositive(float x);
+float orc_activate(uint32_t activation, float g);
+
+/* Monotonic seconds, for the CPU baseline timing. */
+double orc_now(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

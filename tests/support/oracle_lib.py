@@ -1,0 +1,171 @@
+"""ctypes bindings to the CPU oracle (oracle/liborc.so) and, where it was
+built, oracle/_ref/libref.so (the reference's own dequant/repack code).
+
+Test infrastructure only: tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg load these, as the checker.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+
+Q4_0, Q6_K = 2, 14
+BLOCK = {Q4_0: (32, 18), Q6_K: (256, 210)}
+
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+
+
+def _ptr(a, t):
+    return a.ctypes.data_as(t)
+
+
+def _bytes(b):
+    return np.frombuffer(b, dtype=np.uint8) if isinstance(b, (bytes, bytearray)) else np.ascontiguousarray(b, np.uint8)
+
+
+class Oracle:
+    def __init__(self, path=None):
+        path = path or os.path.join(ORACLE_DIR, "liborc.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built: run __graft_entry__.build() or make -C oracle")
+        lib = ctypes.CDLL(path)
+        lib.orc_fp16_to_fp32.restype = ctypes.c_float
+        lib.orc_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        for f in (lib.orc_dequantize_q4_0, lib.orc_dequantize_q6_k):
+            f.argtypes = [_u8p, ctypes.c_uint64, _f32p]
+        lib.orc_dequantize_range.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64, _f32p]
+        lib.orc_layout_bytes.restype = ctypes.c_uint64
+        lib.orc_layout_bytes.argtypes = [ctypes.c_uint32, ctypes.c_uint64]
+        lib.orc_lay_out.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, _u8p]
+        lib.orc_repack_q6_k.argtypes = [_u8p, ctypes.c_uint64, _u8p, _u8p, _u8p, _u8p]
+        lib.orc_unpack_group.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64, _f32p]
+        lib.orc_range_lo.restype = ctypes.c_uint64
+        lib.orc_range_lo.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+        lib.orc_matmul_f32.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64, _f32p,
+                                       ctypes.c_uint32, _f32p, ctypes.c_uint32]
+        lib.orc_matmul_f64.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64, _f32p,
+                                       ctypes.c_uint32, _f64p, _f64p]
+        lib.orc_fill_unit.restype = ctypes.c_float
+        lib.orc_fill_unit.argtypes = [ctypes.c_uint32]
+        lib.orc_fill.argtypes = [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, _f32p]
+        lib.orc_exp_nonpositive.restype = ctypes.c_float
+        lib.orc_exp_nonpositive.argtypes = [ctypes.c_float]
+        lib.orc_activate.restype = ctypes.c_float
+        lib.orc_activate.argtypes = [ctypes.c_uint32, ctypes.c_float]
+        lib.orc_now.restype = ctypes.c_double
+        self.lib = lib
+
+    def fp16_to_fp32(self, h):
+        return self.lib.orc_fp16_to_fp32(h)
+
+    def dequantize(self, gtype, blocks):
+        b = _bytes(blocks)
+        per, nbytes = BLOCK[gtype]
+        n = b.size // nbytes
+        out = np.empty(n * per, np.float32)
+        f = self.lib.orc_dequantize_q4_0 if gtype == Q4_0 else self.lib.orc_dequantize_q6_k
+        f(_ptr(b, _u8p), n, _ptr(out, _f32p))
+        return out
+
+    def layout_bytes(self, gtype, nblocks):
+        return self.lib.orc_layout_bytes(gtype, nblocks)
+
+    def lay_out(self, gtype, blocks):
+        b = _bytes(blocks)
+        n = b.size // BLOCK[gtype][1]
+        out = np.zeros(self.layout_bytes(gtype, n), np.uint8)
+        assert self.lib.orc_lay_out(gtype, _ptr(b, _u8p), n, _ptr(out, _u8p)) == 0
+        return out
+
+    def repack_q6_k(self, blocks):
+        b = _bytes(blocks)
+        n = b.size // 210
+        lo, hi = np.zeros(128 * n, np.uint8), np.zeros(64 * n, np.uint8)
+        sc, d = np.zeros(16 * n, np.uint8), np.zeros(2 * n, np.uint8)
+        self.lib.orc_repack_q6_k(_ptr(b, _u8p), n, _ptr(lo, _u8p), _ptr(hi, _u8p), _ptr(sc, _u8p), _ptr(d, _u8p))
+        return lo, hi, sc, d
+
+    def unpack_group(self, gtype, device, blocks_in_piece, group):
+        out = np.empty(32, np.float32)
+        assert self.lib.orc_unpack_group(gtype, _ptr(device, _u8p), blocks_in_piece, group, _ptr(out, _f32p)) == 0
+        return out
+
+    def range_lo(self, r, groups):
+        return self.lib.orc_range_lo(r, groups)
+
+    def matmul_f32(self, gtype, blocks, rows, columns, x, threads=1):
+        b = _bytes(blocks)
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, columns)
+        y = np.empty((x.shape[0], rows), np.float32)
+        assert self.lib.orc_matmul_f32(gtype, _ptr(b, _u8p), rows, columns, _ptr(x, _f32p), x.shape[0],
+                                       _ptr(y, _f32p), threads) == 0
+        return y
+
+    def matmul_f64(self, gtype, blocks, rows, columns, x):
+        b = _bytes(blocks)
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, columns)
+        y = np.empty((x.shape[0], rows), np.float64)
+        bound = np.empty_like(y)
+        assert self.lib.orc_matmul_f64(gtype, _ptr(b, _u8p), rows, columns, _ptr(x, _f32p), x.shape[0],
+                                       _ptr(y, _f64p), _ptr(bound, _f64p)) == 0
+        return y, bound
+
+    def fill(self, seed, count, amplitude=1.0):
+        out = np.empty(count, np.float32)
+        self.lib.orc_fill(seed, count, amplitude, _ptr(out, _f32p))
+        return out
+
+    def activate(self, activation, g):
+        return self.lib.orc_activate(activation, g)
+
+    def exp_nonpositive(self, x):
+        return self.lib.orc_exp_nonpositive(x)
+
+
+class Reference:
+    """The reference's own code (oracle/_ref/libref.so), built here only."""
+
+    def __init__(self, path=None):
+        path = path or os.path.join(ORACLE_DIR, "_ref", "libref.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        lib = ctypes.CDLL(path)
+        lib.ref_fp16_to_fp32.restype = ctypes.c_float
+        lib.ref_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        for f in (lib.ref_dequantize_q4_0, lib.ref_dequantize_q6_k):
+            f.argtypes = [_u8p, ctypes.c_uint64, _f32p]
+        lib.ref_repack_q6_k.argtypes = [_u8p, ctypes.c_uint64, _u8p, _u8p, _u8p, _u8p]
+        self.lib = lib
+
+    def fp16_to_fp32(self, h):
+        return self.lib.ref_fp16_to_fp32(h)
+
+    def dequantize(self, gtype, blocks):
+        b = _bytes(blocks)
+        per, nbytes = BLOCK[gtype]
+        n = b.size // nbytes
+        out = np.empty(n * per, np.float32)
+        f = self.lib.ref_dequantize_q4_0 if gtype == Q4_0 else self.lib.ref_dequantize_q6_k
+        f(_ptr(b, _u8p), n, _ptr(out, _f32p))
+        return out
+
+    def repack_q6_k(self, blocks):
+        b = _bytes(blocks)
+        n = b.size // 210
+        lo, hi = np.zeros(128 * n, np.uint8), np.zeros(64 * n, np.uint8)
+        sc, d = np.zeros(16 * n, np.uint8), np.zeros(2 * n, np.uint8)
+        self.lib.ref_repack_q6_k(_ptr(b, _u8p), n, _ptr(lo, _u8p), _ptr(hi, _u8p), _ptr(sc, _u8p), _ptr(d, _u8p))
+        return lo, hi, sc, d
+
+
+def reference_or_none():
+    try:
+        return Reference()
+    except (FileNotFoundError, OSError):
+        return None
