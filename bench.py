@@ -1,0 +1,290 @@
+"""Benchmark of the quantized GGUF matmul path on one MI355X.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1,c2,...]
+
+A step is one pass of the hot path over one batch of synthetic input:
+  c1  Q4_0 decode GEMV 3072x1024 (Qwen3-0.6B FFN up)
+  c2  Q6_K LM-head GEMV 262144x1152, repacked (Gemma-3-1B)   <- the headline
+  c3  Qwen3-0.6B decode sweep: 28 layers x 7 Q4_0 GEMVs + Q6_K head 151936x1024
+  c4  Q4_0 prefill GEMM M=512, N=8192, K=2048 (Llama-3.2-1B gate/up)
+  c5  Llama-3.2-1B prefill, M=2048, 16 layers x 7 Q4_0 GEMMs + Q6_K head on the last row
+Inputs are seeded synthetic data (BASELINE's distributions) resident in HBM
+before timing; a GEMV's weights rotate over copies totalling > 2x the 256 MB
+MALL so every step reads HBM. Each config's launches are captured once in a
+HIP graph and replayed; HIP events on the launch stream bracket the K timed
+steps. One JSON line on stdout; progress on stderr.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+FP32_PEAK_TFLOPS = 157.3   # MI355X FP32 (vector and matrix)
+F16_PEAK_TFLOPS = 2516.6   # MI355X FP16 dense matrix
+MALL_BYTES = 256 << 20
+METRIC = "GEMV HBM GB/s (% of 8 TB/s); prefill GEMM TFLOP/s (% peak); host-CPU baseline"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(gtype, rows, columns):
+    from charlotte_amd import synthetic
+
+    return synthetic.stored_bytes(gtype, rows, columns) + 4 * columns + 4 * rows
+
+
+class Setup:
+    def __init__(self):
+        from charlotte_amd import harness as hx
+        from charlotte_amd import matmul as mm
+
+        self.hx, self.mm = hx, mm
+        self.ctx = mm.Context(0)
+        self.stream = hx.Stream()
+        self.buffers = []
+        self.weights = []
+
+    def buffer(self, array=None, nbytes=None):
+        b = self.hx.Buffer.of(array) if array is not None else self.hx.Buffer(nbytes)
+        self.buffers.append(b)
+        return b
+
+    def weight_copies(self, gtype, rows, columns, stored, copies):
+        """`copies` device copies of one weight, laid out once and copied on the device."""
+        mm = self.mm
+        first = mm.Weight(self.ctx, gtype, rows, columns, stored)
+        self.weights.append(first)
+        out = [first]
+        nbytes = mm.layout_bytes(gtype, rows, columns)
+        for _ in range(copies - 1):
+            b = self.buffer(nbytes=nbytes)
+            self.hx.check(self.hx.lib.chx_d2d(b.ptr, first.device, nbytes), "d2d")
+            w = mm.Weight(self.ctx, gtype, rows, columns, device_piece=b.ptr, nbytes=nbytes)
+            self.weights.append(w)
+            out.append(w)
+        return out
+
+    def time_graph(self, body, steps, warmup, launches_a_step=1):
+        """Capture body() (one step's launches) `steps` times into a graph; replay it
+        once untimed (warmup), then timed; return ms per step."""
+        hx = self.hx
+        # warmup, eager
+        for _ in range(warmup):
+            body()
+        self.stream.sync()
+        graph = hx.Graph(self.stream, lambda: [body() for _ in range(steps)])
+        graph.launch()  # untimed replay: first-launch costs
+        self.stream.sync()
+        start, stop = hx.Event(), hx.Event()
+        start.record(self.stream)
+        graph.launch()
+        stop.record(self.stream)
+        stop.sync()
+        ms = start.elapsed_ms(stop) / steps
+        graph.destroy()
+        start.destroy()
+        stop.destroy()
+        return ms
+
+    def close(self):
+        for w in self.weights:
+            w.free()
+        for b in self.buffers:
+            b.free()
+        self.stream.destroy()
+        self.ctx.close()
+
+
+def run_gemv(S, name, gtype, rows, columns, steps, warmup, rng, copies=None):
+    from charlotte_amd import synthetic
+
+    mm = S.mm
+    wbytes = synthetic.stored_bytes(gtype, rows, columns)
+    copies = copies or max(2, -(-2 * MALL_BYTES // wbytes))
+    t0 = time.time()
+    stored = synthetic.weight(rng, gtype, rows, columns)
+    ws = S.weight_copies(gtype, rows, columns, stored, copies)
+    x = S.buffer(synthetic.activations(rng, 1, columns))
+    y = S.buffer(nbytes=4 * rows)
+    launches = [mm.MatmulLaunch([mm.Member(w)], x.ptr, [y.ptr]) for w in ws]
+    state = {"i": 0}
+
+    def body():
+        m = launches[state["i"] % len(launches)]
+        state["i"] += 1
+        mm.launch(S.ctx, m, 1, stream=S.stream.handle)
+
+    log(f"{name}: {rows}x{columns} {'Q4_0' if gtype == 2 else 'Q6_K'}, {copies} copies, setup {time.time() - t0:.1f}s")
+    ms = S.time_graph(body, steps, warmup)
+    nbytes = gemv_bytes(gtype, rows, columns)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"{name}: {ms * 1e3:.2f} us/launch, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
+    return {"ms_per_step": ms, "bytes": nbytes, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "copies": copies,
+            "stored": stored, "x": x, "weights": ws}
+
+
+def run_c3(S, steps, warmup, rng):
+    """Qwen3-0.6B decode step: 28 layers x (q, k, v, o, gate, up, down) + Q6_K head."""
+    from charlotte_amd import synthetic
+
+    mm = S.mm
+    layer = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 1024, 2048), ("gate", 3072, 1024),
+             ("up", 3072, 1024), ("down", 1024, 3072)]
+    t0 = time.time()
+    xs = {c: S.buffer(synthetic.activations(rng, 1, c)) for c in (1024, 2048, 3072)}
+    launches, total = [], 0
+    for _ in range(28):
+        for _n, rows, columns in layer:
+            stored = synthetic.q4_0(rng, rows, columns)
+            w = mm.Weight(S.ctx, 2, rows, columns, stored)
+            S.weights.append(w)
+            y = S.buffer(nbytes=4 * rows)
+            launches.append(mm.MatmulLaunch([mm.Member(w)], xs[columns].ptr, [y.ptr]))
+            total += gemv_bytes(2, rows, columns)
+    head_stored = synthetic.q6_k(rng, 151936, 1024)
+    head = mm.Weight(S.ctx, 14, 151936, 1024, head_stored)
+    S.weights.append(head)
+    yh = S.buffer(nbytes=4 * 151936)
+    launches.append(mm.MatmulLaunch([mm.Member(head)], xs[1024].ptr, [yh.ptr]))
+    total += gemv_bytes(14, 151936, 1024)
+    log(f"c3: {len(launches)} launches, {total / 1e6:.1f} MB, setup {time.time() - t0:.1f}s")
+
+    def body():
+        for m in launches:
+            mm.launch(S.ctx, m, 1, stream=S.stream.handle)
+
+    ms = S.time_graph(body, steps, warmup)
+    gbs = total / (ms * 1e-3) / 1e9
+    log(f"c3: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s aggregate, {1e3 / ms:.0f} tokens/s")
+    return {"ms_per_step": ms, "bytes": total, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "launches": len(launches),
+            "tokens_per_s": 1e3 / ms}
+
+
+def run_gemm(S, name, products, tokens, steps, warmup, rng, head=None):
+    """products: list of (rows, columns) Q4_0 weights run over `tokens` tokens."""
+    from charlotte_amd import synthetic
+
+    mm = S.mm
+    t0 = time.time()
+    widths = sorted({c for _, c in products})
+    xs = {c: S.buffer(synthetic.activations(rng, tokens, c)) for c in widths}
+    launches, flops = [], 0
+    for rows, columns in products:
+        w = mm.Weight(S.ctx, 2, rows, columns, synthetic.q4_0(rng, rows, columns))
+        S.weights.append(w)
+        y = S.buffer(nbytes=4 * rows * tokens)
+        launches.append((mm.MatmulLaunch([mm.Member(w)], xs[columns].ptr, [y.ptr]), tokens))
+        flops += 2 * tokens * rows * columns
+    head_bytes = 0
+    if head is not None:
+        rows, columns = head
+        w = mm.Weight(S.ctx, 14, rows, columns, synthetic.q6_k(rng, rows, columns))
+        S.weights.append(w)
+        y = S.buffer(nbytes=4 * rows)
+        launches.append((mm.MatmulLaunch([mm.Member(w)], xs[columns].ptr, [y.ptr], rows=mm.Rows.LastToken), tokens))
+        head_bytes = gemv_bytes(14, rows, columns)
+    log(f"{name}: {len(launches)} launches, {flops / 1e9:.1f} GFLOP, setup {time.time() - t0:.1f}s")
+
+    def body():
+        for m, t in launches:
+            mm.launch(S.ctx, m, t, stream=S.stream.handle)
+
+    ms = S.time_graph(body, steps, warmup)
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"{name}: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s ({100 * tflops / FP32_PEAK_TFLOPS:.1f}% of FP32 peak)")
+    return {"ms_per_step": ms, "flops": flops, "TFLOP/s": tflops, "frac_fp32": tflops / FP32_PEAK_TFLOPS,
+            "tokens_per_s": tokens / (ms * 1e-3), "launches": len(launches), "head_gemv_bytes": head_bytes}
+
+
+def cpu_baseline_c2(stored, x, rows, columns, seconds=10.0):
+    """The oracle's reference-order f32 GEMV (the CPU restatement of the
+    reference's order of addition, oracle/liborc.so) over all of C2 on the
+    host's cores, repeated for about `seconds`; the median run."""
+    from tests.support.oracle_lib import Oracle
+
+    oracle = Oracle()
+    threads = min(os.cpu_count() or 1, 16)
+    oracle.matmul_f32(14, stored, rows, columns, x, threads=threads)  # warm-up
+    times = []
+    t_end = time.time() + seconds
+    while (time.time() < t_end and len(times) < 200) or len(times) < 5:
+        t0 = time.time()
+        oracle.matmul_f32(14, stored, rows, columns, x, threads=threads)
+        times.append(time.time() - t0)
+    t = float(np.median(times))
+    nbytes = gemv_bytes(14, rows, columns)
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"all of C2 ({rows}x{columns} Q6_K), reference-order f32 fma, median of {len(times)} runs "
+                      f"of {t * 1e3:.1f} ms; oracle/liborc.so on {threads} threads"}
+
+
+def main():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--only", default="c1,c2,c3,c4,c5")
+    p.add_argument("--no-cpu", action="store_true")
+    args = p.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (this path is measured on one MI355X); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    only = set(args.only.split(","))
+    from charlotte_amd import harness as hx
+
+    log("device:", hx.device_name(0))
+    S = Setup()
+    out = {}
+    rng = np.random.default_rng(0xC4A7)
+    c2 = None
+    try:
+        if "c2" in only:
+            c2 = run_gemv(S, "c2", 14, 262144, 1152, max(args.steps, 20), args.warmup, np.random.default_rng(2))
+        if "c1" in only:
+            r = run_gemv(S, "c1", 2, 3072, 1024, max(args.steps, 100), args.warmup, np.random.default_rng(1))
+            out["c1"] = {k: v for k, v in r.items() if k not in ("stored", "x", "weights")}
+        if "c3" in only:
+            out["c3"] = run_c3(S, max(args.steps // 4, 3), args.warmup, rng)
+        if "c4" in only:
+            out["c4"] = run_gemm(S, "c4", [(8192, 2048)], 512, args.steps, args.warmup, rng)
+        if "c5" in only:
+            layer = [(2048, 2048), (512, 2048), (512, 2048), (2048, 2048), (8192, 2048), (8192, 2048), (2048, 8192)]
+            out["c5"] = run_gemm(S, "c5", layer * 16, 2048, max(args.steps // 4, 3), args.warmup, rng,
+                                 head=(128256, 2048))
+    finally:
+        S.close()
+
+    result = {"metric": METRIC, "unit": "GB/s", "higher_is_better": True, "n_gpus": 1, "scaling": "weak",
+              "vs_baseline": None, "dtype": "q6_k x f32 -> f32", "data": "synthetic (seeded; BASELINE distributions)"}
+    if c2 is not None:
+        cpu = None
+        if not args.no_cpu:
+            log("cpu baseline: oracle f32 on a sample of c2 ...")
+            cpu = cpu_baseline_c2(c2["stored"], c2["x"].read(np.float32), 262144, 1152)
+            log(f"cpu baseline: {cpu['value']:.1f} GB/s on {cpu['cores']} threads")
+        result.update({
+            "value": round(c2["GB/s"], 1), "steps": max(args.steps, 20), "warmup": args.warmup,
+            "ms_per_step": c2["ms_per_step"],
+            "config": {"workload": "c2: Q6_K LM-head GEMV y[1,262144] = x[1,1152] W^T (Gemma-3-1B), repacked Q6_K",
+                       "rows": 262144, "columns": 1152, "weight_copies": c2["copies"]},
+            "roofline": {"bound": "hbm", "achieved": round(c2["GB/s"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(c2["frac"], 4), "traffic": None},
+            "cpu_baseline": cpu,
+        })
+    result["configs"] = out
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,305 @@
+// The C ABI (include/charlotte_hip_matmul.h): contexts, weights in the device
+// layout, and each product's launches — the roles of the reference's
+// kernels::matmul_launches (src/core/kernels/matmul/matmul.cpp:252-325) and
+// Program::run (src/core/kernels/program.cpp:601-760), for HIP. Nothing here
+// throws across the ABI; every failure is a status and a message.
+#include "charlotte_hip_matmul.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "layout.hpp"
+#include "product.hpp"
+
+struct charlotte_hip_matmul_context {
+    int device = 0;
+    uint32_t compute_units = 0;
+    charlotte_hip_matmul_gemm_path gemm_path = CHARLOTTE_HIP_MATMUL_GEMM_AUTO;
+    std::string error;
+};
+
+struct charlotte_hip_matmul_weight {
+    charlotte_hip_matmul_context* ctx = nullptr;
+    uint32_t type = 0;
+    uint64_t rows = 0, columns = 0, blocks = 0, bytes = 0;
+    uint8_t* piece = nullptr;
+    bool owned = false;
+};
+
+namespace {
+
+using Status = charlotte_hip_matmul_status;
+
+Status fail(charlotte_hip_matmul_context* ctx, Status s, const std::string& message) {
+    if (ctx) ctx->error = message;
+    return s;
+}
+
+Status ok(charlotte_hip_matmul_context* ctx) {
+    if (ctx) ctx->error.clear();
+    return CHARLOTTE_HIP_MATMUL_OK;
+}
+
+Status hip_fail(charlotte_hip_matmul_context* ctx, hipError_t e, const char* what) {
+    return fail(ctx, e == hipErrorOutOfMemory ? CHARLOTTE_HIP_MATMUL_OUT_OF_MEMORY : CHARLOTTE_HIP_MATMUL_HIP_ERROR,
+                std::string(what) + ": " + hipGetErrorString(e));
+}
+
+bool known(uint32_t type) { return type == CHARLOTTE_HIP_MATMUL_Q4_0 || type == CHARLOTTE_HIP_MATMUL_Q6_K; }
+
+// The shape checks of a weight: rows of whole 32-weight groups
+// (matmul.h:668-671, format.h:138-160) in a tensor of whole blocks.
+Status check_shape(charlotte_hip_matmul_context* ctx, uint32_t type, uint64_t rows, uint64_t columns) {
+    if (!known(type)) return fail(ctx, CHARLOTTE_HIP_MATMUL_UNSUPPORTED_TYPE, "weight: GGUF type " + std::to_string(type));
+    if (rows == 0 || columns == 0) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "weight: no rows or columns");
+    if (columns % 32 != 0)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_SHAPE_NOT_GROUPS,
+                    "weight: " + std::to_string(columns) + " columns are not whole 32-weight groups");
+    if ((rows * columns) % chm::block_weights_host(type) != 0)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_SHAPE_NOT_GROUPS, "weight: not a whole number of blocks");
+    if (rows > 0xFFFFFFFFull || columns / 32 > 0xFFFFFFull)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "weight: too many rows or columns");
+    return CHARLOTTE_HIP_MATMUL_OK;
+}
+
+// kernels_matmul split geometry (matmul.cpp:26-37, 233-250; plan.h:113).
+constexpr uint32_t kTileOutputs = 64, kTileTokens = 32, kPrefillBlock = 512;
+
+}  // namespace
+
+extern "C" {
+
+charlotte_hip_matmul_status charlotte_hip_matmul_context_create(int device, charlotte_hip_matmul_context** out) {
+    if (!out) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) return CHARLOTTE_HIP_MATMUL_NO_DEVICE;
+    if (device < 0 || device >= count) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return CHARLOTTE_HIP_MATMUL_HIP_ERROR;
+    auto* ctx = new (std::nothrow) charlotte_hip_matmul_context;
+    if (!ctx) return CHARLOTTE_HIP_MATMUL_OUT_OF_MEMORY;
+    ctx->device = device;
+    ctx->compute_units = static_cast<uint32_t>(prop.multiProcessorCount);
+    *out = ctx;
+    return CHARLOTTE_HIP_MATMUL_OK;
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_context_destroy(charlotte_hip_matmul_context* ctx) {
+    delete ctx;
+    return CHARLOTTE_HIP_MATMUL_OK;
+}
+
+const char* charlotte_hip_matmul_last_error(const charlotte_hip_matmul_context* ctx) {
+    return ctx ? ctx->error.c_str() : "no context";
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_set_gemm_path(charlotte_hip_matmul_context* ctx,
+                                                               charlotte_hip_matmul_gemm_path path) {
+    if (!ctx) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    if (path != CHARLOTTE_HIP_MATMUL_GEMM_AUTO && path != CHARLOTTE_HIP_MATMUL_GEMM_CANONICAL &&
+        path != CHARLOTTE_HIP_MATMUL_GEMM_SPLIT_F16_MFMA)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gemm path: " + std::to_string(path));
+    ctx->gemm_path = path;
+    return ok(ctx);
+}
+
+uint64_t charlotte_hip_matmul_layout_bytes(uint32_t gguf_type, uint64_t rows, uint64_t columns) {
+    if (check_shape(nullptr, gguf_type, rows, columns) != CHARLOTTE_HIP_MATMUL_OK) return 0;
+    return chm::layout_bytes(gguf_type, rows * columns / chm::block_weights_host(gguf_type));
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_lay_out(uint32_t gguf_type, const void* stored_blocks,
+                                                         uint64_t blocks, void* device) {
+    if (!known(gguf_type)) return CHARLOTTE_HIP_MATMUL_UNSUPPORTED_TYPE;
+    if ((!stored_blocks || !device) && blocks != 0) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    if (blocks == 0) return CHARLOTTE_HIP_MATMUL_OK;
+    return chm::lay_out(gguf_type, static_cast<const uint8_t*>(stored_blocks), blocks, static_cast<uint8_t*>(device))
+               ? CHARLOTTE_HIP_MATMUL_OK
+               : CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_repack_q6_k(const void* stored_blocks, uint64_t blocks,
+                                                             void* const streams[4]) {
+    if (blocks == 0) return CHARLOTTE_HIP_MATMUL_OK;
+    if (!stored_blocks || !streams || !streams[0] || !streams[1] || !streams[2] || !streams[3])
+        return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    chm::repack_q6_k(static_cast<const uint8_t*>(stored_blocks), blocks, static_cast<uint8_t*>(streams[0]),
+                     static_cast<uint8_t*>(streams[1]), static_cast<uint8_t*>(streams[2]),
+                     static_cast<uint8_t*>(streams[3]));
+    return CHARLOTTE_HIP_MATMUL_OK;
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_weight_upload(charlotte_hip_matmul_context* ctx,
+                                                               uint32_t gguf_type, uint64_t rows,
+                                                               uint64_t columns, const void* stored_blocks,
+                                                               uint64_t bytes, charlotte_hip_matmul_weight** out) {
+    if (!ctx || !out || !stored_blocks) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "weight upload: null argument");
+    *out = nullptr;
+    if (Status s = check_shape(ctx, gguf_type, rows, columns); s != CHARLOTTE_HIP_MATMUL_OK) return s;
+    const uint64_t blocks = rows * columns / chm::block_weights_host(gguf_type);
+    if (bytes != blocks * chm::block_bytes_host(gguf_type))
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT,
+                    "weight upload: " + std::to_string(bytes) + " bytes for " + std::to_string(blocks) + " blocks");
+    const uint64_t device_bytes = chm::layout_bytes(gguf_type, blocks);
+    std::vector<uint8_t> host;
+    try {
+        host.resize(device_bytes);
+    } catch (const std::bad_alloc&) {
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_OUT_OF_MEMORY, "weight upload: host staging");
+    }
+    chm::lay_out(gguf_type, static_cast<const uint8_t*>(stored_blocks), blocks, host.data());
+    if (hipError_t e = hipSetDevice(ctx->device); e != hipSuccess) return hip_fail(ctx, e, "weight upload: hipSetDevice");
+    void* dev = nullptr;
+    if (hipError_t e = hipMalloc(&dev, device_bytes); e != hipSuccess) return hip_fail(ctx, e, "weight upload: hipMalloc");
+    if (hipError_t e = hipMemcpy(dev, host.data(), device_bytes, hipMemcpyHostToDevice); e != hipSuccess) {
+        (void)hipFree(dev);
+        return hip_fail(ctx, e, "weight upload: hipMemcpy");
+    }
+    auto* w = new (std::nothrow) charlotte_hip_matmul_weight;
+    if (!w) {
+        (void)hipFree(dev);
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_OUT_OF_MEMORY, "weight upload");
+    }
+    *w = {ctx, gguf_type, rows, columns, blocks, device_bytes, static_cast<uint8_t*>(dev), true};
+    *out = w;
+    return ok(ctx);
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_weight_wrap(charlotte_hip_matmul_context* ctx, uint32_t gguf_type,
+                                                             uint64_t rows, uint64_t columns, const void* device_piece,
+                                                             uint64_t bytes, charlotte_hip_matmul_weight** out) {
+    if (!ctx || !out || !device_piece) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "weight wrap: null argument");
+    *out = nullptr;
+    if (Status s = check_shape(ctx, gguf_type, rows, columns); s != CHARLOTTE_HIP_MATMUL_OK) return s;
+    const uint64_t blocks = rows * columns / chm::block_weights_host(gguf_type);
+    if (bytes < chm::layout_bytes(gguf_type, blocks))
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "weight wrap: piece shorter than its layout");
+    if (reinterpret_cast<uintptr_t>(device_piece) % 16 != 0)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "weight wrap: piece not 16-byte aligned");
+    auto* w = new (std::nothrow) charlotte_hip_matmul_weight;
+    if (!w) return fail(ctx, CHARLOTTE_HIP_MATMUL_OUT_OF_MEMORY, "weight wrap");
+    *w = {ctx, gguf_type, rows, columns, blocks, bytes,
+          const_cast<uint8_t*>(static_cast<const uint8_t*>(device_piece)), false};
+    *out = w;
+    return ok(ctx);
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_weight_free(charlotte_hip_matmul_weight* weight) {
+    if (!weight) return CHARLOTTE_HIP_MATMUL_OK;
+    Status s = CHARLOTTE_HIP_MATMUL_OK;
+    if (weight->owned && weight->piece) {
+        (void)hipSetDevice(weight->ctx->device);
+        if (hipFree(weight->piece) != hipSuccess) s = CHARLOTTE_HIP_MATMUL_HIP_ERROR;
+    }
+    delete weight;
+    return s;
+}
+
+const void* charlotte_hip_matmul_weight_device(const charlotte_hip_matmul_weight* weight) {
+    return weight ? weight->piece : nullptr;
+}
+
+uint32_t charlotte_hip_matmul_split_tokens(uint32_t epilogue, uint64_t rows, uint64_t columns,
+                                           charlotte_hip_matmul_split_gate gate) {
+    if (epilogue == CHARLOTTE_HIP_MATMUL_GATED_ACTIVATION || gate.denominator == 0 || rows == 0) return 1;
+    const uint64_t groups = columns / 32;
+    const uint64_t out_tiles = (rows + kTileOutputs - 1) / kTileOutputs;
+    const uint64_t by_ratio = groups * gate.numerator / (uint64_t{gate.denominator} * out_tiles);
+    const uint64_t by_cap = gate.max_workgroups / out_tiles;
+    const uint64_t token_tiles = std::min(by_ratio, by_cap);
+    if (token_tiles == 0) return 1;
+    return static_cast<uint32_t>(std::min<uint64_t>(token_tiles * kTileTokens, kPrefillBlock));
+}
+
+uint64_t charlotte_hip_matmul_range_sum_floats(uint32_t epilogue, uint64_t rows, uint64_t columns,
+                                               charlotte_hip_matmul_split_gate gate) {
+    const uint32_t split = charlotte_hip_matmul_split_tokens(epilogue, rows, columns, gate);
+    return split < 2 ? 0 : uint64_t{split} * rows * 32;
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_context* ctx,
+                                                        const charlotte_hip_matmul_desc* desc,
+                                                        charlotte_hip_matmul_split_gate gate, void* range_sums,
+                                                        uint64_t range_sums_bytes, uint32_t tokens, void* stream) {
+    (void)gate;
+    (void)range_sums;
+    (void)range_sums_bytes;
+    if (!ctx) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    if (!desc) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: no descriptor");
+    if (tokens == 0) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: a step of no tokens");
+    const charlotte_hip_matmul_desc& d = *desc;
+    if (d.member_count < 1 || d.member_count > 3)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member_count " + std::to_string(d.member_count));
+    if (d.epilogue > CHARLOTTE_HIP_MATMUL_GATED_BY_INPUT)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: epilogue " + std::to_string(d.epilogue));
+    if (d.rows > CHARLOTTE_HIP_MATMUL_LAST_TOKEN)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: rows " + std::to_string(d.rows));
+    if (d.epilogue == CHARLOTTE_HIP_MATMUL_GATED_ACTIVATION || d.epilogue == CHARLOTTE_HIP_MATMUL_GATED_BY_INPUT ||
+        d.clip || d.bias || d.activated)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_UNSUPPORTED, "launch: epilogue or option not built");
+    if (d.epilogue == CHARLOTTE_HIP_MATMUL_WRITE && d.member_count != 1)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: a Write takes one member");
+    if (!d.input) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: no input");
+    if (reinterpret_cast<uintptr_t>(d.input) % 16 != 0)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: input not 16-byte aligned");
+
+    chm::Product a{};
+    const charlotte_hip_matmul_weight* head = d.members[0].weight;
+    if (!head) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member 0 has no weight");
+    uint64_t rows = 0;
+    for (uint32_t i = 0; i < d.member_count; ++i) {
+        const charlotte_hip_matmul_member& m = d.members[i];
+        if (!m.weight) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member " + std::to_string(i) + " has no weight");
+        if (m.weight->type != head->type || m.weight->columns != head->columns)
+            return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: members differ in format or width");
+        if (m.rows == 0 || m.row_offset + m.rows > m.weight->rows)
+            return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member " + std::to_string(i) + " rows past its weight");
+        float* out = d.epilogue == CHARLOTTE_HIP_MATMUL_QKV ? d.outputs[i] : d.outputs[0];
+        if (!out) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member " + std::to_string(i) + " has no output");
+        const uint64_t width = d.out_width ? d.out_width : 0;
+        a.m[i] = chm::Member{m.weight->piece,
+                             m.weight->blocks,
+                             static_cast<uint32_t>(m.row_offset),
+                             static_cast<uint32_t>(m.rows),
+                             static_cast<uint32_t>(rows),
+                             static_cast<uint32_t>(m.output_row),
+                             static_cast<uint32_t>(width),
+                             0,
+                             out};
+        rows += m.rows;
+    }
+    if (rows > 0x7FFFFFFFull) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: too many rows");
+    for (uint32_t i = 0; i < d.member_count; ++i) {
+        if (a.m[i].out_width == 0) a.m[i].out_width = static_cast<uint32_t>(rows);
+        if (d.epilogue == CHARLOTTE_HIP_MATMUL_WRITE && a.m[i].out_row + a.m[i].rows > a.m[i].out_width)
+            return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: output rows past out_width");
+    }
+    a.x = d.input;
+    a.members = d.member_count;
+    a.rows = static_cast<uint32_t>(rows);
+    a.groups = static_cast<uint32_t>(head->columns / 32);
+    a.epilogue = d.epilogue;
+    a.activation = d.activation;
+    a.last_token = d.rows == CHARLOTTE_HIP_MATMUL_LAST_TOKEN;
+    a.tokens = tokens;
+
+    if (hipError_t e = hipSetDevice(ctx->device); e != hipSuccess) return hip_fail(ctx, e, "launch: hipSetDevice");
+    auto* s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    if (tokens == 1 || a.last_token) {
+        e = chm::launch_gemv(a, head->type, ctx->compute_units, s);
+    } else {
+        e = chm::launch_gemm_canonical(a, head->type, ctx->compute_units, s);
+    }
+    if (e != hipSuccess) return hip_fail(ctx, e, "launch");
+    return ok(ctx);
+}
+
+}  // extern "C"

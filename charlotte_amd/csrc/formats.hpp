@@ -1,0 +1,134 @@
+// The two weight formats as the kernels read them from a piece's streams,
+// and the one multiply-add order every canonical kernel shares.
+//
+// A piece of n blocks holds each stream whole, one after another
+// (src/core/formats/device_layout.h:111-136):
+//   Q4_0  codes   [0, 16n)      16 bytes a block: byte j = weight j (low nibble),
+//                               weight j + 16 (high nibble)
+//         scales  [16n, 18n)    fp16 d a block
+//   Q6_K  lo      [0, 128n)     16 bytes a 32-weight group: byte j = weight j's low
+//                               nibble (low half), weight j + 16's (high half)
+//         hi      [128n, 192n)  8 bytes a group: byte m = the high bit pairs of
+//                               weights m, m + 8, m + 16, m + 24 at bits 0, 2, 4, 6
+//         scales  [192n, 208n)  int8, two a group: weights 0..15, then 16..31
+//         d       [208n, 210n)  fp16 a super-block of 8 groups
+// Groups are counted flat over the piece — group gi is row gi / G's group
+// gi % G — so a Q6_K row need not be whole super-blocks (q6_k.wgsl:13-42).
+//
+// Every weight decodes exactly: (q - 8) d and (d sc)(q - 32) are products of
+// at most 24 significant bits, so fma(q, d, -8d) and fma(q, d sc, -32 d sc)
+// return them exactly, one instruction a weight after the code's conversion.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace chm {
+
+enum Format : uint32_t { kQ4_0 = 2, kQ6_K = 14 };
+
+// Bytes a stored block, and weights a block.
+constexpr uint32_t block_bytes(uint32_t f) { return f == kQ4_0 ? 18u : f == kQ6_K ? 210u : 0u; }
+constexpr uint32_t block_weights(uint32_t f) { return f == kQ4_0 ? 32u : f == kQ6_K ? 256u : 0u; }
+
+// binary16 bits -> binary32, exact for every finite input, subnormals
+// included (the f16 denormal mode is left at its IEEE default).
+__device__ __forceinline__ float half_to_float(uint32_t bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+}
+
+// The 16 code bytes and scale of Q4_0 group gi, and the group's data of Q6_K.
+struct Q4_0Group {
+    uint32_t w[4];
+    float d, minus_8d;
+};
+
+struct Q6_KGroup {
+    uint32_t lo[4];
+    uint32_t hi[2];
+    float first, minus_32_first, second, minus_32_second;
+};
+
+__device__ __forceinline__ Q4_0Group load_q4_0(const uint8_t* piece, uint64_t n, uint64_t gi) {
+    Q4_0Group g;
+    const uint4 c = *reinterpret_cast<const uint4*>(piece + 16 * gi);
+    g.w[0] = c.x;
+    g.w[1] = c.y;
+    g.w[2] = c.z;
+    g.w[3] = c.w;
+    g.d = half_to_float(*reinterpret_cast<const uint16_t*>(piece + 16 * n + 2 * gi));
+    g.minus_8d = -8.0f * g.d;
+    return g;
+}
+
+__device__ __forceinline__ Q6_KGroup load_q6_k(const uint8_t* piece, uint64_t n, uint64_t gi) {
+    Q6_KGroup g;
+    const uint4 lo = *reinterpret_cast<const uint4*>(piece + 16 * gi);
+    const uint2 hi = *reinterpret_cast<const uint2*>(piece + 128 * n + 8 * gi);
+    const uint32_t sc = *reinterpret_cast<const uint16_t*>(piece + 192 * n + 2 * gi);
+    const float d = half_to_float(*reinterpret_cast<const uint16_t*>(piece + 208 * n + 2 * (gi / 8)));
+    g.lo[0] = lo.x;
+    g.lo[1] = lo.y;
+    g.lo[2] = lo.z;
+    g.lo[3] = lo.w;
+    g.hi[0] = hi.x;
+    g.hi[1] = hi.y;
+    g.first = d * static_cast<float>(static_cast<int8_t>(sc & 0xFFu));
+    g.second = d * static_cast<float>(static_cast<int8_t>(sc >> 8));
+    g.minus_32_first = -32.0f * g.first;
+    g.minus_32_second = -32.0f * g.second;
+    return g;
+}
+
+// Weight l (0..31) of a group, exact.
+__device__ __forceinline__ float weight(const Q4_0Group& g, int l) {
+    const uint32_t q = (g.w[(l & 15) >> 2] >> (8 * (l & 3) + 4 * (l >> 4))) & 0xFu;
+    return __builtin_fmaf(static_cast<float>(q), g.d, g.minus_8d);
+}
+
+__device__ __forceinline__ float weight(const Q6_KGroup& g, int l) {
+    const uint32_t low = (g.lo[(l & 15) >> 2] >> (8 * (l & 3) + 4 * (l >> 4))) & 0xFu;
+    const uint32_t pair = (g.hi[(l & 7) >> 2] >> (8 * (l & 3) + 2 * (l >> 3))) & 3u;
+    const float q = static_cast<float>(low | (pair << 4));
+    return l < 16 ? __builtin_fmaf(q, g.first, g.minus_32_first) : __builtin_fmaf(q, g.second, g.minus_32_second);
+}
+
+// s continued over the group's 32 weights in k order, each an fma:
+// s = fma(w_l, x_l, s) for l = 0..31 (matmul.wgsl:121-126, 224-230).
+template <typename G>
+__device__ __forceinline__ float chain(const G& g, const float* x, float s) {
+#pragma unroll
+    for (int l = 0; l < 32; ++l) s = __builtin_fmaf(weight(g, l), x[l], s);
+    return s;
+}
+
+template <uint32_t F>
+__device__ __forceinline__ float chain_group(const uint8_t* piece, uint64_t n, uint64_t gi, const float* x, float s) {
+    if constexpr (F == kQ4_0) {
+        return chain(load_q4_0(piece, n, gi), x, s);
+    } else {
+        return chain(load_q6_k(piece, n, gi), x, s);
+    }
+}
+
+// The 32 weights of group gi, exact (the unpack of format.h:36-77).
+template <uint32_t F>
+__device__ __forceinline__ void unpack(const uint8_t* piece, uint64_t n, uint64_t gi, float* out) {
+    if constexpr (F == kQ4_0) {
+        const Q4_0Group g = load_q4_0(piece, n, gi);
+#pragma unroll
+        for (int l = 0; l < 32; ++l) out[l] = weight(g, l);
+    } else {
+        const Q6_KGroup g = load_q6_k(piece, n, gi);
+#pragma unroll
+        for (int l = 0; l < 32; ++l) out[l] = weight(g, l);
+    }
+}
+
+// Range r of a row's G groups: groups [range_lo(r, G), range_lo(r + 1, G))
+// (matmul.wgsl:134-137).
+__host__ __device__ __forceinline__ uint32_t range_lo(uint32_t r, uint32_t groups) {
+    return static_cast<uint32_t>((static_cast<uint64_t>(r) * groups) / 32u);
+}
+
+}  // namespace chm

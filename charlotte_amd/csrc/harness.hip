@@ -1,0 +1,122 @@
+// Test and benchmark harness (libcharlotte_hip_harness.so) — not part of
+// the product's ABI. Device memory, copies, streams, events and graphs for
+// Python callers that do not load a framework, plus two kernels:
+//   chx_unpack — the formats' unpack (formats.hpp, the code the product's
+//     kernels inline) writing each group's 32 weights out, so a test can hold
+//     it to the CPU dequant bit for bit (tests/gpu/support/unpack.h:30-109's
+//     role);
+//   chx_copy — a plain copy of known size, the yardstick rocprofv3's
+//     FETCH_SIZE / WRITE_SIZE counters are scaled by.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <cstdio>
+
+#include "formats.hpp"
+
+namespace {
+
+template <uint32_t F>
+__global__ void unpack_kernel(const uint8_t* piece, uint64_t blocks, uint64_t groups, float* out) {
+    const uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (g >= groups) return;
+    float w[32];
+    chm::unpack<F>(piece, blocks, g, w);
+    float4* dst = reinterpret_cast<float4*>(out + 32 * g);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) dst[v] = make_float4(w[4 * v], w[4 * v + 1], w[4 * v + 2], w[4 * v + 3]);
+}
+
+__global__ void copy_kernel(const float4* __restrict__ src, float4* __restrict__ dst, uint64_t n) {
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x)
+        dst[i] = src[i];
+}
+
+}  // namespace
+
+extern "C" {
+
+int chx_device_count() {
+    int n = 0;
+    return hipGetDeviceCount(&n) == hipSuccess ? n : 0;
+}
+
+int chx_set_device(int d) { return hipSetDevice(d); }
+
+int chx_device_name(int d, char* out, int len) {
+    hipDeviceProp_t p;
+    const hipError_t e = hipGetDeviceProperties(&p, d);
+    if (e != hipSuccess) return e;
+    snprintf(out, len, "%s|%s|cus=%d|clock_khz=%d|mem=%zu", p.name, p.gcnArchName, p.multiProcessorCount,
+             p.clockRate, static_cast<size_t>(p.totalGlobalMem));
+    return 0;
+}
+
+const char* chx_error_string(int e) { return hipGetErrorString(static_cast<hipError_t>(e)); }
+
+int chx_malloc(void** p, uint64_t bytes) { return hipMalloc(p, bytes); }
+int chx_free(void* p) { return hipFree(p); }
+int chx_h2d(void* dst, const void* src, uint64_t bytes) { return hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice); }
+int chx_d2h(void* dst, const void* src, uint64_t bytes) { return hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost); }
+int chx_d2d(void* dst, const void* src, uint64_t bytes) { return hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice); }
+int chx_memset(void* p, int value, uint64_t bytes) { return hipMemset(p, value, bytes); }
+int chx_sync() { return hipDeviceSynchronize(); }
+int chx_last_error() { return hipGetLastError(); }
+
+int chx_stream_create(void** s) { return hipStreamCreate(reinterpret_cast<hipStream_t*>(s)); }
+int chx_stream_destroy(void* s) { return hipStreamDestroy(static_cast<hipStream_t>(s)); }
+int chx_stream_sync(void* s) { return hipStreamSynchronize(static_cast<hipStream_t>(s)); }
+
+int chx_event_create(void** e) { return hipEventCreate(reinterpret_cast<hipEvent_t*>(e)); }
+int chx_event_destroy(void* e) { return hipEventDestroy(static_cast<hipEvent_t>(e)); }
+int chx_event_record(void* e, void* s) { return hipEventRecord(static_cast<hipEvent_t>(e), static_cast<hipStream_t>(s)); }
+int chx_event_sync(void* e) { return hipEventSynchronize(static_cast<hipEvent_t>(e)); }
+int chx_event_elapsed_ms(float* ms, void* start, void* stop) {
+    return hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop));
+}
+
+// Graphs: capture a stream's launches, then replay them.
+int chx_capture_begin(void* s) {
+    return hipStreamBeginCapture(static_cast<hipStream_t>(s), hipStreamCaptureModeThreadLocal);
+}
+int chx_capture_end(void* s, void** exec) {
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(static_cast<hipStream_t>(s), &g);
+    if (e != hipSuccess) return e;
+    e = hipGraphInstantiate(reinterpret_cast<hipGraphExec_t*>(exec), g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    return e;
+}
+int chx_graph_launch(void* exec, void* s) {
+    return hipGraphLaunch(static_cast<hipGraphExec_t>(exec), static_cast<hipStream_t>(s));
+}
+int chx_graph_destroy(void* exec) { return hipGraphExecDestroy(static_cast<hipGraphExec_t>(exec)); }
+
+int chx_unpack(uint32_t type, const void* piece, uint64_t blocks_in_piece, uint64_t groups, float* out, void* s) {
+    if (reinterpret_cast<uintptr_t>(piece) % 16 != 0) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<uint32_t>((groups + 63) / 64));
+    const auto* p = static_cast<const uint8_t*>(piece);
+    if (type == chm::kQ4_0) {
+        hipLaunchKernelGGL((unpack_kernel<chm::kQ4_0>), grid, dim3(64), 0, static_cast<hipStream_t>(s), p,
+                           blocks_in_piece, groups, out);
+    } else if (type == chm::kQ6_K) {
+        hipLaunchKernelGGL((unpack_kernel<chm::kQ6_K>), grid, dim3(64), 0, static_cast<hipStream_t>(s), p,
+                           blocks_in_piece, groups, out);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+int chx_copy(const void* src, void* dst, uint64_t bytes, void* s) {
+    if (bytes % 16 != 0) return hipErrorInvalidValue;
+    const uint64_t n = bytes / 16;
+    const uint32_t blocks = static_cast<uint32_t>(std::min<uint64_t>((n + 255) / 256, 65536));
+    hipLaunchKernelGGL(copy_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(s),
+                       static_cast<const float4*>(src), static_cast<float4*>(dst), n);
+    return hipGetLastError();
+}
+
+}  // extern "C"

@@ -1,0 +1,23 @@
+// Host-side device layout (layout.cpp) and the kernels' launchers, as the
+// C ABI (capi.cpp) calls them.
+#pragma once
+
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+namespace chm {
+
+struct Product;
+
+constexpr uint32_t block_bytes_host(uint32_t f) { return f == 2 ? 18u : f == 14 ? 210u : 0u; }
+constexpr uint32_t block_weights_host(uint32_t f) { return f == 2 ? 32u : f == 14 ? 256u : 0u; }
+
+uint64_t layout_bytes(uint32_t format, uint64_t blocks);
+bool lay_out(uint32_t format, const uint8_t* stored, uint64_t blocks, uint8_t* device);
+void repack_q6_k(const uint8_t* stored, uint64_t blocks, uint8_t* lo, uint8_t* hi, uint8_t* scales, uint8_t* d);
+
+hipError_t launch_gemv(const Product& a, uint32_t format, uint32_t compute_units, hipStream_t stream);
+hipError_t launch_gemm_canonical(const Product& a, uint32_t format, uint32_t compute_units, hipStream_t stream);
+
+}  // namespace chm

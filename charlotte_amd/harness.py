@@ -1,0 +1,184 @@
+"""Device memory, streams, events and graphs for tests and the benchmark,
+over libcharlotte_hip_harness.so (charlotte_amd/csrc/harness.hip) — plain
+HIP, so GPU processes need no framework. Not part of the product's ABI.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(HERE, "libcharlotte_hip_harness.so")
+
+_c = ctypes
+_SIGS = {
+    "chx_device_count": (_c.c_int, []),
+    "chx_set_device": (_c.c_int, [_c.c_int]),
+    "chx_device_name": (_c.c_int, [_c.c_int, _c.c_char_p, _c.c_int]),
+    "chx_error_string": (_c.c_char_p, [_c.c_int]),
+    "chx_malloc": (_c.c_int, [_c.POINTER(_c.c_void_p), _c.c_uint64]),
+    "chx_free": (_c.c_int, [_c.c_void_p]),
+    "chx_h2d": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_uint64]),
+    "chx_d2h": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_uint64]),
+    "chx_d2d": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_uint64]),
+    "chx_memset": (_c.c_int, [_c.c_void_p, _c.c_int, _c.c_uint64]),
+    "chx_sync": (_c.c_int, []),
+    "chx_last_error": (_c.c_int, []),
+    "chx_stream_create": (_c.c_int, [_c.POINTER(_c.c_void_p)]),
+    "chx_stream_destroy": (_c.c_int, [_c.c_void_p]),
+    "chx_stream_sync": (_c.c_int, [_c.c_void_p]),
+    "chx_event_create": (_c.c_int, [_c.POINTER(_c.c_void_p)]),
+    "chx_event_destroy": (_c.c_int, [_c.c_void_p]),
+    "chx_event_record": (_c.c_int, [_c.c_void_p, _c.c_void_p]),
+    "chx_event_sync": (_c.c_int, [_c.c_void_p]),
+    "chx_event_elapsed_ms": (_c.c_int, [_c.POINTER(_c.c_float), _c.c_void_p, _c.c_void_p]),
+    "chx_capture_begin": (_c.c_int, [_c.c_void_p]),
+    "chx_capture_end": (_c.c_int, [_c.c_void_p, _c.POINTER(_c.c_void_p)]),
+    "chx_graph_launch": (_c.c_int, [_c.c_void_p, _c.c_void_p]),
+    "chx_graph_destroy": (_c.c_int, [_c.c_void_p]),
+    "chx_unpack": (_c.c_int, [_c.c_uint32, _c.c_void_p, _c.c_uint64, _c.c_uint64, _c.c_void_p, _c.c_void_p]),
+    "chx_copy": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
+}
+
+
+def _load():
+    if not os.path.exists(LIBRARY):
+        raise ImportError(f"{LIBRARY} is not built: run __graft_entry__.build()")
+    lib = ctypes.CDLL(LIBRARY)
+    for name, (restype, argtypes) in _SIGS.items():
+        f = getattr(lib, name)
+        f.restype, f.argtypes = restype, argtypes
+    return lib
+
+
+lib = _load()
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def check(e, what=""):
+    if e != 0:
+        raise HipError(f"{what}: {lib.chx_error_string(e).decode()} ({e})")
+
+
+def device_count():
+    return lib.chx_device_count()
+
+
+def device_name(d=0):
+    buf = ctypes.create_string_buffer(512)
+    check(lib.chx_device_name(d, buf, 512), "device name")
+    return buf.value.decode()
+
+
+def sync():
+    check(lib.chx_sync(), "device synchronize")
+
+
+class Buffer:
+    """Device memory of `nbytes` bytes."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        check(lib.chx_malloc(ctypes.byref(p), max(self.nbytes, 16)), f"hipMalloc({self.nbytes})")
+        self.ptr = p.value
+
+    @classmethod
+    def of(cls, array):
+        a = np.ascontiguousarray(array)
+        b = cls(a.nbytes)
+        b.write(a)
+        return b
+
+    def write(self, array, offset=0):
+        a = np.ascontiguousarray(array)
+        check(lib.chx_h2d(self.ptr + offset, a.ctypes.data, a.nbytes), "h2d")
+
+    def read(self, dtype=np.float32, count=None, offset=0):
+        dtype = np.dtype(dtype)
+        count = (self.nbytes - offset) // dtype.itemsize if count is None else count
+        out = np.empty(count, dtype)
+        check(lib.chx_d2h(out.ctypes.data, self.ptr + offset, out.nbytes), "d2h")
+        return out
+
+    def fill(self, byte):
+        check(lib.chx_memset(self.ptr, byte, self.nbytes), "memset")
+
+    def free(self):
+        if self.ptr:
+            check(lib.chx_free(self.ptr), "hipFree")
+            self.ptr = None
+
+
+class Stream:
+    def __init__(self):
+        s = ctypes.c_void_p()
+        check(lib.chx_stream_create(ctypes.byref(s)), "stream create")
+        self.handle = s.value
+
+    def sync(self):
+        check(lib.chx_stream_sync(self.handle), "stream sync")
+
+    def destroy(self):
+        if self.handle:
+            lib.chx_stream_destroy(self.handle)
+            self.handle = None
+
+
+class Event:
+    def __init__(self):
+        e = ctypes.c_void_p()
+        check(lib.chx_event_create(ctypes.byref(e)), "event create")
+        self.handle = e.value
+
+    def record(self, stream=None):
+        check(lib.chx_event_record(self.handle, stream.handle if isinstance(stream, Stream) else stream), "event record")
+
+    def sync(self):
+        check(lib.chx_event_sync(self.handle), "event sync")
+
+    def elapsed_ms(self, later):
+        ms = ctypes.c_float()
+        check(lib.chx_event_elapsed_ms(ctypes.byref(ms), self.handle, later.handle), "event elapsed")
+        return ms.value
+
+    def destroy(self):
+        if self.handle:
+            lib.chx_event_destroy(self.handle)
+            self.handle = None
+
+
+class Graph:
+    """The launches a callable makes on `stream`, captured once, replayable."""
+
+    def __init__(self, stream: Stream, body):
+        check(lib.chx_capture_begin(stream.handle), "capture begin")
+        try:
+            body()
+        finally:
+            exe = ctypes.c_void_p()
+            e = lib.chx_capture_end(stream.handle, ctypes.byref(exe))
+        check(e, "capture end")
+        self.exec = exe.value
+        self.stream = stream
+
+    def launch(self):
+        check(lib.chx_graph_launch(self.exec, self.stream.handle), "graph launch")
+
+    def destroy(self):
+        if self.exec:
+            lib.chx_graph_destroy(self.exec)
+            self.exec = None
+
+
+def unpack(gguf_type, piece_ptr, blocks_in_piece, groups, out_ptr, stream=None):
+    check(lib.chx_unpack(int(gguf_type), piece_ptr, blocks_in_piece, groups, out_ptr,
+                         stream.handle if isinstance(stream, Stream) else stream), "unpack")
+
+
+def copy(src_ptr, dst_ptr, nbytes, stream=None):
+    check(lib.chx_copy(src_ptr, dst_ptr, nbytes, stream.handle if isinstance(stream, Stream) else stream), "copy")

@@ -1,0 +1,306 @@
+"""The matrix product's operator interface, over the C ABI
+(include/charlotte_hip_matmul.h, libcharlotte_hip_matmul.so).
+
+It mirrors the reference's operator surface for this path
+(src/core/kernels/matmul/matmul.h:594-673): ``Epilogue``, ``MatmulLaunch``,
+``SplitGate``, ``split_tokens`` and ``range_sum_floats``. A launch takes
+device pointers (ints) for its input and outputs, as the reference's
+BufferRanges name device buffers, and runs on a HIP stream. Errors raise
+``MatmulError`` carrying the status and the library's message; the library
+itself never throws across its ABI.
+
+The native library must be built (``__graft_entry__.build()``); importing
+this module without it raises, so nothing can silently run elsewhere.
+"""
+
+import ctypes
+import enum
+import os
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(HERE, "libcharlotte_hip_matmul.so")
+
+
+class Status(enum.IntEnum):
+    OK = 0
+    INVALID_ARGUMENT = 1
+    UNSUPPORTED_TYPE = 2
+    SHAPE_NOT_GROUPS = 3
+    OUT_OF_MEMORY = 4
+    HIP_ERROR = 5
+    NO_DEVICE = 6
+    UNSUPPORTED = 7
+
+
+class TensorType(enum.IntEnum):
+    Q4_0 = 2
+    Q6_K = 14
+
+
+class Epilogue(enum.IntEnum):
+    Write = 0
+    QKV = 1
+    GatedActivation = 2
+    GatedByInput = 3
+
+
+class Activation(enum.IntEnum):
+    SiLU = 0
+    GeluTanh = 1
+    Sigmoid = 2
+
+
+class Rows(enum.IntEnum):
+    EveryToken = 0
+    LastToken = 1
+
+
+class GemmPath(enum.IntEnum):
+    AUTO = 0
+    CANONICAL = 1
+    SPLIT_F16_MFMA = 2
+
+
+class MatmulError(RuntimeError):
+    def __init__(self, status, message=""):
+        self.status = Status(status)
+        super().__init__(f"{self.status.name}: {message}")
+
+
+@dataclass(frozen=True)
+class SplitGate:
+    """kernels::SplitGate (matmul.h:634-646)."""
+
+    numerator: int
+    denominator: int
+    max_workgroups: int
+
+
+# The reference's test gates (tests/kernels_matmul_test.cpp:36-39) and its
+# measured value (matmul.h:646).
+kNever = SplitGate(0, 1, 0)
+kAlways = SplitGate(1024, 1, 1024)
+kSplitGate = SplitGate(2, 1, 64)
+
+
+class _Gate(ctypes.Structure):
+    _fields_ = [("numerator", ctypes.c_uint32), ("denominator", ctypes.c_uint32), ("max_workgroups", ctypes.c_uint32)]
+
+
+class _Member(ctypes.Structure):
+    _fields_ = [
+        ("weight", ctypes.c_void_p),
+        ("row_offset", ctypes.c_uint64),
+        ("rows", ctypes.c_uint64),
+        ("output_row", ctypes.c_uint64),
+    ]
+
+
+class _Desc(ctypes.Structure):
+    _fields_ = [
+        ("members", _Member * 3),
+        ("member_count", ctypes.c_uint32),
+        ("epilogue", ctypes.c_uint32),
+        ("activation", ctypes.c_uint32),
+        ("rows", ctypes.c_uint32),
+        ("input", ctypes.c_void_p),
+        ("outputs", ctypes.c_void_p * 3),
+        ("out_width", ctypes.c_uint64),
+        ("gate_input", ctypes.c_void_p),
+        ("gate_input_stride", ctypes.c_uint32),
+        ("gate_input_column", ctypes.c_uint32),
+        ("clip", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("activated", ctypes.c_uint32),
+    ]
+
+
+# Every symbol the header declares, with its ctypes signature.
+_c = ctypes
+SIGNATURES = {
+    "charlotte_hip_matmul_context_create": (_c.c_int, [_c.c_int, _c.POINTER(_c.c_void_p)]),
+    "charlotte_hip_matmul_context_destroy": (_c.c_int, [_c.c_void_p]),
+    "charlotte_hip_matmul_last_error": (_c.c_char_p, [_c.c_void_p]),
+    "charlotte_hip_matmul_set_gemm_path": (_c.c_int, [_c.c_void_p, _c.c_int]),
+    "charlotte_hip_matmul_layout_bytes": (_c.c_uint64, [_c.c_uint32, _c.c_uint64, _c.c_uint64]),
+    "charlotte_hip_matmul_lay_out": (_c.c_int, [_c.c_uint32, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
+    "charlotte_hip_matmul_repack_q6_k": (_c.c_int, [_c.c_void_p, _c.c_uint64, _c.POINTER(_c.c_void_p)]),
+    "charlotte_hip_matmul_weight_upload": (
+        _c.c_int,
+        [_c.c_void_p, _c.c_uint32, _c.c_uint64, _c.c_uint64, _c.c_void_p, _c.c_uint64, _c.POINTER(_c.c_void_p)],
+    ),
+    "charlotte_hip_matmul_weight_wrap": (
+        _c.c_int,
+        [_c.c_void_p, _c.c_uint32, _c.c_uint64, _c.c_uint64, _c.c_void_p, _c.c_uint64, _c.POINTER(_c.c_void_p)],
+    ),
+    "charlotte_hip_matmul_weight_free": (_c.c_int, [_c.c_void_p]),
+    "charlotte_hip_matmul_weight_device": (_c.c_void_p, [_c.c_void_p]),
+    "charlotte_hip_matmul_launch": (
+        _c.c_int,
+        [_c.c_void_p, _c.POINTER(_Desc), _Gate, _c.c_void_p, _c.c_uint64, _c.c_uint32, _c.c_void_p],
+    ),
+    "charlotte_hip_matmul_split_tokens": (_c.c_uint32, [_c.c_uint32, _c.c_uint64, _c.c_uint64, _Gate]),
+    "charlotte_hip_matmul_range_sum_floats": (_c.c_uint64, [_c.c_uint32, _c.c_uint64, _c.c_uint64, _Gate]),
+}
+
+
+def _load():
+    if not os.path.exists(LIBRARY):
+        raise ImportError(f"{LIBRARY} is not built: run __graft_entry__.build() (make -C charlotte_amd/csrc)")
+    lib = ctypes.CDLL(LIBRARY)
+    for name, (restype, argtypes) in SIGNATURES.items():
+        f = getattr(lib, name)
+        f.restype = restype
+        f.argtypes = argtypes
+    return lib
+
+
+lib = _load()
+
+
+def _gate(g: SplitGate):
+    return _Gate(g.numerator, g.denominator, g.max_workgroups)
+
+
+def split_tokens(epilogue, rows, columns, gate: SplitGate):
+    return lib.charlotte_hip_matmul_split_tokens(int(epilogue), rows, columns, _gate(gate))
+
+
+def range_sum_floats(epilogue, rows, columns, gate: SplitGate):
+    return lib.charlotte_hip_matmul_range_sum_floats(int(epilogue), rows, columns, _gate(gate))
+
+
+def layout_bytes(gguf_type, rows, columns):
+    return lib.charlotte_hip_matmul_layout_bytes(int(gguf_type), rows, columns)
+
+
+def lay_out(gguf_type, stored: bytes, blocks: int) -> bytes:
+    """File-order blocks -> the device layout, on the host."""
+    per = {TensorType.Q4_0: 32, TensorType.Q6_K: 256}[TensorType(gguf_type)]
+    out = ctypes.create_string_buffer(layout_bytes(gguf_type, 1, per * blocks) if blocks else 0)
+    src = ctypes.create_string_buffer(bytes(stored), len(stored))
+    s = lib.charlotte_hip_matmul_lay_out(int(gguf_type), src, blocks, out)
+    if s != 0:
+        raise MatmulError(s, "lay_out")
+    return out.raw
+
+
+def repack_q6_k(stored: bytes, blocks: int):
+    bufs = [ctypes.create_string_buffer(w * blocks) for w in (128, 64, 16, 2)]
+    arr = (ctypes.c_void_p * 4)(*[ctypes.cast(b, ctypes.c_void_p) for b in bufs])
+    src = ctypes.create_string_buffer(bytes(stored), len(stored))
+    s = lib.charlotte_hip_matmul_repack_q6_k(src, blocks, arr)
+    if s != 0:
+        raise MatmulError(s, "repack_q6_k")
+    return [b.raw for b in bufs]
+
+
+class Context:
+    """One device (charlotte_hip_matmul_context)."""
+
+    def __init__(self, device=0):
+        h = ctypes.c_void_p()
+        s = lib.charlotte_hip_matmul_context_create(device, ctypes.byref(h))
+        if s != 0:
+            raise MatmulError(s, f"context on device {device}")
+        self.handle = h
+
+    def error(self):
+        return (lib.charlotte_hip_matmul_last_error(self.handle) or b"").decode()
+
+    def check(self, status):
+        if status != 0:
+            raise MatmulError(status, self.error())
+
+    def set_gemm_path(self, path: GemmPath):
+        self.check(lib.charlotte_hip_matmul_set_gemm_path(self.handle, int(path)))
+
+    def close(self):
+        if self.handle:
+            lib.charlotte_hip_matmul_context_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+class Weight:
+    """A weight in the device layout (residency::WeightView of one piece)."""
+
+    def __init__(self, ctx: Context, gguf_type, rows, columns, stored: Optional[bytes] = None, device_piece=None,
+                 nbytes=None):
+        h = ctypes.c_void_p()
+        if device_piece is None:
+            buf = ctypes.create_string_buffer(bytes(stored), len(stored)) if not isinstance(stored, ctypes.Array) else stored
+            ctx.check(lib.charlotte_hip_matmul_weight_upload(ctx.handle, int(gguf_type), rows, columns, buf,
+                                                             len(stored), ctypes.byref(h)))
+        else:
+            ctx.check(lib.charlotte_hip_matmul_weight_wrap(ctx.handle, int(gguf_type), rows, columns, device_piece,
+                                                           nbytes, ctypes.byref(h)))
+        self.ctx, self.type, self.rows, self.columns, self.handle = ctx, TensorType(gguf_type), rows, columns, h
+
+    @property
+    def device(self):
+        return lib.charlotte_hip_matmul_weight_device(self.handle)
+
+    def free(self):
+        if self.handle:
+            lib.charlotte_hip_matmul_weight_free(self.handle)
+            self.handle = None
+
+
+@dataclass
+class Member:
+    weight: Weight
+    row_offset: int = 0
+    rows: Optional[int] = None
+    output_row: int = 0
+
+
+@dataclass
+class MatmulLaunch:
+    """kernels::MatmulLaunch (matmul.h:602-632) with device pointers."""
+
+    members: Sequence[Member]
+    input: int
+    outputs: Sequence[int]
+    epilogue: Epilogue = Epilogue.Write
+    activation: Activation = Activation.SiLU
+    rows: Rows = Rows.EveryToken
+    out_width: int = 0
+    gate_input: int = 0
+    gate_input_stride: int = 0
+    gate_input_column: int = 0
+    clip: int = 0
+    bias: int = 0
+    activated: bool = False
+    _desc: Optional[_Desc] = field(default=None, repr=False)
+
+    def desc(self):
+        d = _Desc()
+        for i, m in enumerate(self.members):
+            d.members[i] = _Member(m.weight.handle, m.row_offset, m.weight.rows - m.row_offset if m.rows is None else m.rows,
+                                   m.output_row)
+        d.member_count = len(self.members)
+        d.epilogue, d.activation, d.rows = int(self.epilogue), int(self.activation), int(self.rows)
+        d.input = self.input
+        for i, o in enumerate(self.outputs):
+            d.outputs[i] = o
+        d.out_width = self.out_width
+        d.gate_input, d.gate_input_stride, d.gate_input_column = self.gate_input, self.gate_input_stride, self.gate_input_column
+        d.clip, d.bias, d.activated = self.clip, self.bias, int(self.activated)
+        return d
+
+
+def launch(ctx: Context, m: MatmulLaunch, tokens: int, gate: SplitGate = kNever, range_sums=0, range_sums_bytes=0,
+           stream=None):
+    """One product over a step of `tokens` tokens, asynchronous on `stream`."""
+    if m._desc is None:
+        m._desc = m.desc()
+    ctx.check(lib.charlotte_hip_matmul_launch(ctx.handle, ctypes.byref(m._desc), _gate(gate), range_sums,
+                                              range_sums_bytes, tokens, stream))

@@ -1,0 +1,224 @@
+/*
+ * charlotte_hip_matmul — the quantized GGUF matrix product of
+ * plainsight-systems/charlotte on AMD Instinct MI355X (gfx950), behind a C ABI.
+ *
+ *   y[t][o] = sum_k W[o][k] * x[t][k]
+ *
+ * W stays in its GGUF format (Q4_0, or Q6_K repacked) in device memory and is
+ * decoded in the kernels' load path; x and y are f32. One token runs the
+ * decode form (a matrix-vector product bound by HBM), more tokens the prefill
+ * form (a tiled matrix product).
+ *
+ * What each part replaces in the reference (paths relative to its root):
+ *   charlotte_hip_matmul_desc       kernels::MatmulLaunch  src/core/kernels/matmul/matmul.h:602-632
+ *   charlotte_hip_matmul_member     a member weight's piece and rows, the Matmul
+ *                                   constants' members     src/core/kernels/matmul/matmul.wgsl:22-38,
+ *                                                          matmul.cpp:39-52
+ *   charlotte_hip_matmul_split_gate kernels::SplitGate     matmul.h:634-646
+ *   charlotte_hip_matmul_launch     kernels::matmul_launches + Program::run
+ *                                                          matmul.h:661-673, src/core/kernels/program.h:271-318
+ *   charlotte_hip_matmul_split_tokens / _range_sum_floats  matmul.h:648-659, matmul.cpp:233-250
+ *   charlotte_hip_matmul_weight_*   residency::WeightView/WeightPiece + PieceWriter
+ *                                                          src/core/residency/weight_view.h:28-53,
+ *                                                          src/core/residency/piece_writer.cpp:194-205
+ *   charlotte_hip_matmul_lay_out    formats::DeviceLayout   src/core/formats/device_layout.h:95-136
+ *   charlotte_hip_matmul_repack_q6_k formats::detail::repack_q6_k
+ *                                                          src/core/formats/q6_k/q6_k_repack.cpp:52-87
+ *   charlotte_hip_matmul_status     kernels::ProgramError  src/core/kernels/program.h:159-169
+ *
+ * Conventions: every function returns a status and never throws; a failure
+ * names its subject in charlotte_hip_matmul_last_error(ctx). A context owns
+ * one device; calls on one context come from one host thread. Launches are
+ * asynchronous and ordered on the stream given (a hipStream_t passed as
+ * void*, NULL for the null stream); the caller owns inputs and outputs, which
+ * are borrowed until the stream reaches the launch. No launch allocates.
+ *
+ * Order of addition (determinism, batch invariance): every path but the
+ * matrix-core prefill adds each output's products in the reference's one
+ * order, fixed by K alone (matmul.h:34-50): a row's G = K / 32 groups cut into
+ * 32 ranges, range r groups floor(rG/32) .. floor((r+1)G/32), each range an
+ * fma chain from zero in k order, the 32 range sums added in order to a total
+ * from zero. So a token's outputs are the same bits decoded alone or
+ * prefilled in a step of any size, and the same bits as the CPU restatement
+ * of that order.
+ */
+#ifndef CHARLOTTE_HIP_MATMUL_H
+#define CHARLOTTE_HIP_MATMUL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* kernels::ProgramError (program.h:159-169) and the launcher's
+ * preconditions (matmul.h:661-671), as codes. */
+typedef enum {
+    CHARLOTTE_HIP_MATMUL_OK = 0,
+    CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT = 1,  /* a null, a size or a pointer the operation cannot take */
+    CHARLOTTE_HIP_MATMUL_UNSUPPORTED_TYPE = 2,  /* a GGUF type this library has no kernels for */
+    CHARLOTTE_HIP_MATMUL_SHAPE_NOT_GROUPS = 3,  /* K not whole 32-weight groups, or a tensor not whole blocks */
+    CHARLOTTE_HIP_MATMUL_OUT_OF_MEMORY = 4,
+    CHARLOTTE_HIP_MATMUL_HIP_ERROR = 5,         /* the HIP runtime refused a call; its message is in last_error */
+    CHARLOTTE_HIP_MATMUL_NO_DEVICE = 6,
+    CHARLOTTE_HIP_MATMUL_UNSUPPORTED = 7        /* an epilogue, option or combination not built */
+} charlotte_hip_matmul_status;
+
+/* GGUF tensor types the kernels read (src/core/gguf/types.h:41-43). */
+enum {
+    CHARLOTTE_HIP_MATMUL_Q4_0 = 2,
+    CHARLOTTE_HIP_MATMUL_Q6_K = 14
+};
+
+/* kernels::Epilogue (matmul.h:594-599). */
+typedef enum {
+    CHARLOTTE_HIP_MATMUL_WRITE = 0,
+    CHARLOTTE_HIP_MATMUL_QKV = 1,
+    CHARLOTTE_HIP_MATMUL_GATED_ACTIVATION = 2,
+    CHARLOTTE_HIP_MATMUL_GATED_BY_INPUT = 3
+} charlotte_hip_matmul_epilogue;
+
+/* model::FeedForwardActivation, as the launcher passes it (matmul.cpp:62-69). */
+typedef enum {
+    CHARLOTTE_HIP_MATMUL_SILU = 0,
+    CHARLOTTE_HIP_MATMUL_GELU_TANH = 1,
+    CHARLOTTE_HIP_MATMUL_SIGMOID = 2
+} charlotte_hip_matmul_activation;
+
+/* kernels::Rows (src/core/kernels/interface.h:212-215). */
+typedef enum {
+    CHARLOTTE_HIP_MATMUL_EVERY_TOKEN = 0,
+    CHARLOTTE_HIP_MATMUL_LAST_TOKEN = 1  /* the head: the step's last token alone, y written as one row */
+} charlotte_hip_matmul_rows;
+
+/* Which prefill kernel runs (no counterpart: the reference has one, on WebGPU's
+ * shader cores). CANONICAL is the VALU tile in the order above, bit-exact and
+ * batch-invariant; SPLIT_F16_MFMA runs the products on the matrix cores with
+ * x split into two f16 parts, within the tolerance max|err| / max|y| <= 1e-5
+ * but not bit-exact; AUTO takes the matrix cores where a shape is built for
+ * them. */
+typedef enum {
+    CHARLOTTE_HIP_MATMUL_GEMM_AUTO = 0,
+    CHARLOTTE_HIP_MATMUL_GEMM_CANONICAL = 1,
+    CHARLOTTE_HIP_MATMUL_GEMM_SPLIT_F16_MFMA = 2
+} charlotte_hip_matmul_gemm_path;
+
+typedef struct charlotte_hip_matmul_context charlotte_hip_matmul_context;
+typedef struct charlotte_hip_matmul_weight charlotte_hip_matmul_weight;
+
+/* ---- context ---------------------------------------------------------- */
+
+charlotte_hip_matmul_status charlotte_hip_matmul_context_create(int device, charlotte_hip_matmul_context** out);
+charlotte_hip_matmul_status charlotte_hip_matmul_context_destroy(charlotte_hip_matmul_context* ctx);
+/* The last failure's message, naming its subject; "" after success. Owned by ctx. */
+const char* charlotte_hip_matmul_last_error(const charlotte_hip_matmul_context* ctx);
+charlotte_hip_matmul_status charlotte_hip_matmul_set_gemm_path(charlotte_hip_matmul_context* ctx,
+                                                               charlotte_hip_matmul_gemm_path path);
+
+/* ---- device layout (host only; no device needed) ---------------------------- */
+
+/* Bytes of the device layout of `rows` x `columns` weights of `gguf_type`:
+ * the stored bytes rounded up to 4 (device_layout.h:59-63). 0 when the type is
+ * not one of the above or the shape is not whole blocks. */
+uint64_t charlotte_hip_matmul_layout_bytes(uint32_t gguf_type, uint64_t rows, uint64_t columns);
+/* File-order blocks -> the piece's streams, in host memory: Q4_0 as its codes
+ * then its scales (device_layout.h:121), Q6_K repacked, then its lo, hi,
+ * scales and d streams (device_layout.h:124-127, q6_k.h:11-21). `device` holds
+ * layout_bytes(...) bytes. */
+charlotte_hip_matmul_status charlotte_hip_matmul_lay_out(uint32_t gguf_type, const void* stored_blocks,
+                                                         uint64_t blocks, void* device);
+/* The Q6_K repack alone, block i's stream s at streams[s] + i * width(s),
+ * widths 128, 64, 16, 2 (q6_k_repack.cpp:52-87). */
+charlotte_hip_matmul_status charlotte_hip_matmul_repack_q6_k(const void* stored_blocks, uint64_t blocks,
+                                                             void* const streams[4]);
+
+/* ---- weights ------------------------------------------------------------ */
+
+/* A weight of `rows` rows of `columns` (K) in the device layout, owned by the
+ * library: the stored blocks (file order, `bytes` of them) laid out and copied
+ * to the device. Rows need not be whole Q6_K super-blocks (Gemma 3's 1,152);
+ * the tensor must be. Synchronous. */
+charlotte_hip_matmul_status charlotte_hip_matmul_weight_upload(charlotte_hip_matmul_context* ctx,
+                                                               uint32_t gguf_type, uint64_t rows,
+                                                               uint64_t columns, const void* stored_blocks,
+                                                               uint64_t bytes, charlotte_hip_matmul_weight** out);
+/* A weight whose piece the caller already wrote in the device layout at
+ * `device_piece` (16-byte aligned), as the reference's PieceWriter writes a
+ * piece; borrowed, never freed by the library. */
+charlotte_hip_matmul_status charlotte_hip_matmul_weight_wrap(charlotte_hip_matmul_context* ctx,
+                                                             uint32_t gguf_type, uint64_t rows, uint64_t columns,
+                                                             const void* device_piece, uint64_t bytes,
+                                                             charlotte_hip_matmul_weight** out);
+charlotte_hip_matmul_status charlotte_hip_matmul_weight_free(charlotte_hip_matmul_weight* weight);
+/* The weight's piece on the device (its first stream's first byte). */
+const void* charlotte_hip_matmul_weight_device(const charlotte_hip_matmul_weight* weight);
+
+/* ---- the product ------------------------------------------------------- */
+
+/* One member of a product: rows row_offset .. row_offset + rows - 1 of
+ * `weight`, the product's next `rows` outputs.
+ *   WRITE, GATED_BY_INPUT: output index of the member's first row is
+ *     output_row (a piece's first_row, matmul.cpp:283-291), in a row of
+ *     desc.out_width outputs a token.
+ *   QKV: members Q, K, V write outputs[0], [1], [2], each `rows` wide a token
+ *     (matmul.wgsl:298-314); output_row is ignored.
+ *   GATED_ACTIVATION: members gate then up, equal rows; row_offset is each
+ *     member's first row within its weight — for a GLU over one weight's
+ *     halves, gate {w, half, half} and up {w, 0, half} (matmul.cpp:270-279). */
+typedef struct {
+    const charlotte_hip_matmul_weight* weight;
+    uint64_t row_offset;
+    uint64_t rows;
+    uint64_t output_row;
+} charlotte_hip_matmul_member;
+
+typedef struct {
+    charlotte_hip_matmul_member members[3];
+    uint32_t member_count;            /* 1, 2 or 3; members share K */
+    uint32_t epilogue;                /* charlotte_hip_matmul_epilogue */
+    uint32_t activation;              /* charlotte_hip_matmul_activation (gated epilogues, `activated`) */
+    uint32_t rows;                    /* charlotte_hip_matmul_rows */
+    const float* input;               /* device: tokens rows of K floats */
+    float* outputs[3];                /* device: WRITE/GATED* use outputs[0]; QKV all three */
+    uint64_t out_width;               /* floats a token's output row (WRITE/GATED_BY_INPUT; 0 = product rows) */
+    /* GATED_BY_INPUT: output o of token t times u[t * stride + column + o]. */
+    const float* gate_input;
+    uint32_t gate_input_stride;
+    uint32_t gate_input_column;
+    /* Options (matmul.h:229-255): `clip` four device floats in_min, in_max,
+     * out_min, out_max, or NULL; `bias` device floats, one an output row, or
+     * NULL (WRITE); `activated` nonzero applies `activation` last (WRITE). */
+    const float* clip;
+    const float* bias;
+    uint32_t activated;
+} charlotte_hip_matmul_desc;
+
+/* kernels::SplitGate: the tiled prefill splits along K when its workgroups W
+ * satisfy W * denominator <= G * numerator and W <= max_workgroups. */
+typedef struct {
+    uint32_t numerator;
+    uint32_t denominator;
+    uint32_t max_workgroups;
+} charlotte_hip_matmul_split_gate;
+
+/* One product over a step of `tokens` tokens (1 decodes; more prefill), on
+ * `stream`. `range_sums` is the split's working buffer (device, bytes), or
+ * NULL/0: a step splits only while its range sums fit it (matmul.cpp:166-172). */
+charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_context* ctx,
+                                                        const charlotte_hip_matmul_desc* desc,
+                                                        charlotte_hip_matmul_split_gate gate, void* range_sums,
+                                                        uint64_t range_sums_bytes, uint32_t tokens, void* stream);
+
+/* matmul.h:648-659: the most tokens a step may hold for the product to split,
+ * a whole number of 32-token tiles up to 512, or 1 when it never splits; and
+ * the floats range_sums must hold for it. */
+uint32_t charlotte_hip_matmul_split_tokens(uint32_t epilogue, uint64_t rows, uint64_t columns,
+                                           charlotte_hip_matmul_split_gate gate);
+uint64_t charlotte_hip_matmul_range_sum_floats(uint32_t epilogue, uint64_t rows, uint64_t columns,
+                                               charlotte_hip_matmul_split_gate gate);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

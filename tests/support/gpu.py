@@ -1,0 +1,50 @@
+"""GPU test helpers: upload a weight, run a product through the C ABI, read
+the outputs back (test infrastructure)."""
+
+import numpy as np
+
+from charlotte_amd import harness as hx
+from charlotte_amd import matmul as mm
+
+
+class Runner:
+    def __init__(self, ctx: mm.Context):
+        self.ctx = ctx
+
+    def weight(self, gtype, rows, columns, stored):
+        return mm.Weight(self.ctx, gtype, rows, columns, stored)
+
+    def product(self, members, x, tokens, out_widths, epilogue=mm.Epilogue.Write, rows=mm.Rows.EveryToken,
+                out_width=0, gate=mm.kNever, sums_bytes=0):
+        """Run one product over the first `tokens` rows of x; return each output as [rows_written, width]."""
+        x = np.ascontiguousarray(x, np.float32)
+        xb = hx.Buffer.of(x)
+        out_rows = 1 if rows == mm.Rows.LastToken else tokens
+        outs = [hx.Buffer(out_rows * w * 4) for w in out_widths]
+        for o in outs:
+            o.fill(0xFF)  # NaN: an output left unwritten shows
+        sums = hx.Buffer(sums_bytes) if sums_bytes else None
+        m = mm.MatmulLaunch(members, xb.ptr, [o.ptr for o in outs], epilogue=epilogue, rows=rows, out_width=out_width)
+        mm.launch(self.ctx, m, tokens, gate, sums.ptr if sums else 0, sums_bytes)
+        hx.sync()
+        got = [o.read(np.float32).reshape(out_rows, w) for o, w in zip(outs, out_widths)]
+        for b in [xb, *outs] + ([sums] if sums else []):
+            b.free()
+        return got
+
+    def write(self, w, x, tokens, rows=mm.Rows.EveryToken, **kw):
+        return self.product([mm.Member(w)], x, tokens, [w.rows], rows=rows, **kw)[0]
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and bool((a.view(np.uint32) == b.view(np.uint32)).all())
+
+
+def first_difference(a, b):
+    idx = np.argwhere(np.ascontiguousarray(a, np.float32).view(np.uint32) != np.ascontiguousarray(b, np.float32).view(np.uint32))
+    if idx.size == 0:
+        return None
+    i = tuple(idx[0])
+    return f"{len(idx)} differ; first at {i}: got {a[i]!r} want {b[i]!r}"
