@@ -293,7 +293,11 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
     if (hipError_t e = hipSetDevice(ctx->device); e != hipSuccess) return hip_fail(ctx, e, "launch: hipSetDevice");
     auto* s = static_cast<hipStream_t>(stream);
     hipError_t e;
-    if (tokens == 1 || a.last_token) {
+    const bool decode = tokens == 1 || a.last_token;
+    if (decode && !chm::gemv_supports(a.groups))
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_UNSUPPORTED,
+                    "launch: decode of K = " + std::to_string(head->columns) + " (built for K up to 8,192)");
+    if (decode) {
         e = chm::launch_gemv(a, head->type, ctx->compute_units, s);
     } else {
         e = chm::launch_gemm_canonical(a, head->type, ctx->compute_units, s);

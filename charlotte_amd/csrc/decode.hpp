@@ -1,0 +1,123 @@
+// Fast exact decode of one 32-weight group into the canonical fma chain.
+//
+// formats.hpp's weight() is one weight at a time; here a group's bytes are
+// taken a dword — four codes — at a time:
+//   - the four codes are assembled into the four bytes of a dword (Q4_0: a
+//     mask; Q6_K: a bitfield insert of the low nibbles into the high pairs);
+//   - v_perm_b32 lifts two code bytes into the low bytes of two binary16
+//     values whose high byte is 0x64, i.e. 1024 + q, exactly;
+//   - v_fma_mix_f32 takes one binary16 half as an f32 operand, so
+//     w = fma(1024 + q, scale, -(1024 + bias) * scale) is the weight, exactly:
+//     (1024 + q) * scale has at most 11 + 18 bits and the fma rounds once, and
+//     the constant and the result are exact (q - bias is at most 6 bits, the
+//     scale at most 18);
+//   - the chain s = fma(w_l, x_l, s) runs in k order, as formats.hpp's.
+// About 2.9 VALU operations a Q4_0 weight and 3.4 a Q6_K weight, against
+// formats.hpp's 5 to 6. The bits are the same: each w is the exact weight.
+#pragma once
+
+#include "formats.hpp"
+
+namespace chm {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+constexpr uint32_t kHalf1024 = 0x64646464u;    // 0x64 in every byte: binary16 1024 + q's high byte
+constexpr uint32_t kLowPair = 0x04010400u;     // bytes 0, 1 of a dword -> halves (1024 + b0, 1024 + b1)
+constexpr uint32_t kHighPair = 0x04030402u;    // bytes 2, 3 -> halves (1024 + b2, 1024 + b3)
+
+__device__ __forceinline__ half2_t lift(uint32_t codes, uint32_t selector) {
+    return __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(kHalf1024, codes, selector));
+}
+
+// Four weights from four code bytes, continuing the chain over x[0..3].
+__device__ __forceinline__ float chain4(uint32_t codes, float scale, float offset, const float* x, float s) {
+    const half2_t a = lift(codes, kLowPair), b = lift(codes, kHighPair);
+    s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(a.x), scale, offset), x[0], s);
+    s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(a.y), scale, offset), x[1], s);
+    s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(b.x), scale, offset), x[2], s);
+    s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(b.y), scale, offset), x[3], s);
+    return s;
+}
+
+__device__ __forceinline__ uint32_t bitfield_insert(uint32_t mask, uint32_t a, uint32_t b) {
+    return (a & mask) | (b & ~mask);
+}
+
+// A Q4_0 group: 4 code dwords, its fp16 scale bits.
+__device__ __forceinline__ float chain_q4_0(const uint32_t w[4], uint32_t d_bits, const float* x, float s) {
+    const float d = half_to_float(d_bits);
+    // low nibbles: (1024 + q) d - 1032 d; high nibbles as bytes 16q:
+    // (1024 + 16q) (d / 16) - 72 d. d / 16 is exact (f32 has the range).
+    const float low_offset = -1032.0f * d, d16 = d * 0.0625f, high_offset = -72.0f * d;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s = chain4(w[c] & 0x0F0F0F0Fu, d, low_offset, x + 4 * c, s);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s = chain4(w[c] & 0xF0F0F0F0u, d16, high_offset, x + 16 + 4 * c, s);
+    return s;
+}
+
+// A Q6_K group: 4 lo dwords, 2 hi dwords, its two int8 scales (low 16 bits
+// of sc), its super-block's fp16 d bits.
+__device__ __forceinline__ float chain_q6_k(const uint32_t lo[4], const uint32_t hi[2], uint32_t sc, uint32_t d_bits,
+                                            const float* x, float s) {
+    const float d = half_to_float(d_bits);
+    const float first = d * static_cast<float>(static_cast<int8_t>(sc & 0xFFu));
+    const float second = d * static_cast<float>(static_cast<int8_t>((sc >> 8) & 0xFFu));
+    const float first_offset = -1056.0f * first, second_offset = -1056.0f * second;
+    // hi byte m: pairs of weights m, m + 8, m + 16, m + 24 at bits 0, 2, 4, 6.
+    // a: pairs at bits 0 and 4 of each byte; b: the others, moved there.
+    const uint32_t a0 = hi[0] & 0x33333333u, a1 = hi[1] & 0x33333333u;
+    const uint32_t b0 = (hi[0] >> 2) & 0x33333333u, b1 = (hi[1] >> 2) & 0x33333333u;
+    constexpr uint32_t kNib = 0x0F0F0F0Fu;
+    // weights 0..15: low nibbles of lo, pairs at bits 0 (l < 8) or 2 (l >= 8), moved to bits 4-5
+    s = chain4(bitfield_insert(kNib, lo[0], a0 << 4), first, first_offset, x + 0, s);
+    s = chain4(bitfield_insert(kNib, lo[1], a1 << 4), first, first_offset, x + 4, s);
+    s = chain4(bitfield_insert(kNib, lo[2], b0 << 4), first, first_offset, x + 8, s);
+    s = chain4(bitfield_insert(kNib, lo[3], b1 << 4), first, first_offset, x + 12, s);
+    // weights 16..31: high nibbles of lo, pairs at bits 4 (l < 24) or 6 (l >= 24), at bits 4-5
+    s = chain4(bitfield_insert(kNib, lo[0] >> 4, a0), second, second_offset, x + 16, s);
+    s = chain4(bitfield_insert(kNib, lo[1] >> 4, a1), second, second_offset, x + 20, s);
+    s = chain4(bitfield_insert(kNib, lo[2] >> 4, b0), second, second_offset, x + 24, s);
+    s = chain4(bitfield_insert(kNib, lo[3] >> 4, b1), second, second_offset, x + 28, s);
+    return s;
+}
+
+// A group's raw bytes as a kernel holds them between load and use.
+template <uint32_t F>
+struct Raw;
+
+template <>
+struct Raw<kQ4_0> {
+    uint32_t w[4];
+    uint32_t d;
+    __device__ __forceinline__ void load(const uint8_t* piece, uint64_t n, uint64_t gi) {
+        const uint4 c = *reinterpret_cast<const uint4*>(piece + 16 * gi);
+        w[0] = c.x;
+        w[1] = c.y;
+        w[2] = c.z;
+        w[3] = c.w;
+        d = *reinterpret_cast<const uint16_t*>(piece + 16 * n + 2 * gi);
+    }
+    __device__ __forceinline__ float chain(const float* x, float s) const { return chain_q4_0(w, d, x, s); }
+};
+
+template <>
+struct Raw<kQ6_K> {
+    uint32_t lo[4], hi[2], sc, d;
+    __device__ __forceinline__ void load(const uint8_t* piece, uint64_t n, uint64_t gi) {
+        const uint4 l = *reinterpret_cast<const uint4*>(piece + 16 * gi);
+        const uint2 h = *reinterpret_cast<const uint2*>(piece + 128 * n + 8 * gi);
+        lo[0] = l.x;
+        lo[1] = l.y;
+        lo[2] = l.z;
+        lo[3] = l.w;
+        hi[0] = h.x;
+        hi[1] = h.y;
+        sc = *reinterpret_cast<const uint16_t*>(piece + 192 * n + 2 * gi);
+        d = *reinterpret_cast<const uint16_t*>(piece + 208 * n + 2 * (gi / 8));
+    }
+    __device__ __forceinline__ float chain(const float* x, float s) const { return chain_q6_k(lo, hi, sc, d, x, s); }
+};
+
+}  // namespace chm

@@ -18,14 +18,7 @@ namespace chm {
 constexpr int kRowsATile = 128;
 
 __device__ __forceinline__ void store_output(const Product& a, uint32_t token, uint32_t p, float v) {
-    uint32_t row;
-    const int m = locate(a, p, &row);
-    const Member& mem = a.m[m];
-    if (a.epilogue == kQKV) {
-        mem.out[static_cast<uint64_t>(token) * mem.rows + (p - mem.first)] = v;
-    } else {
-        mem.out[static_cast<uint64_t>(token) * mem.out_width + mem.out_row + (p - mem.first)] = v;
-    }
+    *output_of(a, p, token) = v;
 }
 
 template <uint32_t F, int BM>
@@ -43,9 +36,7 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
     const uint32_t srow = t & 127u, shalf = t >> 7;
     const uint32_t sp = n0 + srow;
     const bool slive = sp < a.rows;
-    uint32_t spiece_row = 0;
-    const Member* smem = &a.m[0];
-    if (slive) smem = &a.m[locate(a, sp, &spiece_row)];
+    const Piece spiece = piece_of(a, slive ? sp : 0);
     constexpr int XPer = BM / 8;                 // floats a lane stages: 16 or 8
     const uint32_t xtok = t % BM, xpart = t / BM;
     const bool xlive = m0 + xtok < a.tokens;
@@ -67,13 +58,13 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
         {
             float w[16];
             if (slive) {
-                const uint64_t gi = static_cast<uint64_t>(spiece_row) * G + g;
+                const uint64_t gi = static_cast<uint64_t>(spiece.row) * G + g;
                 if constexpr (F == kQ4_0) {
-                    const Q4_0Group q = load_q4_0(smem->piece, smem->blocks, gi);
+                    const Q4_0Group q = load_q4_0(spiece.piece, spiece.blocks, gi);
 #pragma unroll
                     for (int j = 0; j < 16; ++j) w[j] = weight(q, 16 * shalf + j);
                 } else {
-                    const Q6_KGroup q = load_q6_k(smem->piece, smem->blocks, gi);
+                    const Q6_KGroup q = load_q6_k(spiece.piece, spiece.blocks, gi);
 #pragma unroll
                     for (int j = 0; j < 16; ++j) w[j] = weight(q, 16 * shalf + j);
                 }

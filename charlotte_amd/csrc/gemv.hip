@@ -1,48 +1,77 @@
 // Decode: the matrix-vector product, one token, bound by reading each weight
-// once from HBM. Every output in the canonical order (formats.hpp's chain,
-// range sums added in order from zero), so its bits are the prefill tile's
-// and the CPU restatement's.
+// once from HBM. Every output in the canonical order, so its bits are the
+// prefill tile's and the CPU restatement's.
 //
-// gemv_ranges — the reference's lane mapping (matmul.wgsl:207-296) on wave64:
-// a wave is two half-waves, each taking one row at a time; lane r of a half
-// owns range r, so the half's 32 lanes read 32 adjacent groups of the row —
-// adjacent 16-byte code blocks, coalesced — and lane r's slice of x never
-// changes, so it is loaded into registers once per wave and reused for every
-// row the wave takes. Each half takes `rows_per_half` consecutive rows (1 to
-// 32, chosen so the launch still fills the GPU); the range sums meet in LDS
-// and lane i then adds row i's 32 sums in order, all lanes at once.
+// Mapping: L lanes a row. Lane j of a row owns ranges [32j/L, 32(j+1)/L) —
+// groups [Gj/L, G(j+1)/L), at most SPAN of them — and runs each range's chain
+// from zero; a wave takes 64/L rows a step and `steps` steps. L = 32 is the
+// reference's mapping (matmul.wgsl:207-243): a half-wave reads a row's 32
+// adjacent groups, coalesced. It balances when 32 divides G (K = 1,024,
+// 2,048, 3,072); for K = 1,152 (G = 36) four ranges hold two groups and the
+// rest one, so L = 32 leaves 44% of the lanes idle, and L = 4 gives every
+// lane exactly 9 groups — 8 ranges, 144 contiguous code bytes.
+//
+// x: lane j's slice never changes, so with SPAN <= 3 groups it is loaded into
+// registers once; otherwise the workgroup stages all of x in LDS once and
+// lanes read it there (lanes of one j read the same words: a broadcast).
+// Each step loads all of its groups' bytes before decoding any, so a wave
+// has a step's weights in flight at once.
+// Range sums meet in LDS, 33 floats a row (padded against bank conflicts);
+// then lane i adds row i's 32 sums in order from zero and writes the output.
+#include <algorithm>
+
+#include "decode.hpp"
 #include "product.hpp"
 
 namespace chm {
 
-constexpr int kWaves = 4;        // waves a workgroup
-constexpr int kPad = 33;         // a row's 32 range sums, padded so lane-per-row reads spread over banks
+// Workgroups a CU is asked to hold at once, as launch bounds: the L = 32
+// kernel's registers allow 4 waves a SIMD at SPAN <= 2 as it stands; the L = 4
+// Q6_K kernel holds a 9-group run (65 registers) and spills past 128.
+#ifndef CHM_RANGES_MIN_BLOCKS
+#define CHM_RANGES_MIN_BLOCKS 2
+#endif
+#ifndef CHM_QUARTERS_MIN_BLOCKS
+#define CHM_QUARTERS_MIN_BLOCKS 3
+#endif
 
-__device__ __forceinline__ void write_output(const Product& a, uint32_t p, float total) {
-    uint32_t row;
-    const int m = locate(a, p, &row);
-    const Member& mem = a.m[m];
-    const uint32_t at = (a.epilogue == kQKV ? 0u : mem.out_row) + (p - mem.first);
-    mem.out[at] = total;
+constexpr int kWaves = 4;     // waves a workgroup
+constexpr int kPad = 33;      // a row's 32 range sums, padded
+constexpr int kWaveRows = 64; // rows a wave covers at most (steps * 64 / L)
+constexpr uint32_t kMaxStagedK = 8192;
+
+// The range sums a wave writes to LDS are read back by lanes of the same wave
+// only. A wave's LDS operations execute in order, so ordering the compiler's
+// view of them is all that is needed: no workgroup barrier, whose fence would
+// also wait for every outstanding global load.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// MAXG > 0: every range holds at most MAXG groups and x's slice lives in
-// registers. MAXG == 0: any width; x is read per group (from cache).
-template <uint32_t F, int MAXG>
-__global__ __launch_bounds__(256) void gemv_ranges(Product a, uint32_t rows_per_half) {
-    __shared__ float partials[kWaves][64 * kPad];
+__device__ __forceinline__ void write_output(const Product& a, uint32_t p, float total) {
+    *output_of(a, p, 0) = total;
+}
+
+// L = 32: lane r of a half-wave owns range r — at most SPAN groups, its
+// chain from zero over them, and no other range; its range sum goes to LDS.
+template <uint32_t F, int SPAN, bool XREG>
+__global__ __launch_bounds__(256, CHM_RANGES_MIN_BLOCKS) void gemv_ranges(Product a, uint32_t steps, uint32_t tiles) {
+    __shared__ float partials[kWaves][kWaveRows * kPad];
+    extern __shared__ float4 xs4[];  // x, staged when it is not held in registers
+
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t half = lane >> 5, r = lane & 31u;
     const uint32_t G = a.groups;
     const uint32_t g0 = range_lo(r, G), g1 = range_lo(r + 1, G);
     const uint32_t token = a.last_token ? a.tokens - 1 : 0;
     const float* x = a.x + static_cast<uint64_t>(token) * G * 32;
-    const uint32_t first_row = ((blockIdx.x * kWaves + wave) * 2 + half) * rows_per_half;
 
-    float xr[MAXG > 0 ? MAXG * 32 : 1];
-    if constexpr (MAXG > 0) {
+    float xr[XREG ? SPAN * 32 : 1];
+    if constexpr (XREG) {
 #pragma unroll
-        for (int i = 0; i < MAXG; ++i) {
+        for (int i = 0; i < SPAN; ++i) {
             if (g0 + i < g1) {
                 const float4* src = reinterpret_cast<const float4*>(x + (g0 + i) * 32);
 #pragma unroll
@@ -55,81 +84,393 @@ __global__ __launch_bounds__(256) void gemv_ranges(Product a, uint32_t rows_per_
                 }
             }
         }
+    } else {
+        const float4* src = reinterpret_cast<const float4*>(x);
+        for (uint32_t v = threadIdx.x; v < G * 8; v += 256) xs4[v] = src[v];
+        __syncthreads();
     }
 
     float* mine = partials[wave];
-    for (uint32_t i = 0; i < rows_per_half; ++i) {
-        const uint32_t p = first_row + i;
-        float s = 0.0f;
-        if (p < a.rows) {
-            uint32_t row;
-            const Member& mem = a.m[locate(a, p, &row)];
-            const uint64_t base = static_cast<uint64_t>(row) * G;
-            if constexpr (MAXG > 0) {
+    // Rows a batch: B steps' loads are issued before any is decoded, so a
+    // wave keeps B rows' bytes in flight rather than one.
+    constexpr int B = SPAN >= 3 ? 2 : SPAN == 2 ? 4 : 8;
+    for (uint32_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+        const uint32_t wave_first = (tile * kWaves + wave) * steps * 2;
+        for (uint32_t step0 = 0; step0 < steps; step0 += B) {
+            Raw<F> raw[B][SPAN];
+            // Every lane issues the same loads on every path — rows past the
+            // product read its last row, groups past the lane's range the
+            // row's last group, unused — so a decode waits for its own loads.
 #pragma unroll
-                for (int j = 0; j < MAXG; ++j) {
-                    if (g0 + j < g1) s = chain_group<F>(mem.piece, mem.blocks, base + g0 + j, xr + 32 * j, s);
-                }
-            } else {
-                for (uint32_t g = g0; g < g1; ++g) {
-                    float xg[32];
-                    const float4* src = reinterpret_cast<const float4*>(x + g * 32);
+            for (int b = 0; b < B; ++b) {
+                const uint32_t p = min(wave_first + (step0 + b) * 2 + half, a.rows - 1);
+                const Piece w = piece_of(a, p);
+                const uint64_t row0 = static_cast<uint64_t>(w.row) * G;
 #pragma unroll
-                    for (int v = 0; v < 8; ++v) {
-                        const float4 q = src[v];
-                        xg[4 * v + 0] = q.x;
-                        xg[4 * v + 1] = q.y;
-                        xg[4 * v + 2] = q.z;
-                        xg[4 * v + 3] = q.w;
+                for (int i = 0; i < SPAN; ++i) raw[b][i].load(w.piece, w.blocks, row0 + min(g0 + i, G - 1));
+            }
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const uint32_t slot = (step0 + b) * 2 + half;
+                if (step0 + b >= steps) break;
+                float s = 0.0f;
+                if (wave_first + slot < a.rows) {
+#pragma unroll
+                    for (int i = 0; i < SPAN; ++i) {
+                        if (g0 + i < g1) {
+                            if constexpr (XREG) {
+                                s = raw[b][i].chain(xr + 32 * i, s);
+                            } else {
+                                float xg[32];
+                                const float4* src = xs4 + 8 * (g0 + i);
+#pragma unroll
+                                for (int v = 0; v < 8; ++v) {
+                                    const float4 q = src[v];
+                                    xg[4 * v] = q.x;
+                                    xg[4 * v + 1] = q.y;
+                                    xg[4 * v + 2] = q.z;
+                                    xg[4 * v + 3] = q.w;
+                                }
+                                s = raw[b][i].chain(xg, s);
+                            }
+                        }
                     }
-                    s = chain_group<F>(mem.piece, mem.blocks, base + g, xg, s);
+                }
+                mine[slot * kPad + r] = s;  // an empty range's sum is zero
+            }
+        }
+        wave_sync();
+        if (lane < steps * 2) {
+            const uint32_t p = wave_first + lane;
+            if (p < a.rows) {
+                const float* sums = mine + lane * kPad;
+                float total = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 32; ++q) total = total + sums[q];
+                write_output(a, p, total);
+            }
+        }
+        wave_sync();  // the sums are read before the next tile writes them
+    }
+}
+
+// Q6_K's 9 groups from a lane's run: lo, hi, scales contiguous from group gi0,
+// and the two super-blocks' d the run touches (9 groups from gi0 = 9m span
+// super-blocks gi0 / 8 and gi0 / 8 + 1).
+template <uint32_t F, int SPAN>
+struct Run;
+
+template <int SPAN>
+struct Run<kQ4_0, SPAN> {
+    uint32_t w[SPAN][4];
+    uint32_t d[SPAN];
+    __device__ __forceinline__ void load(const uint8_t* piece, uint64_t n, uint64_t gi0) {
+        const uint4* c = reinterpret_cast<const uint4*>(piece + 16 * gi0);
+        const uint16_t* s = reinterpret_cast<const uint16_t*>(piece + 16 * n + 2 * gi0);
+#pragma unroll
+        for (int i = 0; i < SPAN; ++i) {
+            const uint4 q = c[i];
+            w[i][0] = q.x;
+            w[i][1] = q.y;
+            w[i][2] = q.z;
+            w[i][3] = q.w;
+            d[i] = s[i];
+        }
+    }
+    __device__ __forceinline__ float chain(int i, uint64_t, const float* x, float s) const {
+        return chain_q4_0(w[i], d[i], x, s);
+    }
+};
+
+template <int SPAN>
+struct Run<kQ6_K, SPAN> {
+    // The lane's run of SPAN groups in few wide loads:
+    //   lo     SPAN 16-byte loads (16 bytes a group, 16-byte aligned);
+    //   hi     8 bytes a group from an 8-byte-aligned start: the 16-byte-
+    //          aligned window holding it, and its phase there (0 or 2 dwords);
+    //   scales 2 bytes a group from a 2-byte-aligned start: the 8-byte-aligned
+    //          window holding it, realigned once with v_alignbyte;
+    //   d      the run touches super-blocks gi0 / 8 and, at most, the next
+    //          (SPAN <= 9): two dwords from a 4-byte-aligned start, pulled back
+    //          so they never pass the piece's end, (210 n + 3) & ~3.
+    // Every read lies inside the piece's layout (its streams run on past each
+    // window's slack: hi into the scales, scales into the d's).
+    static_assert(SPAN <= 9, "a run spans at most two super-blocks");
+    static constexpr int kHiWords = (8 * SPAN + 8 + 15) / 16 * 4;
+    static constexpr int kScWords = (2 * SPAN + 6 + 7) / 8 * 2;
+    static constexpr int kScAligned = (2 * SPAN + 3) / 4;
+    uint32_t lo[SPAN][4];
+    uint32_t hiw[kHiWords];
+    uint32_t sc[kScAligned];
+    uint32_t dw[2];
+    uint32_t hi_phase, d_byte;
+    uint64_t first_block;
+    __device__ __forceinline__ void load(const uint8_t* piece, uint64_t n, uint64_t gi0) {
+        const uint4* l = reinterpret_cast<const uint4*>(piece + 16 * gi0);
+#pragma unroll
+        for (int i = 0; i < SPAN; ++i) {
+            const uint4 q = l[i];
+            lo[i][0] = q.x;
+            lo[i][1] = q.y;
+            lo[i][2] = q.z;
+            lo[i][3] = q.w;
+        }
+        const uint64_t hi_at = 128 * n + 8 * gi0;
+        const uint4* h = reinterpret_cast<const uint4*>(piece + (hi_at & ~uint64_t{15}));
+        hi_phase = static_cast<uint32_t>(hi_at & 15) >> 2;
+#pragma unroll
+        for (int i = 0; i < kHiWords / 4; ++i) {
+            const uint4 q = h[i];
+            hiw[4 * i] = q.x;
+            hiw[4 * i + 1] = q.y;
+            hiw[4 * i + 2] = q.z;
+            hiw[4 * i + 3] = q.w;
+        }
+        const uint64_t sc_at = 192 * n + 2 * gi0;
+        const uint2* c = reinterpret_cast<const uint2*>(piece + (sc_at & ~uint64_t{7}));
+        uint32_t scw[kScWords];
+#pragma unroll
+        for (int i = 0; i < kScWords / 2; ++i) {
+            const uint2 q = c[i];
+            scw[2 * i] = q.x;
+            scw[2 * i + 1] = q.y;
+        }
+        const uint32_t sc_byte = static_cast<uint32_t>(sc_at & 7);  // 0, 2, 4 or 6
+        const bool skip = sc_byte >= 4;
+#pragma unroll
+        for (int k = 0; k < kScAligned; ++k) {
+            const uint32_t a0 = skip ? scw[k + 1] : scw[k];
+            // The last aligned dword's high half is never used; its index is
+            // held inside the window.
+            const uint32_t a1 = skip ? scw[k + 2 < kScWords ? k + 2 : kScWords - 1] : scw[k + 1];
+            sc[k] = __builtin_amdgcn_alignbyte(a1, a0, sc_byte & 3);
+        }
+        first_block = gi0 / 8;
+        const uint64_t d_at = 208 * n + 2 * first_block;
+        const uint64_t end = (210 * n + 3) & ~uint64_t{3};
+        uint64_t at = d_at & ~uint64_t{3};
+        if (at + 8 > end) at = end - 8;
+        const uint32_t* dp = reinterpret_cast<const uint32_t*>(piece + at);
+        dw[0] = dp[0];
+        dw[1] = dp[1];
+        d_byte = static_cast<uint32_t>(d_at - at);
+    }
+    __device__ __forceinline__ float chain(int i, uint64_t gi, const float* x, float s) const {
+        const uint32_t h[2] = {hi_phase == 0 ? hiw[2 * i] : hiw[2 * i + 2],
+                               hi_phase == 0 ? hiw[2 * i + 1] : hiw[2 * i + 3]};
+        const uint32_t scales = (sc[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+        const uint32_t byte = d_byte + 2 * static_cast<uint32_t>(gi / 8 - first_block);
+        const uint64_t both = (static_cast<uint64_t>(dw[1]) << 32) | dw[0];
+        const uint32_t d = static_cast<uint32_t>(both >> (8 * byte)) & 0xFFFFu;
+        return chain_q6_k(lo[i], h, scales, d, x, s);
+    }
+};
+
+// x in LDS for the L = 4 kernel: slice j (groups SPAN j .. SPAN j + SPAN - 1)
+// at float4 SPAN 8 j + j — one float4 of padding a slice, so the 4 slices a
+// read takes start in different banks.
+template <int SPAN>
+__device__ __forceinline__ uint32_t x_slot(uint32_t v) {
+    return v + v / (8 * SPAN);
+}
+
+// L = 4: lane j of a row owns ranges 8j .. 8j + 7, exactly G / 4 = SPAN
+// groups (G = 4 SPAN, G >= 32, so no range is empty). Its run's bytes are
+// contiguous. With CHM_QUARTERS_PIPELINE, a wave loads its next step's runs
+// while it decodes the current one (two run buffers, used in turn).
+#ifndef CHM_QUARTERS_PIPELINE
+#define CHM_QUARTERS_PIPELINE 0
+#endif
+
+template <uint32_t F, int SPAN>
+__global__ __launch_bounds__(256, CHM_QUARTERS_MIN_BLOCKS) void gemv_quarters(Product a, uint32_t steps, uint32_t tiles) {
+    __shared__ float partials[kWaves][kWaveRows * kPad];
+    extern __shared__ float4 xs4[];
+
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t rho = lane >> 2, j = lane & 3u;
+    const uint32_t G = a.groups;
+    const uint32_t g0 = SPAN * j;
+    const uint32_t token = a.last_token ? a.tokens - 1 : 0;
+    const float* x = a.x + static_cast<uint64_t>(token) * G * 32;
+    {
+        const float4* src = reinterpret_cast<const float4*>(x);
+        for (uint32_t v = threadIdx.x; v < G * 8; v += 256) xs4[x_slot<SPAN>(v)] = src[v];
+    }
+    const float4* xl = xs4 + x_slot<SPAN>(8 * g0);
+    // Which of the run's groups end a range; the run's first range is 8j.
+    uint32_t ends = 0;
+#pragma unroll
+    for (int i = 0; i < SPAN; ++i) {
+        const uint32_t g = g0 + i;
+        const uint32_t r = (32 * g + 31) / G;  // the range holding g
+        if (g + 1 == range_lo(r + 1, G)) ends |= 1u << i;
+    }
+    __syncthreads();
+
+    float* mine = partials[wave];
+    // Step n of this wave: tile blockIdx.x + (n / steps) gridDim.x, step n % steps.
+    const uint32_t total_steps = (tiles - blockIdx.x + gridDim.x - 1) / gridDim.x * steps;
+    auto row_of = [&](uint32_t n) -> uint32_t {
+        const uint32_t tile = blockIdx.x + (n / steps) * gridDim.x;
+        return (tile * kWaves + wave) * steps * 16 + (n % steps) * 16 + rho;
+    };
+    // Every step issues the same loads — a row past the product reads the
+    // last row, unused — so the count of loads in flight is the same on every
+    // path and a decode waits for its own step's loads only.
+    auto load = [&](Run<F, SPAN>& run, uint32_t n) {
+        const uint32_t p = min(row_of(n < total_steps ? n : total_steps - 1), a.rows - 1);
+        const Piece w = piece_of(a, p);
+        run.load(w.piece, w.blocks, static_cast<uint64_t>(w.row) * G + g0);
+    };
+    auto decode = [&](const Run<F, SPAN>& run, uint32_t n) {
+        const uint32_t p = row_of(n);
+        const uint32_t slot = (n % steps) * 16 + rho;
+        float* sums = mine + slot * kPad;
+        if (p < a.rows) {
+            const uint64_t first_gi = static_cast<uint64_t>(piece_of(a, p).row) * G + g0;
+            float s = 0.0f;
+            uint32_t r = 8 * j;
+#pragma unroll
+            for (int i = 0; i < SPAN; ++i) {
+                float xg[32];
+#pragma unroll
+                for (int v = 0; v < 8; ++v) {
+                    const float4 q = xl[8 * i + v];
+                    xg[4 * v] = q.x;
+                    xg[4 * v + 1] = q.y;
+                    xg[4 * v + 2] = q.z;
+                    xg[4 * v + 3] = q.w;
+                }
+                s = run.chain(i, first_gi + i, xg, s);
+                if (ends & (1u << i)) {
+                    sums[r] = s;
+                    s = 0.0f;
+                    ++r;
                 }
             }
         }
-        mine[(half * rows_per_half + i) * kPad + r] = s;
-    }
-    __syncthreads();
-    if (lane < 2 * rows_per_half) {
-        const uint32_t p = ((blockIdx.x * kWaves + wave) * 2 + lane / rows_per_half) * rows_per_half +
-                           lane % rows_per_half;
-        if (p < a.rows) {
-            const float* sums = mine + lane * kPad;
-            float total = 0.0f;
+        if (n % steps == steps - 1) {  // a tile's last step: its rows' totals
+            wave_sync();
+            const uint32_t tile_first = p - slot;
+            if (lane < steps * 16) {
+                const uint32_t q = tile_first + lane;
+                if (q < a.rows) {
+                    const float* rs = mine + lane * kPad;
+                    float total = 0.0f;
 #pragma unroll
-            for (int q = 0; q < 32; ++q) total = total + sums[q];
-            write_output(a, p, total);
+                    for (int k = 0; k < 32; ++k) total = total + rs[k];
+                    write_output(a, q, total);
+                }
+            }
+            wave_sync();
         }
+    };
+    if constexpr (CHM_QUARTERS_PIPELINE) {
+        Run<F, SPAN> even, odd;
+        load(even, 0);
+        for (uint32_t n = 0; n < total_steps; n += 2) {
+            load(odd, n + 1);
+            decode(even, n);
+            if (n + 1 >= total_steps) break;
+            load(even, n + 2);
+            decode(odd, n + 1);
+        }
+    } else {
+        for (uint32_t n = 0; n < total_steps; ++n) {
+            Run<F, SPAN> run;
+            load(run, n);
+            decode(run, n);
+        }
+    }
+}
+
+// How a product's GEMV runs: lanes a row, the most groups a lane holds,
+// whether x's slice is held in registers, and the steps a wave takes.
+struct GemvPlan {
+    int lanes, span;
+    bool xreg;
+    uint32_t steps;
+};
+
+// K = 1,152 (G = 36) takes 4 lanes a row, 9 groups each; every other K of
+// whole 32-groups up to 8,192 takes the reference's 32, x in registers while
+// a lane's slice is at most 3 groups. Returns false for K past 8,192.
+bool gemv_plan(uint32_t rows, uint32_t groups, uint32_t compute_units, GemvPlan* plan) {
+    if (groups == 0 || groups * 32 > kMaxStagedK) return false;
+    if (groups == 36) {
+        *plan = {4, 9, false, 1};
+    } else {
+        const int span = static_cast<int>((groups + 31) / 32);
+        *plan = {32, span, span <= 3, 1};
+    }
+    const uint32_t rows_a_step = 64 / plan->lanes;
+    const uint32_t max_steps = kWaveRows / rows_a_step;
+    // Steps a wave: the most, up to max_steps, that still gives every CU
+    // about 8 waves.
+    const uint32_t steps = rows / (rows_a_step * compute_units * 8);
+    plan->steps = steps < 1 ? 1 : steps > max_steps ? max_steps : steps;
+    return true;
+}
+
+bool gemv_supports(uint32_t groups) {
+    GemvPlan plan;
+    return gemv_plan(1, groups, 1, &plan);
+}
+
+// Workgroups of `kernel` a CU holds at once with `lds` bytes of dynamic LDS.
+template <typename K>
+static uint32_t resident(K kernel, size_t lds) {
+    int blocks = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 256, lds) != hipSuccess || blocks < 1) blocks = 1;
+    return static_cast<uint32_t>(blocks);
+}
+
+// A grid of at most the workgroups the GPU holds at once, each looping over
+// tiles, so no tail round runs part-empty.
+template <uint32_t F, int L, int SPAN, bool XREG>
+static void go(const Product& a, uint32_t steps, uint32_t compute_units, hipStream_t stream) {
+    const uint32_t rows_a_tile = kWaves * steps * (64 / L);
+    const uint32_t tiles = (a.rows + rows_a_tile - 1) / rows_a_tile;
+    const size_t lds = XREG ? 0 : (static_cast<size_t>(a.groups) * 32 + (L == 4 ? 16 : 0)) * sizeof(float);
+    if constexpr (L == 32) {
+        thread_local size_t cached_lds = ~size_t{0};
+        thread_local uint32_t per_cu = 1;
+        if (cached_lds != lds) per_cu = resident(gemv_ranges<F, SPAN, XREG>, lds), cached_lds = lds;
+        const dim3 grid(std::min(tiles, per_cu * compute_units));
+        hipLaunchKernelGGL((gemv_ranges<F, SPAN, XREG>), grid, dim3(256), lds, stream, a, steps, tiles);
+    } else {
+        thread_local size_t cached_lds = ~size_t{0};
+        thread_local uint32_t per_cu = 1;
+        if (cached_lds != lds) per_cu = resident(gemv_quarters<F, SPAN>, lds), cached_lds = lds;
+        const dim3 grid(std::min(tiles, per_cu * compute_units));
+        hipLaunchKernelGGL((gemv_quarters<F, SPAN>), grid, dim3(256), lds, stream, a, steps, tiles);
     }
 }
 
 template <uint32_t F>
-static hipError_t launch_format(const Product& a, uint32_t rows_per_half, hipStream_t stream) {
-    const uint32_t rows_a_block = kWaves * 2 * rows_per_half;
-    const dim3 grid((a.rows + rows_a_block - 1) / rows_a_block);
-    const uint32_t span = (a.groups + 31) / 32;  // the most groups a range holds
-    switch (span) {
-        case 1: hipLaunchKernelGGL((gemv_ranges<F, 1>), grid, dim3(256), 0, stream, a, rows_per_half); break;
-        case 2: hipLaunchKernelGGL((gemv_ranges<F, 2>), grid, dim3(256), 0, stream, a, rows_per_half); break;
-        case 3: hipLaunchKernelGGL((gemv_ranges<F, 3>), grid, dim3(256), 0, stream, a, rows_per_half); break;
-        default: hipLaunchKernelGGL((gemv_ranges<F, 0>), grid, dim3(256), 0, stream, a, rows_per_half); break;
+static hipError_t launch_format(const Product& a, const GemvPlan& plan, uint32_t cus, hipStream_t stream) {
+    if (plan.lanes == 4) {
+        go<F, 4, 9, false>(a, plan.steps, cus, stream);
+    } else {
+        switch (plan.span) {
+            case 1: go<F, 32, 1, true>(a, plan.steps, cus, stream); break;
+            case 2: go<F, 32, 2, true>(a, plan.steps, cus, stream); break;
+            case 3: go<F, 32, 3, true>(a, plan.steps, cus, stream); break;
+            case 4: go<F, 32, 4, false>(a, plan.steps, cus, stream); break;
+            case 5: case 6: go<F, 32, 6, false>(a, plan.steps, cus, stream); break;
+            case 7: case 8: go<F, 32, 8, false>(a, plan.steps, cus, stream); break;
+            default: return hipErrorInvalidValue;
+        }
     }
     return hipGetLastError();
 }
 
-// Rows a half-wave takes: the most, up to 32, that still gives every CU
-// about 8 waves, so x's registers are reused as far as the GPU's fill allows.
-uint32_t gemv_rows_per_half(uint32_t rows, uint32_t compute_units) {
-    const uint32_t waves = compute_units * 8;
-    uint32_t rph = rows / (2 * waves);
-    if (rph < 1) rph = 1;
-    if (rph > 32) rph = 32;
-    return rph;
-}
-
 hipError_t launch_gemv(const Product& a, uint32_t format, uint32_t compute_units, hipStream_t stream) {
-    const uint32_t rph = gemv_rows_per_half(a.rows, compute_units);
-    if (format == kQ4_0) return launch_format<kQ4_0>(a, rph, stream);
-    return launch_format<kQ6_K>(a, rph, stream);
+    GemvPlan plan;
+    if (!gemv_plan(a.rows, a.groups, compute_units, &plan)) return hipErrorInvalidValue;
+    if (format == kQ4_0) return launch_format<kQ4_0>(a, plan, compute_units, stream);
+    return launch_format<kQ6_K>(a, plan, compute_units, stream);
 }
 
 }  // namespace chm

@@ -17,6 +17,7 @@ uint64_t layout_bytes(uint32_t format, uint64_t blocks);
 bool lay_out(uint32_t format, const uint8_t* stored, uint64_t blocks, uint8_t* device);
 void repack_q6_k(const uint8_t* stored, uint64_t blocks, uint8_t* lo, uint8_t* hi, uint8_t* scales, uint8_t* d);
 
+bool gemv_supports(uint32_t groups);
 hipError_t launch_gemv(const Product& a, uint32_t format, uint32_t compute_units, hipStream_t stream);
 hipError_t launch_gemm_canonical(const Product& a, uint32_t format, uint32_t compute_units, hipStream_t stream);
 

@@ -42,12 +42,36 @@ struct Product {
     const float* bias;     // device, or null
 };
 
-// The member holding product row p, and p's row within its piece.
-__device__ __forceinline__ int locate(const Product& a, uint32_t p, uint32_t* row) {
-    int m = 0;
-    if (a.members > 1 && p >= a.m[0].first + a.m[0].rows) m = (a.members > 2 && p >= a.m[1].first + a.m[1].rows) ? 2 : 1;
-    *row = a.m[m].row_offset + (p - a.m[m].first);
-    return m;
+// Where product row p's weights lie: its member's piece and p's row within
+// it. Members are compared with constant indices only, so their fields stay
+// in scalar registers (an index into the kernel argument would reload them
+// from memory on every use).
+struct Piece {
+    const uint8_t* piece;
+    uint64_t blocks;
+    uint32_t row;
+};
+
+__device__ __forceinline__ Piece piece_of(const Product& a, uint32_t p) {
+    Piece w{a.m[0].piece, a.m[0].blocks, a.m[0].row_offset + (p - a.m[0].first)};
+    if (a.members > 1 && p >= a.m[1].first) w = {a.m[1].piece, a.m[1].blocks, a.m[1].row_offset + (p - a.m[1].first)};
+    if (a.members > 2 && p >= a.m[2].first) w = {a.m[2].piece, a.m[2].blocks, a.m[2].row_offset + (p - a.m[2].first)};
+    return w;
+}
+
+// Where product row p's output of `token` goes: QKV writes each member's own
+// buffer, `rows` wide; the others write out_row + their row, out_width wide.
+__device__ __forceinline__ float* output_of(const Product& a, uint32_t p, uint32_t token) {
+    float* out = a.m[0].out;
+    uint32_t first = a.m[0].first, at = a.m[0].out_row, width = a.m[0].out_width, rows = a.m[0].rows;
+    if (a.members > 1 && p >= a.m[1].first) {
+        out = a.m[1].out, first = a.m[1].first, at = a.m[1].out_row, width = a.m[1].out_width, rows = a.m[1].rows;
+    }
+    if (a.members > 2 && p >= a.m[2].first) {
+        out = a.m[2].out, first = a.m[2].first, at = a.m[2].out_row, width = a.m[2].out_width, rows = a.m[2].rows;
+    }
+    if (a.epilogue == kQKV) return out + static_cast<uint64_t>(token) * rows + (p - first);
+    return out + static_cast<uint64_t>(token) * width + at + (p - first);
 }
 
 }  // namespace chm

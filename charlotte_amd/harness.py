@@ -39,6 +39,7 @@ _SIGS = {
     "chx_graph_destroy": (_c.c_int, [_c.c_void_p]),
     "chx_unpack": (_c.c_int, [_c.c_uint32, _c.c_void_p, _c.c_uint64, _c.c_uint64, _c.c_void_p, _c.c_void_p]),
     "chx_copy": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
+    "chx_null": (_c.c_int, [_c.c_void_p]),
 }
 
 
@@ -182,3 +183,7 @@ def unpack(gguf_type, piece_ptr, blocks_in_piece, groups, out_ptr, stream=None):
 
 def copy(src_ptr, dst_ptr, nbytes, stream=None):
     check(lib.chx_copy(src_ptr, dst_ptr, nbytes, stream.handle if isinstance(stream, Stream) else stream), "copy")
+
+
+def null(stream=None):
+    check(lib.chx_null(stream.handle if isinstance(stream, Stream) else stream), "null kernel")

@@ -20,7 +20,8 @@ from dataclasses import dataclass, field
 from typing import Optional, Sequence
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIBRARY = os.path.join(HERE, "libcharlotte_hip_matmul.so")
+# CHARLOTTE_HIP_MATMUL_LIBRARY names another build of the same ABI.
+LIBRARY = os.environ.get("CHARLOTTE_HIP_MATMUL_LIBRARY") or os.path.join(HERE, "libcharlotte_hip_matmul.so")
 
 
 class Status(enum.IntEnum):

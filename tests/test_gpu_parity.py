@@ -170,6 +170,26 @@ def test_a_weight_in_pieces_writes_its_rows(oracle, run, source, fixture_tensors
         w.free()
 
 
+@pytest.mark.parametrize("rows", [2, 18, 130])
+def test_q6_k_1152_small_pieces(oracle, run, rows):
+    # K = 1,152 (Gemma 3): rows straddle super-blocks; small pieces put the
+    # last rows' windows against the piece's end.
+    from charlotte_amd import synthetic
+    from tests.support.gpu import bits_equal, first_difference
+
+    rng = np.random.default_rng(rows)
+    stored = synthetic.q6_k(rng, rows, 1152)
+    x = synthetic.activations(rng, 3, 1152)
+    w = run.weight(Q6_K, rows, 1152, stored)
+    for tokens in (1, 3):
+        got = run.write(w, x, tokens)
+        want = oracle.matmul_f32(Q6_K, stored, rows, 1152, x[:tokens])
+        assert bits_equal(got, want), first_difference(got, want)
+    last = run.write(w, x, 3, rows=__import__("charlotte_amd.matmul", fromlist=["Rows"]).Rows.LastToken)
+    assert bits_equal(last[0], oracle.matmul_f32(Q6_K, stored, rows, 1152, x[2:3])[0])
+    w.free()
+
+
 # ---- BASELINE shapes at full size ------------------------------------------
 
 
