@@ -228,6 +228,29 @@ def cpu_baseline_c2(stored, x, rows, columns, seconds=10.0):
                       f"of {t * 1e3:.1f} ms; oracle/liborc.so on {threads} threads"}
 
 
+def run_copy(S, nbytes=256 << 20, reps=5):
+    """A plain device copy of known size: the yardstick the HBM counters
+    (rocprofv3 FETCH_SIZE / WRITE_SIZE) are scaled by."""
+    hx = S.hx
+    a, b = S.buffer(nbytes=nbytes), S.buffer(nbytes=nbytes)
+    for _ in range(reps):
+        hx.copy(a.ptr, b.ptr, nbytes, S.stream)
+    S.stream.sync()
+    log(f"copy: {reps} x {nbytes >> 20} MiB")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel, from the rocprofv3 counter
+    runs recorded in profiles/traffic_c2.json (FETCH_SIZE and WRITE_SIZE in KiB
+    per dispatch, each scaled by what the counter reads for a copy of known
+    size); None when absent."""
+    path = os.path.join(ROOT, "profiles", "traffic_c2.json")
+    if not os.path.exists(path):
+        return None
+    t = json.load(open(path))
+    return int(round((t["fetch_kib"] * t["fetch_scale"] + t["write_kib"] * t["write_scale"]) * 1024))
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -250,6 +273,8 @@ def main():
     c2 = None
     c2_x = None
     try:
+        if "copy" in only:
+            run_copy(S)
         if "c2" in only:
             c2 = run_gemv(S, "c2", 14, 262144, 1152, max(args.steps, 20), args.warmup, np.random.default_rng(2))
             c2_x = c2["x"].read(np.float32)
@@ -281,7 +306,7 @@ def main():
             "config": {"workload": "c2: Q6_K LM-head GEMV y[1,262144] = x[1,1152] W^T (Gemma-3-1B), repacked Q6_K",
                        "rows": 262144, "columns": 1152, "weight_copies": c2["copies"]},
             "roofline": {"bound": "hbm", "achieved": round(c2["GB/s"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(c2["frac"], 4), "traffic": None},
+                         "frac": round(c2["frac"], 4), "traffic": measured_traffic()},
             "cpu_baseline": cpu,
         })
     result["configs"] = out
