@@ -228,9 +228,6 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
                                                         const charlotte_hip_matmul_desc* desc,
                                                         charlotte_hip_matmul_split_gate gate, void* range_sums,
                                                         uint64_t range_sums_bytes, uint32_t tokens, void* stream) {
-    (void)gate;
-    (void)range_sums;
-    (void)range_sums_bytes;
     if (!ctx) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
     if (!desc) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: no descriptor");
     if (tokens == 0) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: a step of no tokens");
@@ -241,11 +238,21 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
         return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: epilogue " + std::to_string(d.epilogue));
     if (d.rows > CHARLOTTE_HIP_MATMUL_LAST_TOKEN)
         return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: rows " + std::to_string(d.rows));
-    if (d.epilogue == CHARLOTTE_HIP_MATMUL_GATED_ACTIVATION || d.epilogue == CHARLOTTE_HIP_MATMUL_GATED_BY_INPUT ||
-        d.clip || d.bias || d.activated)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_UNSUPPORTED, "launch: epilogue or option not built");
-    if (d.epilogue == CHARLOTTE_HIP_MATMUL_WRITE && d.member_count != 1)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: a Write takes one member");
+    if (d.activation > CHARLOTTE_HIP_MATMUL_SIGMOID)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: activation " + std::to_string(d.activation));
+    const bool gated = d.epilogue == CHARLOTTE_HIP_MATMUL_GATED_ACTIVATION;
+    const bool by_input = d.epilogue == CHARLOTTE_HIP_MATMUL_GATED_BY_INPUT;
+    // The options are a Write's; a gated product may be clipped (matmul.h:229-255, 623-629).
+    if ((d.bias || d.activated) && d.epilogue != CHARLOTTE_HIP_MATMUL_WRITE)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: bias and activated are a Write's options");
+    if (d.clip && d.epilogue != CHARLOTTE_HIP_MATMUL_WRITE && !gated)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: clip is a Write's or a gated product's option");
+    if (gated && d.member_count != 2)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: a gated product takes two members, gate and up");
+    if (gated && d.members[0].rows != d.members[1].rows)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: gate and up rows differ");
+    if (by_input && !d.gate_input)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: GatedByInput without its input");
     if (!d.input) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: no input");
     if (reinterpret_cast<uintptr_t>(d.input) % 16 != 0)
         return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: input not 16-byte aligned");
@@ -257,28 +264,34 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
     for (uint32_t i = 0; i < d.member_count; ++i) {
         const charlotte_hip_matmul_member& m = d.members[i];
         if (!m.weight) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member " + std::to_string(i) + " has no weight");
+        if (m.weight->ctx != ctx) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member " + std::to_string(i) + " of another context");
         if (m.weight->type != head->type || m.weight->columns != head->columns)
             return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: members differ in format or width");
         if (m.rows == 0 || m.row_offset + m.rows > m.weight->rows)
             return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member " + std::to_string(i) + " rows past its weight");
         float* out = d.epilogue == CHARLOTTE_HIP_MATMUL_QKV ? d.outputs[i] : d.outputs[0];
         if (!out) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member " + std::to_string(i) + " has no output");
-        const uint64_t width = d.out_width ? d.out_width : 0;
         a.m[i] = chm::Member{m.weight->piece,
                              m.weight->blocks,
                              static_cast<uint32_t>(m.row_offset),
                              static_cast<uint32_t>(m.rows),
                              static_cast<uint32_t>(rows),
                              static_cast<uint32_t>(m.output_row),
-                             static_cast<uint32_t>(width),
+                             static_cast<uint32_t>(d.out_width),
                              0,
                              out};
         rows += m.rows;
     }
-    if (rows > 0x7FFFFFFFull) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: too many rows");
+    if (rows > 0x7FFFFFFFull || d.out_width > 0xFFFFFFFFull)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: too many rows");
+    // A gated product writes its gate's rows a token; the rest, out_width
+    // (0: the product's rows) with each member at its output_row.
+    const uint64_t width = gated ? d.members[0].rows : rows;
     for (uint32_t i = 0; i < d.member_count; ++i) {
-        if (a.m[i].out_width == 0) a.m[i].out_width = static_cast<uint32_t>(rows);
-        if (d.epilogue == CHARLOTTE_HIP_MATMUL_WRITE && a.m[i].out_row + a.m[i].rows > a.m[i].out_width)
+        if (a.m[i].out_width == 0) a.m[i].out_width = static_cast<uint32_t>(width);
+        if (gated && a.m[i].out_width < width)
+            return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: out_width below the gate's rows");
+        if ((d.epilogue == CHARLOTTE_HIP_MATMUL_WRITE || by_input) && a.m[i].out_row + a.m[i].rows > a.m[i].out_width)
             return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: output rows past out_width");
     }
     a.x = d.input;
@@ -289,6 +302,12 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
     a.activation = d.activation;
     a.last_token = d.rows == CHARLOTTE_HIP_MATMUL_LAST_TOKEN;
     a.tokens = tokens;
+    a.gate_stride = d.gate_input_stride;
+    a.gate_column = d.gate_input_column;
+    a.gate_input = d.gate_input;
+    a.clip = d.clip;
+    a.bias = d.bias;
+    a.activated = d.activated ? 1u : 0u;
 
     if (hipError_t e = hipSetDevice(ctx->device); e != hipSuccess) return hip_fail(ctx, e, "launch: hipSetDevice");
     auto* s = static_cast<hipStream_t>(stream);
@@ -300,7 +319,19 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
     if (decode) {
         e = chm::launch_gemv(a, head->type, ctx->compute_units, s);
     } else {
-        e = chm::launch_gemm_canonical(a, head->type, ctx->compute_units, s);
+        // The split form takes the steps the gate allows whose range sums fit
+        // the buffer; a product with options, or gated, never splits
+        // (matmul.cpp:166-172, 233-241).
+        uint64_t split = 1;
+        const bool options = d.clip || d.bias || d.activated;
+        if (!options && !gated && range_sums && range_sums_bytes && gate.denominator) {
+            if (reinterpret_cast<uintptr_t>(range_sums) % 4 != 0)
+                return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: range_sums not 4-byte aligned");
+            const uint64_t fits = range_sums_bytes / 4 / (rows * 32);
+            split = std::min<uint64_t>(charlotte_hip_matmul_split_tokens(d.epilogue, rows, head->columns, gate), fits);
+        }
+        float* sums = tokens <= split ? static_cast<float*>(range_sums) : nullptr;
+        e = chm::launch_gemm_canonical(a, head->type, ctx->compute_units, sums, s);
     }
     if (e != hipSuccess) return hip_fail(ctx, e, "launch");
     return ok(ctx);

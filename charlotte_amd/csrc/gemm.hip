@@ -11,23 +11,35 @@
 // output's order of addition is decode's, whatever BM. Workgroups are
 // numbered token tile first, so the tiles that read one weight tile run
 // together and find it in L2 (matmul.wgsl:480-482).
+//
+// Split along K (matmul.wgsl:592-695): the same tile over a chunk of the 32
+// ranges only, each range sum written to `range_sums` range first,
+// [32][tokens][rows]; the combine adds a row's 32 sums in order from zero.
+// Range sums are the same bits either way, so split and tiled outputs agree.
 #include "product.hpp"
 
 namespace chm {
 
 constexpr int kRowsATile = 128;
 
-__device__ __forceinline__ void store_output(const Product& a, uint32_t token, uint32_t p, float v) {
-    *output_of(a, p, token) = v;
+// Where range r's sum of product row p for `token` lies (matmul.wgsl:603-605).
+__device__ __forceinline__ uint64_t range_sum_at(const Product& a, uint32_t r, uint32_t token, uint32_t p) {
+    return (static_cast<uint64_t>(r) * a.tokens + token) * a.rows + p;
 }
 
-template <uint32_t F, int BM>
-__global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_tiles) {
+// SPLIT: `chunks` workgroups a tile, chunk c taking ranges [32c / chunks,
+// 32(c + 1) / chunks) and writing their sums to `range_sums`; else one a
+// tile, writing the outputs.
+template <uint32_t F, int BM, bool SPLIT, bool FULL>
+__global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_tiles, uint32_t row_tiles,
+                                                      uint32_t chunks, float* range_sums) {
     constexpr int TM = BM / 16;  // a lane's tokens
     __shared__ float4 Ws[32][kRowsATile / 4];
     __shared__ float4 Xs[32][BM / 4];
     const uint32_t t = threadIdx.x, tx = t & 15u, ty = t >> 4;
-    const uint32_t tile_t = blockIdx.x % token_tiles, tile_r = blockIdx.x / token_tiles;
+    const uint32_t tile_t = blockIdx.x % token_tiles, tile_r = (blockIdx.x / token_tiles) % row_tiles;
+    const uint32_t chunk = blockIdx.x / (token_tiles * row_tiles);
+    const uint32_t r_begin = 32 * chunk / chunks, r_end = 32 * (chunk + 1) / chunks;
     const uint32_t m0 = tile_t * BM, n0 = tile_r * kRowsATile;
     const uint32_t G = a.groups, K = G * 32;
 
@@ -50,10 +62,14 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
 #pragma unroll
         for (int j = 0; j < 8; ++j) s[i][j] = tot[i][j] = 0.0f;
 
-    uint32_t next_r = 1;  // the next range boundary, range_lo(next_r)
-    while (next_r < 32 && range_lo(next_r, G) == 0) ++next_r;
+    // The range that ends after group g is the one before `next_r`'s first
+    // group; ranges with no groups hold zero and add nothing to a total, which
+    // is never -0.
+    uint32_t next_r = r_begin + 1;
+    const uint32_t g_begin = range_lo(r_begin, G), g_end = range_lo(r_end, G);
+    while (next_r < r_end && range_lo(next_r, G) <= g_begin) ++next_r;
 
-    for (uint32_t g = 0; g < G; ++g) {
+    for (uint32_t g = g_begin; g < g_end; ++g) {
         __syncthreads();  // the last group's tiles are read
         {
             float w[16];
@@ -81,7 +97,7 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
                 const float4* src = reinterpret_cast<const float4*>(xsrc + g * 32);
 #pragma unroll
                 for (int v = 0; v < XPer / 4; ++v) {
-                    const float4 q = src[v];
+                    const float4 q = clamp_input(a, src[v]);
                     xv[4 * v] = q.x;
                     xv[4 * v + 1] = q.y;
                     xv[4 * v + 2] = q.z;
@@ -117,18 +133,34 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
 #pragma unroll
                 for (int j = 0; j < 8; ++j) s[i][j] = __builtin_fmaf(w[j], x[i], s[i][j]);
         }
-        if (g + 1 == range_lo(next_r, G)) {
+        if (g + 1 == range_lo(next_r, G)) {  // range next_r - 1 ends
+            if constexpr (SPLIT) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+                for (int i = 0; i < TM; ++i) {
+                    const uint32_t token = m0 + 4 * ty + (i & 3) + 64 * (i >> 2);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    tot[i][j] = tot[i][j] + s[i][j];
-                    s[i][j] = 0.0f;
+                    for (int j = 0; j < 8; ++j) {
+                        const uint32_t p = n0 + 4 * tx + (j & 3) + 64 * (j >> 2);
+                        if (token < a.tokens && p < a.rows) range_sums[range_sum_at(a, next_r - 1, token, p)] = s[i][j];
+                        s[i][j] = 0.0f;
+                    }
                 }
-            while (next_r < 32 && range_lo(next_r, G) <= g + 1) ++next_r;
+            } else {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        tot[i][j] = tot[i][j] + s[i][j];
+                        s[i][j] = 0.0f;
+                    }
+            }
+            while (next_r < r_end && range_lo(next_r, G) <= g + 1) ++next_r;
         }
     }
+    if constexpr (SPLIT) return;
 
+    // Rows p, p + 1 of a micro-tile (j, j + 1 for even j) are adjacent, so a
+    // gated product's gate and up totals meet in one lane.
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const uint32_t token = m0 + 4 * ty + (i & 3) + 64 * (i >> 2);
@@ -136,28 +168,64 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint32_t p = n0 + 4 * tx + (j & 3) + 64 * (j >> 2);
-            if (p < a.rows) store_output(a, token, p, tot[i][j]);
+            if (p < a.rows) emit<FULL>(a, p, token, token, tot[i][j], (j & 1) ? 0.0f : tot[i][j ^ 1]);
         }
     }
 }
 
-hipError_t launch_gemm_canonical(const Product& a, uint32_t format, uint32_t compute_units, hipStream_t stream) {
+// The combine (matmul.wgsl:621-695): a lane an output of each token, its 32
+// range sums added in order to a total from zero, then the epilogue. Empty
+// ranges (G < 32) are never written by the split form and add nothing.
+__global__ __launch_bounds__(256) void combine_ranges(Product a, const float* range_sums) {
+    const uint64_t id = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (id >= static_cast<uint64_t>(a.tokens) * a.rows) return;
+    const uint32_t token = static_cast<uint32_t>(id / a.rows), p = static_cast<uint32_t>(id % a.rows);
+    float total = 0.0f;
+    for (uint32_t r = 0; r < 32; ++r)
+        if (range_lo(r, a.groups) < range_lo(r + 1, a.groups)) total = total + range_sums[range_sum_at(a, r, token, p)];
+    emit<true>(a, p, token, token, total, 0.0f);
+}
+
+template <uint32_t F, int BM>
+static void go(const Product& a, uint32_t token_tiles, uint32_t row_tiles, uint32_t chunks, float* range_sums,
+               hipStream_t stream) {
+    const dim3 grid(token_tiles * row_tiles * chunks);
+    if (range_sums)
+        hipLaunchKernelGGL((gemm_canonical<F, BM, true, false>), grid, dim3(256), 0, stream, a, token_tiles, row_tiles,
+                           chunks, range_sums);
+    else if (plain_epilogue(a))
+        hipLaunchKernelGGL((gemm_canonical<F, BM, false, false>), grid, dim3(256), 0, stream, a, token_tiles, row_tiles,
+                           1u, nullptr);
+    else
+        hipLaunchKernelGGL((gemm_canonical<F, BM, false, true>), grid, dim3(256), 0, stream, a, token_tiles, row_tiles,
+                           1u, nullptr);
+}
+
+// The tiled form; with `range_sums` (room for 32 x tokens x rows floats), the
+// split form and its combine, the ranges cut into as few chunks as still give
+// every CU two workgroups.
+hipError_t launch_gemm_canonical(const Product& a, uint32_t format, uint32_t compute_units, float* range_sums,
+                                 hipStream_t stream) {
     const uint32_t row_tiles = (a.rows + kRowsATile - 1) / kRowsATile;
     const bool wide = ((a.tokens + 127) / 128) * row_tiles >= 2 * compute_units;
-    if (wide) {
-        const uint32_t token_tiles = (a.tokens + 127) / 128;
-        const dim3 grid(token_tiles * row_tiles);
-        if (format == kQ4_0)
-            hipLaunchKernelGGL((gemm_canonical<kQ4_0, 128>), grid, dim3(256), 0, stream, a, token_tiles);
-        else
-            hipLaunchKernelGGL((gemm_canonical<kQ6_K, 128>), grid, dim3(256), 0, stream, a, token_tiles);
+    const uint32_t bm = wide ? 128 : 64;
+    const uint32_t token_tiles = (a.tokens + bm - 1) / bm;
+    uint32_t chunks = 1;
+    if (range_sums) {
+        chunks = 2;
+        while (chunks < 32 && token_tiles * row_tiles * chunks < 2 * compute_units) chunks *= 2;
+    }
+    if (format == kQ4_0) {
+        wide ? go<kQ4_0, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
+             : go<kQ4_0, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
     } else {
-        const uint32_t token_tiles = (a.tokens + 63) / 64;
-        const dim3 grid(token_tiles * row_tiles);
-        if (format == kQ4_0)
-            hipLaunchKernelGGL((gemm_canonical<kQ4_0, 64>), grid, dim3(256), 0, stream, a, token_tiles);
-        else
-            hipLaunchKernelGGL((gemm_canonical<kQ6_K, 64>), grid, dim3(256), 0, stream, a, token_tiles);
+        wide ? go<kQ6_K, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
+             : go<kQ6_K, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
+    }
+    if (range_sums) {
+        const uint64_t outputs = static_cast<uint64_t>(a.tokens) * a.rows;
+        hipLaunchKernelGGL(combine_ranges, dim3(static_cast<uint32_t>((outputs + 255) / 256)), dim3(256), 0, stream, a,
+                           range_sums);
     }
     return hipGetLastError();
 }

@@ -50,13 +50,21 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ void write_output(const Product& a, uint32_t p, float total) {
-    *output_of(a, p, 0) = total;
+// The outputs of a wave's rows first .. first + count - 1, lane i holding
+// row first + i's total (first even, so a gated product's gate and up totals
+// are adjacent lanes). Every lane of the wave calls it.
+template <bool FULL>
+__device__ __forceinline__ void finish_rows(const Product& a, uint32_t first, uint32_t count, float total) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t p = first + lane;
+    float partner = 0.0f;
+    if (FULL && a.epilogue == kGated) partner = __shfl_xor(total, 1);
+    if (lane < count && p < a.rows) emit<FULL>(a, p, 0, a.last_token ? a.tokens - 1 : 0, total, partner);
 }
 
 // L = 32: lane r of a half-wave owns range r — at most SPAN groups, its
 // chain from zero over them, and no other range; its range sum goes to LDS.
-template <uint32_t F, int SPAN, bool XREG>
+template <uint32_t F, int SPAN, bool XREG, bool FULL>
 __global__ __launch_bounds__(256, CHM_RANGES_MIN_BLOCKS) void gemv_ranges(Product a, uint32_t steps, uint32_t tiles) {
     __shared__ float partials[kWaves][kWaveRows * kPad];
     extern __shared__ float4 xs4[];  // x, staged when it is not held in registers
@@ -76,7 +84,7 @@ __global__ __launch_bounds__(256, CHM_RANGES_MIN_BLOCKS) void gemv_ranges(Produc
                 const float4* src = reinterpret_cast<const float4*>(x + (g0 + i) * 32);
 #pragma unroll
                 for (int v = 0; v < 8; ++v) {
-                    const float4 q = src[v];
+                    const float4 q = clamp_input(a, src[v]);
                     xr[i * 32 + 4 * v + 0] = q.x;
                     xr[i * 32 + 4 * v + 1] = q.y;
                     xr[i * 32 + 4 * v + 2] = q.z;
@@ -86,7 +94,7 @@ __global__ __launch_bounds__(256, CHM_RANGES_MIN_BLOCKS) void gemv_ranges(Produc
         }
     } else {
         const float4* src = reinterpret_cast<const float4*>(x);
-        for (uint32_t v = threadIdx.x; v < G * 8; v += 256) xs4[v] = src[v];
+        for (uint32_t v = threadIdx.x; v < G * 8; v += 256) xs4[v] = clamp_input(a, src[v]);
         __syncthreads();
     }
 
@@ -140,16 +148,13 @@ __global__ __launch_bounds__(256, CHM_RANGES_MIN_BLOCKS) void gemv_ranges(Produc
             }
         }
         wave_sync();
-        if (lane < steps * 2) {
-            const uint32_t p = wave_first + lane;
-            if (p < a.rows) {
-                const float* sums = mine + lane * kPad;
-                float total = 0.0f;
+        float total = 0.0f;
+        if (lane < steps * 2 && wave_first + lane < a.rows) {
+            const float* sums = mine + lane * kPad;
 #pragma unroll
-                for (int q = 0; q < 32; ++q) total = total + sums[q];
-                write_output(a, p, total);
-            }
+            for (int q = 0; q < 32; ++q) total = total + sums[q];
         }
+        finish_rows<FULL>(a, wave_first, steps * 2, total);
         wave_sync();  // the sums are read before the next tile writes them
     }
 }
@@ -282,7 +287,7 @@ __device__ __forceinline__ uint32_t x_slot(uint32_t v) {
 #define CHM_QUARTERS_PIPELINE 0
 #endif
 
-template <uint32_t F, int SPAN>
+template <uint32_t F, int SPAN, bool FULL>
 __global__ __launch_bounds__(256, CHM_QUARTERS_MIN_BLOCKS) void gemv_quarters(Product a, uint32_t steps, uint32_t tiles) {
     __shared__ float partials[kWaves][kWaveRows * kPad];
     extern __shared__ float4 xs4[];
@@ -295,7 +300,7 @@ __global__ __launch_bounds__(256, CHM_QUARTERS_MIN_BLOCKS) void gemv_quarters(Pr
     const float* x = a.x + static_cast<uint64_t>(token) * G * 32;
     {
         const float4* src = reinterpret_cast<const float4*>(x);
-        for (uint32_t v = threadIdx.x; v < G * 8; v += 256) xs4[x_slot<SPAN>(v)] = src[v];
+        for (uint32_t v = threadIdx.x; v < G * 8; v += 256) xs4[x_slot<SPAN>(v)] = clamp_input(a, src[v]);
     }
     const float4* xl = xs4 + x_slot<SPAN>(8 * g0);
     // Which of the run's groups end a range; the run's first range is 8j.
@@ -353,16 +358,13 @@ __global__ __launch_bounds__(256, CHM_QUARTERS_MIN_BLOCKS) void gemv_quarters(Pr
         if (n % steps == steps - 1) {  // a tile's last step: its rows' totals
             wave_sync();
             const uint32_t tile_first = p - slot;
-            if (lane < steps * 16) {
-                const uint32_t q = tile_first + lane;
-                if (q < a.rows) {
-                    const float* rs = mine + lane * kPad;
-                    float total = 0.0f;
+            float total = 0.0f;
+            if (lane < steps * 16 && tile_first + lane < a.rows) {
+                const float* rs = mine + lane * kPad;
 #pragma unroll
-                    for (int k = 0; k < 32; ++k) total = total + rs[k];
-                    write_output(a, q, total);
-                }
+                for (int k = 0; k < 32; ++k) total = total + rs[k];
             }
+            finish_rows<FULL>(a, tile_first, steps * 16, total);
             wave_sync();
         }
     };
@@ -428,24 +430,32 @@ static uint32_t resident(K kernel, size_t lds) {
 
 // A grid of at most the workgroups the GPU holds at once, each looping over
 // tiles, so no tail round runs part-empty.
-template <uint32_t F, int L, int SPAN, bool XREG>
-static void go(const Product& a, uint32_t steps, uint32_t compute_units, hipStream_t stream) {
+template <uint32_t F, int L, int SPAN, bool XREG, bool FULL>
+static void go_epilogue(const Product& a, uint32_t steps, uint32_t compute_units, hipStream_t stream) {
     const uint32_t rows_a_tile = kWaves * steps * (64 / L);
     const uint32_t tiles = (a.rows + rows_a_tile - 1) / rows_a_tile;
     const size_t lds = XREG ? 0 : (static_cast<size_t>(a.groups) * 32 + (L == 4 ? 16 : 0)) * sizeof(float);
     if constexpr (L == 32) {
         thread_local size_t cached_lds = ~size_t{0};
         thread_local uint32_t per_cu = 1;
-        if (cached_lds != lds) per_cu = resident(gemv_ranges<F, SPAN, XREG>, lds), cached_lds = lds;
+        if (cached_lds != lds) per_cu = resident(gemv_ranges<F, SPAN, XREG, FULL>, lds), cached_lds = lds;
         const dim3 grid(std::min(tiles, per_cu * compute_units));
-        hipLaunchKernelGGL((gemv_ranges<F, SPAN, XREG>), grid, dim3(256), lds, stream, a, steps, tiles);
+        hipLaunchKernelGGL((gemv_ranges<F, SPAN, XREG, FULL>), grid, dim3(256), lds, stream, a, steps, tiles);
     } else {
         thread_local size_t cached_lds = ~size_t{0};
         thread_local uint32_t per_cu = 1;
-        if (cached_lds != lds) per_cu = resident(gemv_quarters<F, SPAN>, lds), cached_lds = lds;
+        if (cached_lds != lds) per_cu = resident(gemv_quarters<F, SPAN, FULL>, lds), cached_lds = lds;
         const dim3 grid(std::min(tiles, per_cu * compute_units));
-        hipLaunchKernelGGL((gemv_quarters<F, SPAN>), grid, dim3(256), lds, stream, a, steps, tiles);
+        hipLaunchKernelGGL((gemv_quarters<F, SPAN, FULL>), grid, dim3(256), lds, stream, a, steps, tiles);
     }
+}
+
+template <uint32_t F, int L, int SPAN, bool XREG>
+static void go(const Product& a, uint32_t steps, uint32_t compute_units, hipStream_t stream) {
+    if (plain_epilogue(a))
+        go_epilogue<F, L, SPAN, XREG, false>(a, steps, compute_units, stream);
+    else
+        go_epilogue<F, L, SPAN, XREG, true>(a, steps, compute_units, stream);
 }
 
 template <uint32_t F>

@@ -19,6 +19,7 @@ void repack_q6_k(const uint8_t* stored, uint64_t blocks, uint8_t* lo, uint8_t* h
 
 bool gemv_supports(uint32_t groups);
 hipError_t launch_gemv(const Product& a, uint32_t format, uint32_t compute_units, hipStream_t stream);
-hipError_t launch_gemm_canonical(const Product& a, uint32_t format, uint32_t compute_units, hipStream_t stream);
+hipError_t launch_gemm_canonical(const Product& a, uint32_t format, uint32_t compute_units, float* range_sums,
+                                 hipStream_t stream);
 
 }  // namespace chm

@@ -364,6 +364,46 @@ float orc_activate(uint32_t activation, float g) {
     return fmaf(half_g, t, half_g);
 }
 
+/* matmul.wgsl:117-132: WGSL's clamp(e, low, high) = min(max(e, low), high),
+ * the input's bounds as it is staged, the output's on each total. */
+static float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
+
+void orc_clamp(const float* x, uint64_t count, float lo, float hi, float* out) {
+    for (uint64_t i = 0; i < count; ++i) out[i] = clampf(x[i], lo, hi);
+}
+
+/* matmul.wgsl:272-284 (finish): a Write's output from its total, clamped to
+ * the output bounds, then the bias of its output row added, then the
+ * activation, in that order. `clip` is in_min, in_max, out_min, out_max or
+ * NULL; `bias` one float an output row or NULL. totals/out [tokens][rows]. */
+void orc_finish(const float* totals, uint64_t tokens, uint64_t rows, const float* clip, const float* bias,
+                int activated, uint32_t activation, float* out) {
+    for (uint64_t t = 0; t < tokens; ++t)
+        for (uint64_t o = 0; o < rows; ++o) {
+            float y = totals[t * rows + o];
+            if (clip) y = clampf(y, clip[2], clip[3]);
+            if (bias) y = y + bias[o];
+            if (activated) y = orc_activate(activation, y);
+            out[t * rows + o] = y;
+        }
+}
+
+/* matmul.wgsl:318-345, 556-573 (decode_gated, prefill_gated): activation of
+ * the clamped gate total times the clamped up total. */
+void orc_gated(const float* gate, const float* up, uint64_t count, const float* clip, uint32_t activation,
+               float* out) {
+    for (uint64_t i = 0; i < count; ++i) {
+        const float g = clip ? clampf(gate[i], clip[2], clip[3]) : gate[i];
+        const float u = clip ? clampf(up[i], clip[2], clip[3]) : up[i];
+        out[i] = orc_activate(activation, g) * u;
+    }
+}
+
+/* matmul.wgsl:347-351 (gated_by_input): the activation of the total times u. */
+void orc_gated_by_input(const float* totals, const float* u, uint64_t count, uint32_t activation, float* out) {
+    for (uint64_t i = 0; i < count; ++i) out[i] = orc_activate(activation, totals[i]) * u[i];
+}
+
 double orc_now(void) {
     struct timespec ts;
     clock_gettime(CLOCK_MONOTONIC, &ts);

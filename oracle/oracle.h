@@ -30,6 +30,12 @@
  *   orc_fill_unit           the hash of tests/gpu/support/fill.h:24-29, pinned
  *                           by its range and by recomputation in numpy.
  *   orc_activate            against math.exp/tanh within its stated bound.
+ *   orc_clamp, orc_finish,
+ *   orc_gated,
+ *   orc_gated_by_input      known answers whose values differ under any other
+ *                           order of clamp, bias and activation, or with the
+ *                           gate and up swapped; SiLU/GELU/sigmoid against
+ *                           math.exp and math.tanh.
  * Nothing here is "parity unpinned".
  */
 #ifndef CHARLOTTE_ORACLE_H
@@ -79,6 +85,17 @@ void orc_fill(uint32_t seed, uint64_t count, float amplitude, float* out);
 /* matmul.wgsl:169-205: 0 SiLU, 1 GELU (tanh form), 2 sigmoid. */
 float orc_exp_nonpositive(float x);
 float orc_activate(uint32_t activation, float g);
+
+/* Epilogues (matmul.wgsl:117-132, 272-351): clamp_input/clamp_output; a
+ * Write's finish (clamp, bias, activation, in order); the gated product
+ * activate(clamp(gate)) * clamp(up); GatedByInput's activate(total) * u.
+ * clip = {in_min, in_max, out_min, out_max} or NULL. */
+void orc_clamp(const float* x, uint64_t count, float lo, float hi, float* out);
+void orc_finish(const float* totals, uint64_t tokens, uint64_t rows, const float* clip, const float* bias,
+                int activated, uint32_t activation, float* out);
+void orc_gated(const float* gate, const float* up, uint64_t count, const float* clip, uint32_t activation,
+               float* out);
+void orc_gated_by_input(const float* totals, const float* u, uint64_t count, uint32_t activation, float* out);
 
 /* Monotonic seconds, for the CPU baseline timing. */
 double orc_now(void);

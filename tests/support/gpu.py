@@ -15,22 +15,38 @@ class Runner:
         return mm.Weight(self.ctx, gtype, rows, columns, stored)
 
     def product(self, members, x, tokens, out_widths, epilogue=mm.Epilogue.Write, rows=mm.Rows.EveryToken,
-                out_width=0, gate=mm.kNever, sums_bytes=0):
-        """Run one product over the first `tokens` rows of x; return each output as [rows_written, width]."""
+                out_width=0, gate=mm.kNever, sums_bytes=0, activation=mm.Activation.SiLU, gate_input=None,
+                gate_input_stride=0, gate_input_column=0, clip=None, bias=None, activated=False):
+        """Run one product over the first `tokens` rows of x; return each output as [rows_written, width].
+
+        gate_input, clip and bias are host arrays, copied to the device for the launch."""
         x = np.ascontiguousarray(x, np.float32)
         xb = hx.Buffer.of(x)
         out_rows = 1 if rows == mm.Rows.LastToken else tokens
         outs = [hx.Buffer(out_rows * w * 4) for w in out_widths]
         for o in outs:
             o.fill(0xFF)  # NaN: an output left unwritten shows
+        extra = {}
+        owned = [xb, *outs]
+        for name, value in (("gate_input", gate_input), ("clip", clip), ("bias", bias)):
+            if value is not None:
+                b = hx.Buffer.of(np.asarray(value, np.float32))
+                extra[name] = b.ptr
+                owned.append(b)
         sums = hx.Buffer(sums_bytes) if sums_bytes else None
-        m = mm.MatmulLaunch(members, xb.ptr, [o.ptr for o in outs], epilogue=epilogue, rows=rows, out_width=out_width)
-        mm.launch(self.ctx, m, tokens, gate, sums.ptr if sums else 0, sums_bytes)
-        hx.sync()
-        got = [o.read(np.float32).reshape(out_rows, w) for o, w in zip(outs, out_widths)]
-        for b in [xb, *outs] + ([sums] if sums else []):
-            b.free()
-        return got
+        if sums:
+            sums.fill(0xFF)
+            owned.append(sums)
+        m = mm.MatmulLaunch(members, xb.ptr, [o.ptr for o in outs], epilogue=epilogue, rows=rows, out_width=out_width,
+                            activation=activation, gate_input_stride=gate_input_stride,
+                            gate_input_column=gate_input_column, activated=activated, **extra)
+        try:
+            mm.launch(self.ctx, m, tokens, gate, sums.ptr if sums else 0, sums_bytes)
+            hx.sync()
+            return [o.read(np.float32).reshape(out_rows, w) for o, w in zip(outs, out_widths)]
+        finally:
+            for b in owned:
+                b.free()
 
     def write(self, w, x, tokens, rows=mm.Rows.EveryToken, **kw):
         return self.product([mm.Member(w)], x, tokens, [w.rows], rows=rows, **kw)[0]

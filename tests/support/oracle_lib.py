@@ -59,6 +59,11 @@ class Oracle:
         lib.orc_activate.restype = ctypes.c_float
         lib.orc_activate.argtypes = [ctypes.c_uint32, ctypes.c_float]
         lib.orc_now.restype = ctypes.c_double
+        lib.orc_clamp.argtypes = [_f32p, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, _f32p]
+        lib.orc_finish.argtypes = [_f32p, ctypes.c_uint64, ctypes.c_uint64, _f32p, _f32p, ctypes.c_int,
+                                   ctypes.c_uint32, _f32p]
+        lib.orc_gated.argtypes = [_f32p, _f32p, ctypes.c_uint64, _f32p, ctypes.c_uint32, _f32p]
+        lib.orc_gated_by_input.argtypes = [_f32p, _f32p, ctypes.c_uint64, ctypes.c_uint32, _f32p]
         self.lib = lib
 
     def fp16_to_fp32(self, h):
@@ -126,6 +131,43 @@ class Oracle:
 
     def exp_nonpositive(self, x):
         return self.lib.orc_exp_nonpositive(x)
+
+    # Epilogues over arrays (matmul.wgsl:117-132, 272-351).
+    @staticmethod
+    def _f32(a):
+        return np.ascontiguousarray(a, np.float32)
+
+    def clamp(self, x, lo, hi):
+        x = self._f32(x)
+        out = np.empty_like(x)
+        self.lib.orc_clamp(_ptr(x, _f32p), x.size, lo, hi, _ptr(out, _f32p))
+        return out
+
+    def finish(self, totals, clip=None, bias=None, activated=False, activation=0):
+        t = self._f32(totals)
+        tokens, rows = t.reshape(-1, t.shape[-1]).shape
+        c = None if clip is None else self._f32(clip)
+        b = None if bias is None else self._f32(bias)
+        out = np.empty_like(t)
+        self.lib.orc_finish(_ptr(t, _f32p), tokens, rows, None if c is None else _ptr(c, _f32p),
+                            None if b is None else _ptr(b, _f32p), int(activated), activation, _ptr(out, _f32p))
+        return out
+
+    def gated(self, gate, up, clip=None, activation=0):
+        g, u = self._f32(gate), self._f32(up)
+        assert g.shape == u.shape
+        c = None if clip is None else self._f32(clip)
+        out = np.empty_like(g)
+        self.lib.orc_gated(_ptr(g, _f32p), _ptr(u, _f32p), g.size, None if c is None else _ptr(c, _f32p),
+                           activation, _ptr(out, _f32p))
+        return out
+
+    def gated_by_input(self, totals, u, activation=0):
+        t, u = self._f32(totals), self._f32(u)
+        assert t.shape == u.shape
+        out = np.empty_like(t)
+        self.lib.orc_gated_by_input(_ptr(t, _f32p), _ptr(u, _f32p), t.size, activation, _ptr(out, _f32p))
+        return out
 
 
 class Reference:

@@ -324,3 +324,60 @@ def test_activations_near_their_definitions(oracle, activation):
         # absolute, a few units of |g| 2^-24, not relative.
         tail = 2.0**-21 * abs(g) if activation == 1 else 0.0
         assert abs(oracle.activate(activation, g) - want) <= 2.0**-16 * abs(want) + tail + 2.0**-30
+
+
+# ---- epilogues (matmul.wgsl:117-132, 272-351) ---------------------------------
+
+
+def _silu(g):
+    return g / (1 + math.exp(-g))
+
+
+def _gelu(g):
+    return 0.5 * g * (1 + math.tanh(math.sqrt(2 / math.pi) * (g + 0.044715 * g**3)))
+
+
+def test_clamp_is_min_of_max(oracle):
+    x = np.array([-5.0, -1.0, -0.5, 0.25, 1.0, 7.0], np.float32)
+    assert oracle.clamp(x, -1.0, 1.0).tolist() == [-1.0, -1.0, -0.5, 0.25, 1.0, 1.0]
+
+
+def test_finish_orders_clamp_then_bias_then_activation(oracle):
+    # total 3 clamped to [-1, 1] is 1; the bias 0.5 makes 1.5; SiLU last. Any
+    # other order gives another value: bias first 3.5 -> 1 -> SiLU(1) = 0.731;
+    # activation before the bias SiLU(1) + 0.5 = 1.231.
+    clip = [-9.0, 9.0, -1.0, 1.0]
+    got = oracle.finish(np.array([[3.0]]), clip=clip, bias=[0.5], activated=True, activation=0)[0, 0]
+    assert got == pytest.approx(_silu(1.5), rel=2e-6)
+    assert abs(got - _silu(1.0)) > 0.4 and abs(got - (_silu(1.0) + 0.5)) > 4e-3
+    # Each option alone, and the bias indexed by output row.
+    t = np.array([[2.0, -3.0, 0.5], [-0.25, 4.0, 1.5]], np.float32)
+    assert (oracle.finish(t) == t).all()
+    assert oracle.finish(t, clip=[0, 0, -1.0, 1.0]).tolist() == [[1.0, -1.0, 0.5], [-0.25, 1.0, 1.0]]
+    assert oracle.finish(t, bias=[1.0, 10.0, 100.0]).tolist() == [[3.0, 7.0, 100.5], [0.75, 14.0, 101.5]]
+    got = oracle.finish(t, activated=True, activation=1)
+    for a, b in zip(got.ravel(), t.ravel()):
+        # GELU's negative tail: absolute error, as in the activation test.
+        assert a == pytest.approx(_gelu(float(b)), rel=1e-5, abs=2.0**-21 * abs(float(b)))
+
+
+def test_gated_is_activated_gate_times_up(oracle):
+    gate = np.array([-3.0, 0.5, 2.0], np.float32)
+    up = np.array([5.0, -4.0, 0.25], np.float32)
+    got = oracle.gated(gate, up, activation=0)
+    for a, g, u in zip(got, gate, up):
+        assert a == pytest.approx(_silu(float(g)) * float(u), rel=2e-6)
+    # Gate and up are not interchangeable: SiLU(5) * -3 is far from SiLU(-3) * 5.
+    assert abs(got[0] - _silu(5.0) * -3.0) > 10
+    # Clipped: both totals clamped to the output bounds before the activation.
+    got = oracle.gated(gate, up, clip=[0, 0, -2.0, 2.0], activation=2)
+    want = [1 / (1 + math.exp(2.0)) * 2.0, 1 / (1 + math.exp(-0.5)) * -2.0, 1 / (1 + math.exp(-2.0)) * 0.25]
+    assert got.tolist() == pytest.approx(want, rel=2e-6)
+
+
+def test_gated_by_input_is_activated_total_times_u(oracle):
+    t = np.array([0.7, -1.25, 3.0], np.float32)
+    u = np.array([2.0, -0.5, 0.125], np.float32)
+    got = oracle.gated_by_input(t, u, activation=1)
+    for a, g, v in zip(got, t, u):
+        assert a == pytest.approx(_gelu(float(g)) * float(v), rel=1e-5, abs=2.0**-21 * abs(float(g * v)))
