@@ -5,9 +5,14 @@
 A step is one pass of the hot path over one batch of synthetic input:
   c1  Q4_0 decode GEMV 3072x1024 (Qwen3-0.6B FFN up)
   c2  Q6_K LM-head GEMV 262144x1152, repacked (Gemma-3-1B)   <- the headline
-  c3  Qwen3-0.6B decode sweep: 28 layers x 7 Q4_0 GEMVs + Q6_K head 151936x1024
+  c3  Qwen3-0.6B decode sweep: 28 layers x 7 Q4_0 GEMVs + Q6_K head 151936x1024,
+      launched as the reference's graph does (QKV and gate/up fused: 113 launches)
+      and unfused (197)
   c4  Q4_0 prefill GEMM M=512, N=8192, K=2048 (Llama-3.2-1B gate/up)
-  c5  Llama-3.2-1B prefill, M=2048, 16 layers x 7 Q4_0 GEMMs + Q6_K head on the last row
+  c5  Llama-3.2-1B prefill, M=2048, 16 layers x 7 Q4_0 GEMMs (fused as c3) + Q6_K
+      head on the last row
+  c4, c5 run on the matrix cores (split-f16, within tolerance) and again on the
+  canonical VALU tile (bit-exact), reported as c4_canonical, c5_canonical.
 Inputs are seeded synthetic data (BASELINE's distributions) resident in HBM
 before timing; a GEMV's weights rotate over copies totalling > 2x the 256 MB
 MALL so every step reads HBM. Each config's launches are captured once in a
@@ -133,31 +138,70 @@ def run_gemv(S, name, gtype, rows, columns, steps, warmup, rng, copies=None):
             "stored": stored, "x": x, "weights": ws}
 
 
-def run_c3(S, steps, warmup, rng):
-    """Qwen3-0.6B decode step: 28 layers x (q, k, v, o, gate, up, down) + Q6_K head."""
+def build_products(S, rng, plan, tokens, gtype=2):
+    """Weights, inputs and outputs for a list of products. plan: (kind, [(rows, columns), ...]) with kind
+    "write" (one member), "qkv" (three members, three outputs) or "gated" (gate, up; one output of their rows).
+    Returns launches, algorithmic GEMV bytes of one pass, flops of one pass at `tokens` tokens."""
     from charlotte_amd import synthetic
 
     mm = S.mm
-    layer = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 1024, 2048), ("gate", 3072, 1024),
-             ("up", 3072, 1024), ("down", 1024, 3072)]
-    t0 = time.time()
-    xs = {c: S.buffer(synthetic.activations(rng, 1, c)) for c in (1024, 2048, 3072)}
-    launches, total = [], 0
-    for _ in range(28):
-        for _n, rows, columns in layer:
-            stored = synthetic.q4_0(rng, rows, columns)
-            w = mm.Weight(S.ctx, 2, rows, columns, stored)
+    widths = sorted({c for _, members in plan for _, c in members})
+    xs = {c: S.buffer(synthetic.activations(rng, tokens, c)) for c in widths}
+    launches, nbytes, flops = [], 0, 0
+    for kind, members in plan:
+        ws = []
+        for rows, columns in members:
+            w = mm.Weight(S.ctx, gtype, rows, columns, synthetic.weight(rng, gtype, rows, columns))
             S.weights.append(w)
-            y = S.buffer(nbytes=4 * rows)
-            launches.append(mm.MatmulLaunch([mm.Member(w)], xs[columns].ptr, [y.ptr]))
-            total += gemv_bytes(2, rows, columns)
-    head_stored = synthetic.q6_k(rng, 151936, 1024)
-    head = mm.Weight(S.ctx, 14, 151936, 1024, head_stored)
+            ws.append(w)
+            nbytes += synthetic.stored_bytes(gtype, rows, columns)
+            flops += 2 * tokens * rows * columns
+        columns = members[0][1]
+        nbytes += 4 * columns
+        if kind == "qkv":
+            outs = [S.buffer(nbytes=4 * r * tokens) for r, _ in members]
+            nbytes += 4 * sum(r for r, _ in members)
+            m = mm.MatmulLaunch([mm.Member(w) for w in ws], xs[columns].ptr, [o.ptr for o in outs],
+                                epilogue=mm.Epilogue.QKV)
+        elif kind == "gated":
+            out = S.buffer(nbytes=4 * members[0][0] * tokens)
+            nbytes += 4 * members[0][0]
+            m = mm.MatmulLaunch([mm.Member(w) for w in ws], xs[columns].ptr, [out.ptr],
+                                epilogue=mm.Epilogue.GatedActivation, activation=mm.Activation.SiLU)
+        else:
+            out = S.buffer(nbytes=4 * members[0][0] * tokens)
+            nbytes += 4 * members[0][0]
+            m = mm.MatmulLaunch([mm.Member(ws[0])], xs[columns].ptr, [out.ptr])
+        launches.append(m)
+    return launches, xs, nbytes, flops
+
+
+def layer_plan(q, kv, hidden, ffn, fused):
+    """One transformer layer's products: q/k/v, o, gate/up, down."""
+    if fused:
+        return [("qkv", [(q, hidden), (kv, hidden), (kv, hidden)]), ("write", [(hidden, q)]),
+                ("gated", [(ffn, hidden), (ffn, hidden)]), ("write", [(hidden, ffn)])]
+    return [("write", [(q, hidden)]), ("write", [(kv, hidden)]), ("write", [(kv, hidden)]), ("write", [(hidden, q)]),
+            ("write", [(ffn, hidden)]), ("write", [(ffn, hidden)]), ("write", [(hidden, ffn)])]
+
+
+def run_c3(S, steps, warmup, rng, fused=True):
+    """Qwen3-0.6B decode step: 28 layers x (q, k, v, o, gate, up, down) + the Q6_K head. Fused as the
+    reference's graph launches them (QKV one product, gate and up one gated product): 113 launches;
+    unfused: 197."""
+    from charlotte_amd import synthetic
+
+    mm = S.mm
+    t0 = time.time()
+    plan = layer_plan(2048, 1024, 1024, 3072, fused) * 28
+    launches, xs, total, _ = build_products(S, rng, plan, 1)
+    head = mm.Weight(S.ctx, 14, 151936, 1024, synthetic.q6_k(rng, 151936, 1024))
     S.weights.append(head)
     yh = S.buffer(nbytes=4 * 151936)
     launches.append(mm.MatmulLaunch([mm.Member(head)], xs[1024].ptr, [yh.ptr]))
     total += gemv_bytes(14, 151936, 1024)
-    log(f"c3: {len(launches)} launches, {total / 1e6:.1f} MB, setup {time.time() - t0:.1f}s")
+    tag = "c3" if fused else "c3_unfused"
+    log(f"{tag}: {len(launches)} launches, {total / 1e6:.1f} MB, setup {time.time() - t0:.1f}s")
 
     def body():
         for m in launches:
@@ -165,26 +209,20 @@ def run_c3(S, steps, warmup, rng):
 
     ms = S.time_graph(body, steps, warmup)
     gbs = total / (ms * 1e-3) / 1e9
-    log(f"c3: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s aggregate, {1e3 / ms:.0f} tokens/s")
+    log(f"{tag}: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s aggregate, {1e3 / ms:.0f} tokens/s")
     return {"ms_per_step": ms, "bytes": total, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "launches": len(launches),
             "tokens_per_s": 1e3 / ms}
 
 
-def run_gemm(S, name, products, tokens, steps, warmup, rng, head=None):
-    """products: list of (rows, columns) Q4_0 weights run over `tokens` tokens."""
+def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None):
+    """plan: products (build_products) over `tokens` tokens, on prefill path `path`."""
     from charlotte_amd import synthetic
 
     mm = S.mm
     t0 = time.time()
-    widths = sorted({c for _, c in products})
-    xs = {c: S.buffer(synthetic.activations(rng, tokens, c)) for c in widths}
-    launches, flops = [], 0
-    for rows, columns in products:
-        w = mm.Weight(S.ctx, 2, rows, columns, synthetic.q4_0(rng, rows, columns))
-        S.weights.append(w)
-        y = S.buffer(nbytes=4 * rows * tokens)
-        launches.append((mm.MatmulLaunch([mm.Member(w)], xs[columns].ptr, [y.ptr]), tokens))
-        flops += 2 * tokens * rows * columns
+    S.ctx.set_gemm_path(path)
+    launches, xs, _, flops = build_products(S, rng, plan, tokens)
+    launches = [(m, tokens) for m in launches]
     head_bytes = 0
     if head is not None:
         rows, columns = head
@@ -193,7 +231,7 @@ def run_gemm(S, name, products, tokens, steps, warmup, rng, head=None):
         y = S.buffer(nbytes=4 * rows)
         launches.append((mm.MatmulLaunch([mm.Member(w)], xs[columns].ptr, [y.ptr], rows=mm.Rows.LastToken), tokens))
         head_bytes = gemv_bytes(14, rows, columns)
-    log(f"{name}: {len(launches)} launches, {flops / 1e9:.1f} GFLOP, setup {time.time() - t0:.1f}s")
+    log(f"{name}: {len(launches)} launches, {flops / 1e9:.1f} GFLOP, path {path.name}, setup {time.time() - t0:.1f}s")
 
     def body():
         for m, t in launches:
@@ -201,8 +239,10 @@ def run_gemm(S, name, products, tokens, steps, warmup, rng, head=None):
 
     ms = S.time_graph(body, steps, warmup)
     tflops = flops / (ms * 1e-3) / 1e12
-    log(f"{name}: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s ({100 * tflops / FP32_PEAK_TFLOPS:.1f}% of FP32 peak)")
-    return {"ms_per_step": ms, "flops": flops, "TFLOP/s": tflops, "frac_fp32": tflops / FP32_PEAK_TFLOPS,
+    log(f"{name}: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s ({100 * tflops / FP32_PEAK_TFLOPS:.1f}% of FP32 peak, "
+        f"{100 * tflops / F16_PEAK_TFLOPS:.1f}% of dense FP16 matrix peak)")
+    return {"ms_per_step": ms, "flops": flops, "TFLOP/s": tflops, "path": path.name,
+            "frac_fp32": tflops / FP32_PEAK_TFLOPS, "frac_f16_matrix": tflops / F16_PEAK_TFLOPS,
             "tokens_per_s": tokens / (ms * 1e-3), "launches": len(launches), "head_gemv_bytes": head_bytes}
 
 
@@ -283,12 +323,20 @@ def main():
             out["c1"] = {k: v for k, v in r.items() if k not in ("stored", "x", "weights")}
         if "c3" in only:
             out["c3"] = run_c3(S, max(args.steps // 4, 3), args.warmup, rng)
+            out["c3_unfused"] = run_c3(S, max(args.steps // 4, 3), args.warmup, rng, fused=False)
+        # Prefill: the matrix cores (split-f16, within tolerance) and the
+        # canonical VALU tile (bit-exact), each on the same shapes.
+        ws = S.buffer(nbytes=S.mm.workspace_bytes(2048, 8192))
+        S.ctx.set_workspace(ws.ptr, ws.nbytes)
+        paths = [("", S.mm.GemmPath.SPLIT_F16_MFMA), ("_canonical", S.mm.GemmPath.CANONICAL)]
         if "c4" in only:
-            out["c4"] = run_gemm(S, "c4", [(8192, 2048)], 512, args.steps, args.warmup, rng)
+            for tag, path in paths:
+                out["c4" + tag] = run_gemm(S, "c4" + tag, [("write", [(8192, 2048)])], 512, args.steps, args.warmup,
+                                           rng, path)
         if "c5" in only:
-            layer = [(2048, 2048), (512, 2048), (512, 2048), (2048, 2048), (8192, 2048), (8192, 2048), (2048, 8192)]
-            out["c5"] = run_gemm(S, "c5", layer * 16, 2048, max(args.steps // 4, 3), args.warmup, rng,
-                                 head=(128256, 2048))
+            for tag, path in paths:
+                out["c5" + tag] = run_gemm(S, "c5" + tag, layer_plan(2048, 512, 2048, 8192, True) * 16, 2048,
+                                           max(args.steps // 4, 3), args.warmup, rng, path, head=(128256, 2048))
     finally:
         S.close()
 

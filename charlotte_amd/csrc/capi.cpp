@@ -21,6 +21,8 @@ struct charlotte_hip_matmul_context {
     int device = 0;
     uint32_t compute_units = 0;
     charlotte_hip_matmul_gemm_path gemm_path = CHARLOTTE_HIP_MATMUL_GEMM_AUTO;
+    void* workspace = nullptr;  // the matrix-core path's, the caller's memory
+    uint64_t workspace_bytes = 0;
     std::string error;
 };
 
@@ -70,6 +72,8 @@ Status check_shape(charlotte_hip_matmul_context* ctx, uint32_t type, uint64_t ro
 
 // kernels_matmul split geometry (matmul.cpp:26-37, 233-250; plan.h:113).
 constexpr uint32_t kTileOutputs = 64, kTileTokens = 32, kPrefillBlock = 512;
+// Under AUTO, steps of fewer tokens stay on the VALU tile.
+constexpr uint32_t kMfmaLeast = 16;
 
 }  // namespace
 
@@ -108,6 +112,21 @@ charlotte_hip_matmul_status charlotte_hip_matmul_set_gemm_path(charlotte_hip_mat
         return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gemm path: " + std::to_string(path));
     ctx->gemm_path = path;
     return ok(ctx);
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_set_workspace(charlotte_hip_matmul_context* ctx, void* device,
+                                                               uint64_t bytes) {
+    if (!ctx) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    if (device && reinterpret_cast<uintptr_t>(device) % 16 != 0)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "workspace: not 16-byte aligned");
+    ctx->workspace = bytes ? device : nullptr;
+    ctx->workspace_bytes = device ? bytes : 0;
+    return ok(ctx);
+}
+
+uint64_t charlotte_hip_matmul_workspace_bytes(uint32_t tokens, uint64_t columns) {
+    if (tokens == 0 || columns == 0 || columns % 32 != 0 || columns / 32 > 0xFFFFFFull) return 0;
+    return chm::mfma_workspace_bytes(tokens, static_cast<uint32_t>(columns / 32));
 }
 
 uint64_t charlotte_hip_matmul_layout_bytes(uint32_t gguf_type, uint64_t rows, uint64_t columns) {
@@ -331,7 +350,17 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
             split = std::min<uint64_t>(charlotte_hip_matmul_split_tokens(d.epilogue, rows, head->columns, gate), fits);
         }
         float* sums = tokens <= split ? static_cast<float*>(range_sums) : nullptr;
-        e = chm::launch_gemm_canonical(a, head->type, ctx->compute_units, sums, s);
+        // The matrix cores: when asked, or under AUTO for a step the split
+        // form does not take, given a workspace that holds the step.
+        const uint64_t need = chm::mfma_workspace_bytes(tokens, a.groups);
+        const bool room = ctx->workspace && ctx->workspace_bytes >= need;
+        const bool mfma = ctx->gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_SPLIT_F16_MFMA ||
+                          (ctx->gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_AUTO && !sums && room && tokens >= kMfmaLeast);
+        if (mfma && !room)
+            return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT,
+                        "launch: the matrix-core path needs a workspace of " + std::to_string(need) + " bytes");
+        e = mfma ? chm::launch_gemm_mfma(a, head->type, ctx->compute_units, ctx->workspace, s)
+                 : chm::launch_gemm_canonical(a, head->type, ctx->compute_units, sums, s);
     }
     if (e != hipSuccess) return hip_fail(ctx, e, "launch");
     return ok(ctx);

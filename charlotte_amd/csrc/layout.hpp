@@ -21,5 +21,8 @@ bool gemv_supports(uint32_t groups);
 hipError_t launch_gemv(const Product& a, uint32_t format, uint32_t compute_units, hipStream_t stream);
 hipError_t launch_gemm_canonical(const Product& a, uint32_t format, uint32_t compute_units, float* range_sums,
                                  hipStream_t stream);
+uint64_t mfma_workspace_bytes(uint32_t tokens, uint32_t groups);
+hipError_t launch_gemm_mfma(const Product& a, uint32_t format, uint32_t compute_units, void* workspace,
+                            hipStream_t stream);
 
 }  // namespace chm

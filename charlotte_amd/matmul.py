@@ -125,6 +125,8 @@ SIGNATURES = {
     "charlotte_hip_matmul_context_destroy": (_c.c_int, [_c.c_void_p]),
     "charlotte_hip_matmul_last_error": (_c.c_char_p, [_c.c_void_p]),
     "charlotte_hip_matmul_set_gemm_path": (_c.c_int, [_c.c_void_p, _c.c_int]),
+    "charlotte_hip_matmul_set_workspace": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_uint64]),
+    "charlotte_hip_matmul_workspace_bytes": (_c.c_uint64, [_c.c_uint32, _c.c_uint64]),
     "charlotte_hip_matmul_layout_bytes": (_c.c_uint64, [_c.c_uint32, _c.c_uint64, _c.c_uint64]),
     "charlotte_hip_matmul_lay_out": (_c.c_int, [_c.c_uint32, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
     "charlotte_hip_matmul_repack_q6_k": (_c.c_int, [_c.c_void_p, _c.c_uint64, _c.POINTER(_c.c_void_p)]),
@@ -173,6 +175,10 @@ def range_sum_floats(epilogue, rows, columns, gate: SplitGate):
     return lib.charlotte_hip_matmul_range_sum_floats(int(epilogue), rows, columns, _gate(gate))
 
 
+def workspace_bytes(tokens, columns):
+    return lib.charlotte_hip_matmul_workspace_bytes(tokens, columns)
+
+
 def layout_bytes(gguf_type, rows, columns):
     return lib.charlotte_hip_matmul_layout_bytes(int(gguf_type), rows, columns)
 
@@ -217,6 +223,10 @@ class Context:
 
     def set_gemm_path(self, path: GemmPath):
         self.check(lib.charlotte_hip_matmul_set_gemm_path(self.handle, int(path)))
+
+    def set_workspace(self, device_ptr, nbytes):
+        """The matrix-core path's working memory (device pointer, bytes); 0, 0 unsets it."""
+        self.check(lib.charlotte_hip_matmul_set_workspace(self.handle, device_ptr or None, nbytes))
 
     def close(self):
         if self.handle:

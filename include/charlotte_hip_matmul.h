@@ -97,7 +97,7 @@ typedef enum {
  * batch-invariant; SPLIT_F16_MFMA runs the products on the matrix cores with
  * x split into two f16 parts, within the tolerance max|err| / max|y| <= 1e-5
  * but not bit-exact; AUTO takes the matrix cores where a shape is built for
- * them. */
+ * them and the context has a workspace that holds the step (below). */
 typedef enum {
     CHARLOTTE_HIP_MATMUL_GEMM_AUTO = 0,
     CHARLOTTE_HIP_MATMUL_GEMM_CANONICAL = 1,
@@ -115,6 +115,19 @@ charlotte_hip_matmul_status charlotte_hip_matmul_context_destroy(charlotte_hip_m
 const char* charlotte_hip_matmul_last_error(const charlotte_hip_matmul_context* ctx);
 charlotte_hip_matmul_status charlotte_hip_matmul_set_gemm_path(charlotte_hip_matmul_context* ctx,
                                                                charlotte_hip_matmul_gemm_path path);
+
+/* The matrix-core prefill's working memory (no counterpart in the reference,
+ * whose one prefill kernel needs none): the step's input split into two
+ * binary16 parts, 4 bytes a weight column a token plus a scale a token,
+ * tokens rounded up to 64. The caller allocates it and owns it; launches on
+ * the context use it until it is set again (NULL, 0 unsets it), so steps that
+ * use it must be ordered on one stream. AUTO takes the matrix cores only for
+ * a step it holds. */
+charlotte_hip_matmul_status charlotte_hip_matmul_set_workspace(charlotte_hip_matmul_context* ctx, void* device,
+                                                               uint64_t bytes);
+/* Bytes the workspace needs for a step of `tokens` tokens of K = `columns`;
+ * 0 when columns are not whole 32-weight groups. */
+uint64_t charlotte_hip_matmul_workspace_bytes(uint32_t tokens, uint64_t columns);
 
 /* ---- device layout (host only; no device needed) ---------------------------- */
 
