@@ -24,7 +24,7 @@
 // input as the A operand, so a lane's four outputs are four tokens of one
 // weight row and need one scale. A workgroup's four waves share its tokens:
 // their split input is staged once through LDS; each wave's codes go from the
-// piece straight into registers. Both are loaded four groups ahead.
+// piece straight into registers. Both are loaded a batch of groups ahead.
 #include <type_traits>
 
 #include "decode.hpp"
@@ -38,6 +38,7 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kTokenPad = 64;  // prepared tokens: a multiple of the widest wave tile
+constexpr int kBatch = 4;          // groups a batch of the matrix-core loop
 
 uint64_t mfma_padded_tokens(uint32_t tokens) { return (uint64_t{tokens} + kTokenPad - 1) / kTokenPad * kTokenPad; }
 
@@ -136,21 +137,194 @@ __device__ __forceinline__ Codes<F> load_codes(const RowAt& w, uint32_t g, uint3
     return c;
 }
 
+// A wave's codes for one batch of kBatch groups, as loaded.
+//   Q4_0: lane (c, q) loads group b kBatch + q of its row whole (16 bytes;
+//   the row's four groups are 64 contiguous bytes) and the four groups'
+//   scales (8 bytes, when the row's first group is a multiple of 4, else one
+//   load a group); a 4 x 4 transpose across the lane quarters (two
+//   v_permlane32_swap, two v_permlane16_swap) then gives lane (c, q) code
+//   dword q of each of the four groups — what group_product takes. One 16-byte
+//   and one 8-byte load a row block a batch instead of eight narrow ones.
+//   Q6_K: group by group, as load_codes reads them.
+template <uint32_t F, int R>
+struct Batch;
+
+template <int R>
+struct Batch<kQ4_0, R> {
+    u32x4_t raw[R];
+    uint32_t sc[R][2];
+    __device__ __forceinline__ void load(const RowAt (&rows)[R], uint32_t b, uint32_t G, uint32_t q, bool aligned) {
+        const uint32_t first = b * kBatch;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint64_t gi = rows[r].gi0 + min(first + q, G - 1);
+            raw[r] = *reinterpret_cast<const u32x4_t*>(rows[r].piece + 16 * gi);
+            const uint16_t* scales = reinterpret_cast<const uint16_t*>(rows[r].piece + 16 * rows[r].blocks);
+            if (aligned) {
+                const uint2 two = *reinterpret_cast<const uint2*>(scales + rows[r].gi0 + first);
+                sc[r][0] = two.x;
+                sc[r][1] = two.y;
+            } else {
+                const uint64_t g0 = rows[r].gi0;
+                const uint32_t d0 = scales[g0 + min(first, G - 1)], d1 = scales[g0 + min(first + 1, G - 1)];
+                const uint32_t d2 = scales[g0 + min(first + 2, G - 1)], d3 = scales[g0 + min(first + 3, G - 1)];
+                sc[r][0] = d0 | (d1 << 16);
+                sc[r][1] = d2 | (d3 << 16);
+            }
+        }
+    }
+    __device__ __forceinline__ void codes(Codes<kQ4_0> (&wc)[kBatch][R]) const {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            uint32_t v0 = raw[r][0], v1 = raw[r][1], v2 = raw[r][2], v3 = raw[r][3];
+            const auto s02 = __builtin_amdgcn_permlane32_swap(v0, v2, false, false);
+            const auto s13 = __builtin_amdgcn_permlane32_swap(v1, v3, false, false);
+            v0 = s02[0], v2 = s02[1], v1 = s13[0], v3 = s13[1];
+            const auto s01 = __builtin_amdgcn_permlane16_swap(v0, v1, false, false);
+            const auto s23 = __builtin_amdgcn_permlane16_swap(v2, v3, false, false);
+            wc[0][r].code = s01[0], wc[1][r].code = s01[1], wc[2][r].code = s23[0], wc[3][r].code = s23[1];
+            wc[0][r].d = sc[r][0] & 0xFFFFu, wc[1][r].d = sc[r][0] >> 16;
+            wc[2][r].d = sc[r][1] & 0xFFFFu, wc[3][r].d = sc[r][1] >> 16;
+        }
+    }
+};
+
+template <int R>
+struct Batch<kQ6_K, R> {
+    Codes<kQ6_K> c[kBatch][R];
+    __device__ __forceinline__ void load(const RowAt (&rows)[R], uint32_t b, uint32_t G, uint32_t q, bool) {
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+#pragma unroll
+            for (int r = 0; r < R; ++r) c[j][r] = load_codes<kQ6_K>(rows[r], min(b * kBatch + j, G - 1), q);
+    }
+    __device__ __forceinline__ void codes(Codes<kQ6_K> (&wc)[kBatch][R]) const {
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+#pragma unroll
+            for (int r = 0; r < R; ++r) wc[j][r] = c[j][r];
+    }
+};
+
 __device__ __forceinline__ half2_t lift_less(uint32_t codes, uint32_t selector, _Float16 bias) {
     half2_t v = lift(codes, selector);
     const half2_t b = {bias, bias};
     return v - b;  // (1024 + q) - (1024 + bias) = q - bias, exact in binary16
 }
 
+// One group's products for a wave: the codes of its R row blocks (decoded
+// here to binary16) against the T token blocks' split input, each block's
+// P = codes . hi + codes . lo scaled into its totals.
+// A row block's products are issued hi parts first, then lo parts, then the
+// scales: a block's lo multiply accumulates onto its hi result, and its scale
+// waits for the lo, so the T blocks' independent multiplies sit between them.
+template <uint32_t F, int R, int T>
+__device__ __forceinline__ void group_product(float4_t (&tot)[R][T], const half8_t (&xh)[T], const half8_t (&xl)[T],
+                                              const Codes<F> (&cw)[R], uint32_t q) {
+    const float4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (F == kQ4_0) {
+        half8_t b[R];
+        float s[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t lo = cw[r].code & 0x0F0F0F0Fu, hi = (cw[r].code >> 4) & 0x0F0F0F0Fu;
+            const half2_t b0 = lift_less(lo, kLowPair, 1032.0f16), b1 = lift_less(lo, kHighPair, 1032.0f16);
+            const half2_t b2 = lift_less(hi, kLowPair, 1032.0f16), b3 = lift_less(hi, kHighPair, 1032.0f16);
+            b[r] = half8_t{b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
+            s[r] = half_to_float(cw[r].d);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float4_t p[T];
+#pragma unroll
+            for (int t = 0; t < T; ++t) p[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[t], b[r], z, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < T; ++t) p[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[t], b[r], p[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) tot[r][t][k] = __builtin_fmaf(s[r], p[t][k], tot[r][t][k]);
+        }
+    } else {
+        // Codes of weights 4q .. 4q+3 (half 0) and 16+4q .. 16+4q+3 (half
+        // 1): low nibbles from lo, high pairs from hi.
+        half4_t b0[R], b1[R];
+        float s0[R], s1[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t up = q >> 1;
+            const uint32_t h0 = (cw[r].hi >> (2 * up)) & 0x03030303u;
+            const uint32_t h1 = (cw[r].hi >> (2 * (2 + up))) & 0x03030303u;
+            const uint32_t c0 = (cw[r].lo & 0x0F0F0F0Fu) | (h0 << 4);
+            const uint32_t c1 = ((cw[r].lo >> 4) & 0x0F0F0F0Fu) | (h1 << 4);
+            const half2_t a0 = lift_less(c0, kLowPair, 1056.0f16), a1 = lift_less(c0, kHighPair, 1056.0f16);
+            const half2_t a2 = lift_less(c1, kLowPair, 1056.0f16), a3 = lift_less(c1, kHighPair, 1056.0f16);
+            b0[r] = half4_t{a0.x, a0.y, a1.x, a1.y};
+            b1[r] = half4_t{a2.x, a2.y, a3.x, a3.y};
+            const float d = half_to_float(cw[r].d);
+            s0[r] = d * static_cast<float>(static_cast<int8_t>(cw[r].sc & 0xFFu));
+            s1[r] = d * static_cast<float>(static_cast<int8_t>((cw[r].sc >> 8) & 0xFFu));
+        }
+        float4_t p0[R][T], p1[R][T];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const half4_t h0x = {xh[t][0], xh[t][1], xh[t][2], xh[t][3]};
+                const half4_t h1x = {xh[t][4], xh[t][5], xh[t][6], xh[t][7]};
+                p0[r][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(h0x, b0[r], z, 0, 0, 0);
+                p1[r][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(h1x, b1[r], z, 0, 0, 0);
+            }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const half4_t l0x = {xl[t][0], xl[t][1], xl[t][2], xl[t][3]};
+                const half4_t l1x = {xl[t][4], xl[t][5], xl[t][6], xl[t][7]};
+                p0[r][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(l0x, b0[r], p0[r][t], 0, 0, 0);
+                p1[r][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(l1x, b1[r], p1[r][t], 0, 0, 0);
+            }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    tot[r][t][k] = __builtin_fmaf(s0[r], p0[r][t][k], tot[r][t][k]);
+                    tot[r][t][k] = __builtin_fmaf(s1[r], p1[r][t][k], tot[r][t][k]);
+                }
+    }
+}
+
 // A workgroup's four waves share its T x 16 tokens and take R x 16 rows
-// each. The tokens' split input moves through LDS, two buffers of one group
-// each: a group's 128 bytes a token are loaded into registers kDepth groups
-// ahead (all 256 lanes, 16 bytes each), written to the buffer the group after
-// next will not need, and read back as A operands. Each wave loads its rows'
-// codes into registers kDepth groups ahead too. 16-byte chunk k of token t
-// sits at chunk k ^ (t & 7), so the 16 tokens a read takes spread over the
-// banks.
-constexpr int kDepth = 4;
+// each, and walk K a batch of kBatch groups at a time. The tokens' split
+// input goes through LDS, two batch buffers: while a batch is multiplied out
+// of one, the next batch's input is loaded into registers (all 256 lanes, 16
+// bytes a chunk) and written into the other at the batch's end. Each wave's
+// codes for the next batch are loaded into registers alongside. So every
+// load has a whole batch of products to arrive in, and a workgroup meets at
+// one barrier a batch. 16-byte chunk k of token t sits at chunk k ^ (t & 7),
+// spreading the 16 tokens a read takes over the banks.
+#ifndef CHM_MFMA_SWIZZLE
+#define CHM_MFMA_SWIZZLE 1
+#endif
+#ifndef CHM_MFMA_PREFETCH_A
+#define CHM_MFMA_PREFETCH_A 0
+#endif
+#ifndef CHM_MFMA_W_AHEAD
+#define CHM_MFMA_W_AHEAD 1
+#endif
+#ifndef CHM_MFMA_WAVES_A_SIMD
+#define CHM_MFMA_WAVES_A_SIMD 2
+#endif
+
+// The chunk a token's 16-byte chunk k sits at. With 64 banks (256 bytes a
+// bank row), tokens t and t ^ 1 share a row, and t and t + 8 would collide
+// under k ^ (t & 7); k ^ ((t >> 1) & 7) spreads the 16 tokens of a read over
+// all 16 chunk positions of a bank row.
+__device__ __forceinline__ uint32_t swizzle(uint32_t t, uint32_t k) {
+    return CHM_MFMA_SWIZZLE ? k ^ ((t >> 1) & 7u) : k ^ (t & 7u);
+}
 
 template <uint32_t F, int R, int T, bool FULL>
 __global__ __launch_bounds__(256, 2) void gemm_mfma(Product a, const uint8_t* __restrict__ xp,
@@ -158,12 +332,13 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma(Product a, const uint8_t* __
                                                    uint32_t padded_tokens) {
     constexpr int BM = T * 16;
     constexpr int XC = BM * 8 / 256;  // 16-byte chunks a lane stages a group
-    __shared__ u32x4_t xs[2][BM * 8];
+    __shared__ u32x4_t xs[2][kBatch][BM * 8];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t q = lane >> 4, c = lane & 15u;
     const uint32_t tile_t = blockIdx.x % token_tiles, tile_r = blockIdx.x / token_tiles;
     const uint32_t tok0 = tile_t * BM, row0 = (tile_r * 4 + wave) * R * 16;
     const uint32_t G = a.groups;
+    const uint32_t batches = (G + kBatch - 1) / kBatch;
 
     RowAt rows[R];
 #pragma unroll
@@ -180,15 +355,24 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma(Product a, const uint8_t* __
 #pragma unroll
     for (int i = 0; i < XC; ++i) {
         const uint32_t j = threadIdx.x + 256 * i, t = j >> 3;
-        slot[i] = t * 8 + ((j & 7u) ^ (t & 7u));
+        slot[i] = t * 8 + swizzle(t, j & 7u);
     }
-    auto load_x = [&](u32x4_t (&v)[XC], uint32_t g) {
+    // A batch's loads: groups past the last read the last (unused).
+    const bool aligned = (G & 3u) == 0;
+    // A batch's input loads: groups past the last read the last (unused).
+    auto load_x = [&](uint32_t b, u32x4_t (&xr)[kBatch][XC]) {
 #pragma unroll
-        for (int i = 0; i < XC; ++i) v[i] = xsrc[g * group_chunks + threadIdx.x + 256 * i];
+        for (int j = 0; j < kBatch; ++j) {
+            const uint32_t g = min(b * kBatch + j, G - 1);
+#pragma unroll
+            for (int i = 0; i < XC; ++i) xr[j][i] = xsrc[g * group_chunks + threadIdx.x + 256 * i];
+        }
     };
-    auto store_x = [&](const u32x4_t (&v)[XC], uint32_t buf) {
+    auto store = [&](uint32_t buf, const u32x4_t (&xr)[kBatch][XC]) {
 #pragma unroll
-        for (int i = 0; i < XC; ++i) xs[buf][slot[i]] = v[i];
+        for (int j = 0; j < kBatch; ++j)
+#pragma unroll
+            for (int i = 0; i < XC; ++i) xs[buf][j][slot[i]] = xr[j][i];
     };
 
     float4_t tot[R][T];
@@ -197,98 +381,59 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma(Product a, const uint8_t* __
 #pragma unroll
         for (int t = 0; t < T; ++t) tot[r][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    u32x4_t xr[kDepth][XC];
-    Codes<F> wr[kDepth][R];
+    // Batch b: its input in LDS buffer b & 1, its codes in `wc`; the next
+    // batch's loads go to `xr` and `wn`.
+    u32x4_t xr[kBatch][XC];
+    // The codes go CHM_MFMA_W_AHEAD batches ahead (they come from HBM; the
+    // input, from L2): three buffers in turn.
+    Batch<F, R> w0, w1, w2;
+    auto batch = [&](uint32_t b, const Batch<F, R>& wcur, Batch<F, R>& wahead) {
+        __syncthreads();  // buffer b & 1 is written; buffer (b + 1) & 1 is read no more
+        const bool more = b + 1 < batches;
+        if (more) load_x(b + 1, xr);
+        if (b + CHM_MFMA_W_AHEAD < batches) wahead.load(rows, b + CHM_MFMA_W_AHEAD, G, q, aligned);
+        Codes<F> wc[kBatch][R];
+        wcur.codes(wc);
+        const u32x4_t* buf = xs[b & 1u][0];
+        // A operands of group j of the batch; with CHM_MFMA_PREFETCH_A, group
+        // j + 1's are read before group j's products.
+        half8_t ah[2][T], al[2][T];
+        auto read = [&](int j, half8_t (&xh)[T], half8_t (&xl)[T]) {
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-        const uint32_t g = d < G ? d : G - 1;
-        load_x(xr[d], g);
-#pragma unroll
-        for (int r = 0; r < R; ++r) wr[d][r] = load_codes<F>(rows[r], g, q);
-    }
-    store_x(xr[0], 0);
-
-    // One group's step; d = g % kDepth names the register slots at compile
-    // time, so they stay registers.
-    auto step = [&](uint32_t g0, auto slot_d) {
-        constexpr int d = decltype(slot_d)::value;
-        {
-            const uint32_t g = g0 + d;
-            __syncthreads();  // buffer g & 1 is written; buffer (g + 1) & 1 is read no more
-            if (g + 1 < G) store_x(xr[(d + 1) % kDepth], (g + 1) & 1u);
-            const uint32_t ahead = g + kDepth < G ? g + kDepth : G - 1;
-            load_x(xr[d], ahead);
-            if (g < G) {
-                const u32x4_t* buf = xs[g & 1u];
-                half8_t xh[T], xl[T];
-#pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    const uint32_t tok = 16 * t + c;
-                    xh[t] = __builtin_bit_cast(half8_t, buf[tok * 8 + ((2 * q) ^ (tok & 7u))]);
-                    xl[t] = __builtin_bit_cast(half8_t, buf[tok * 8 + ((2 * q + 1) ^ (tok & 7u))]);
-                }
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const Codes<F>& cw = wr[d][r];
-                    if constexpr (F == kQ4_0) {
-                        const uint32_t lo = cw.code & 0x0F0F0F0Fu, hi = (cw.code >> 4) & 0x0F0F0F0Fu;
-                        const half2_t b0 = lift_less(lo, kLowPair, 1032.0f16), b1 = lift_less(lo, kHighPair, 1032.0f16);
-                        const half2_t b2 = lift_less(hi, kLowPair, 1032.0f16), b3 = lift_less(hi, kHighPair, 1032.0f16);
-                        const half8_t b = {b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
-                        const float s = half_to_float(cw.d);
-#pragma unroll
-                        for (int t = 0; t < T; ++t) {
-                            float4_t p = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[t], b, float4_t{0.0f, 0.0f, 0.0f, 0.0f},
-                                                                                0, 0, 0);
-                            p = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[t], b, p, 0, 0, 0);
-#pragma unroll
-                            for (int k = 0; k < 4; ++k) tot[r][t][k] = __builtin_fmaf(s, p[k], tot[r][t][k]);
-                        }
-                    } else {
-                        // Codes of weights 4q .. 4q+3 (half 0) and 16+4q .. 16+4q+3
-                        // (half 1): low nibbles from lo, high pairs from hi.
-                        const uint32_t up = q >> 1;
-                        const uint32_t h0 = (cw.hi >> (2 * up)) & 0x03030303u;
-                        const uint32_t h1 = (cw.hi >> (2 * (2 + up))) & 0x03030303u;
-                        const uint32_t c0 = (cw.lo & 0x0F0F0F0Fu) | (h0 << 4);
-                        const uint32_t c1 = ((cw.lo >> 4) & 0x0F0F0F0Fu) | (h1 << 4);
-                        const half2_t a0 = lift_less(c0, kLowPair, 1056.0f16), a1 = lift_less(c0, kHighPair, 1056.0f16);
-                        const half2_t a2 = lift_less(c1, kLowPair, 1056.0f16), a3 = lift_less(c1, kHighPair, 1056.0f16);
-                        const half4_t b0 = {a0.x, a0.y, a1.x, a1.y}, b1 = {a2.x, a2.y, a3.x, a3.y};
-                        const float dd = half_to_float(cw.d);
-                        const float s0 = dd * static_cast<float>(static_cast<int8_t>(cw.sc & 0xFFu));
-                        const float s1 = dd * static_cast<float>(static_cast<int8_t>((cw.sc >> 8) & 0xFFu));
-#pragma unroll
-                        for (int t = 0; t < T; ++t) {
-                            const half4_t h0x = {xh[t][0], xh[t][1], xh[t][2], xh[t][3]};
-                            const half4_t l0x = {xl[t][0], xl[t][1], xl[t][2], xl[t][3]};
-                            const half4_t h1x = {xh[t][4], xh[t][5], xh[t][6], xh[t][7]};
-                            const half4_t l1x = {xl[t][4], xl[t][5], xl[t][6], xl[t][7]};
-                            const float4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
-                            float4_t p0 = __builtin_amdgcn_mfma_f32_16x16x16f16(h0x, b0, z, 0, 0, 0);
-                            float4_t p1 = __builtin_amdgcn_mfma_f32_16x16x16f16(h1x, b1, z, 0, 0, 0);
-                            p0 = __builtin_amdgcn_mfma_f32_16x16x16f16(l0x, b0, p0, 0, 0, 0);
-                            p1 = __builtin_amdgcn_mfma_f32_16x16x16f16(l1x, b1, p1, 0, 0, 0);
-#pragma unroll
-                            for (int k = 0; k < 4; ++k) {
-                                tot[r][t][k] = __builtin_fmaf(s0, p0[k], tot[r][t][k]);
-                                tot[r][t][k] = __builtin_fmaf(s1, p1[k], tot[r][t][k]);
-                            }
-                        }
-                    }
-                }
+            for (int t = 0; t < T; ++t) {
+                const uint32_t tok = 16 * t + c;
+                xh[t] = __builtin_bit_cast(half8_t, buf[j * BM * 8 + tok * 8 + swizzle(tok, 2 * q)]);
+                xl[t] = __builtin_bit_cast(half8_t, buf[j * BM * 8 + tok * 8 + swizzle(tok, 2 * q + 1)]);
             }
+        };
+        if (CHM_MFMA_PREFETCH_A) read(0, ah[0], al[0]);
 #pragma unroll
-            for (int r = 0; r < R; ++r) wr[d][r] = load_codes<F>(rows[r], ahead, q);
+        for (int j = 0; j < kBatch; ++j) {
+            if (CHM_MFMA_PREFETCH_A) {
+                if (j + 1 < kBatch) read(j + 1, ah[(j + 1) & 1], al[(j + 1) & 1]);
+            } else {
+                read(j, ah[j & 1], al[j & 1]);
+            }
+            if (b * kBatch + j < G) group_product<F, R, T>(tot, ah[j & 1], al[j & 1], wc[j], q);
         }
+        if (more) store((b + 1) & 1u, xr);
     };
-    for (uint32_t g0 = 0; g0 < G; g0 += kDepth) {
-        step(g0, std::integral_constant<int, 0>{});
-        step(g0, std::integral_constant<int, 1>{});
-        step(g0, std::integral_constant<int, 2>{});
-        step(g0, std::integral_constant<int, 3>{});
+    load_x(0, xr);
+    w0.load(rows, 0, G, q, aligned);
+    if (CHM_MFMA_W_AHEAD == 2) w1.load(rows, 1 < batches ? 1 : 0, G, q, aligned);
+    store(0, xr);
+    if constexpr (CHM_MFMA_W_AHEAD == 2) {
+        for (uint32_t b = 0; b < batches; b += 3) {
+            batch(b, w0, w2);
+            if (b + 1 < batches) batch(b + 1, w1, w0);
+            if (b + 2 < batches) batch(b + 2, w2, w1);
+        }
+    } else {
+        for (uint32_t b = 0; b < batches; b += 2) {
+            batch(b, w0, w1);
+            if (b + 1 < batches) batch(b + 1, w1, w0);
+        }
     }
-    static_assert(kDepth == 4, "one step call a slot");
 
     // Lane (c, q) holds tokens 4q .. 4q+3 of each token block for row c of
     // each row block; rows c and c ^ 1 (a gated product's gate and up) are
@@ -331,7 +476,7 @@ static void launch_format(const Product& a, const uint8_t* xp, const float* inv,
     const auto waves = [&](int r, int t) {
         return uint64_t{(a.tokens + 16u * t - 1) / (16u * t)} * ((a.rows + 16u * r - 1) / (16u * r));
     };
-    const uint64_t want = uint64_t{compute_units} * 8;
+    const uint64_t want = uint64_t{compute_units} * 4 * CHM_MFMA_WAVES_A_SIMD;
     if constexpr (F == kQ4_0) {
         if (waves(4, 4) >= want) return go<F, 4, 4>(a, xp, inv, stream);
     }
