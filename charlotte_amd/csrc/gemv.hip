@@ -25,6 +25,9 @@
 
 namespace chm {
 
+bool gemv_stream_takes(const Product& a, uint32_t format);
+hipError_t launch_gemv_stream(const Product& a, uint32_t compute_units, hipStream_t stream);
+
 // Workgroups a CU is asked to hold at once, as launch bounds: the L = 32
 // kernel's registers allow 4 waves a SIMD at SPAN <= 2 as it stands; the L = 4
 // Q6_K kernel holds a 9-group run (65 registers) and spills past 128.
@@ -476,7 +479,12 @@ static hipError_t launch_format(const Product& a, const GemvPlan& plan, uint32_t
     return hipGetLastError();
 }
 
+#ifndef CHM_GEMV_STREAM
+#define CHM_GEMV_STREAM 1
+#endif
+
 hipError_t launch_gemv(const Product& a, uint32_t format, uint32_t compute_units, hipStream_t stream) {
+    if (CHM_GEMV_STREAM && gemv_stream_takes(a, format)) return launch_gemv_stream(a, compute_units, stream);
     GemvPlan plan;
     if (!gemv_plan(a.rows, a.groups, compute_units, &plan)) return hipErrorInvalidValue;
     if (format == kQ4_0) return launch_format<kQ4_0>(a, plan, compute_units, stream);

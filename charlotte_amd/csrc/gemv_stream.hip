@@ -1,0 +1,255 @@
+// Decode of Q6_K rows of K = 1,152 (G = 36 groups) — the LM head of Gemma
+// 3 1B and its QKV and output projections — streamed through LDS.
+//
+// The mapping is gemv_quarters' (4 lanes a row, lane j owning ranges
+// 8j .. 8j + 7 = groups 9j .. 9j + 8), but the bytes arrive differently: a
+// wave works 16 rows at a time (a step), and a step's four streams are
+// contiguous in the piece (16 rows x 36 groups: lo 9,216 bytes, hi 4,608,
+// scales 1,152, d 144 — the step starts on a super-block, 576 groups being 72
+// of them). A wave copies a step into its LDS stage with
+// global_load_lds_dwordx4 — 64 lanes x 16 consecutive bytes an instruction,
+// whole 1 KB runs, no register waiting — then, once it has landed, reads its
+// lanes' share into registers, starts the next step's copy into the same
+// stage, and decodes from registers: the copy of one step runs under the
+// decode of the one before. Stages are wave-private: no workgroup barrier;
+// the wait for a step is one s_waitcnt on the wave's own count. Two
+// workgroups of four waves a CU (two waves a SIMD) fit the LDS.
+//
+// x is staged once in LDS; a lane reads its slice a group at a time. A row's
+// total is its 32 range sums added in order from zero: lane j holds sums
+// 8j .. 8j + 7; lane 0 adds its eight to zero, passes the partial total to
+// lane 1 (a quad permute), which adds its eight, and so on — the canonical
+// order, so the bits are every other kernel's.
+#include <algorithm>
+
+#include "decode.hpp"
+#include "product.hpp"
+
+namespace chm {
+
+constexpr int kStreamWaves = 4;
+constexpr uint32_t kStepRows = 16;
+constexpr uint32_t kStepGroups = kStepRows * 36;  // 576
+// A step's 16-byte chunks a stream: lo 576, hi 288, scales 72, d 9 (144
+// bytes: 72 super-blocks).
+constexpr uint32_t kLoChunks = kStepGroups, kHiChunks = kStepGroups / 2, kScChunks = kStepGroups / 8, kDChunks = 9;
+
+typedef uint32_t u32x4s_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_void;
+
+// vmcnt(0) alone, in s_waitcnt's gfx9 encoding (the other counters at
+// their no-wait values).
+constexpr int kVmcnt0 = (0x7 << 4) | (0xF << 8);
+
+// Copies `chunks` 16-byte chunks from `from` to LDS `to`, 64 a wave
+// instruction (lanes past the last chunk copy nothing).
+template <uint32_t kChunks>
+__device__ __forceinline__ void copy_stream(const uint8_t* from, u32x4s_t* to, uint32_t lane) {
+#pragma unroll
+    for (uint32_t i = 0; i < (kChunks + 63) / 64; ++i) {
+        if (64 * i + 64 <= kChunks || 64 * i + lane < kChunks)
+            __builtin_amdgcn_global_load_lds(from + 16 * (64 * i + lane), (lds_void)(to + 64 * i), 16, 0, 0);
+    }
+}
+
+// A lane's share of a step, as held in registers between the stage and the
+// decode: its nine groups' lo and hi, their scale pairs, the two d's.
+typedef uint32_t u32x2s_t __attribute__((ext_vector_type(2)));
+struct StepRun {
+    u32x4s_t lo[9];
+    u32x2s_t hi[9];
+    uint32_t sc[9];
+    uint32_t d_first, d_next;
+};
+
+template <bool FULL>
+__global__ __launch_bounds__(256, 2) void gemv_stream(Product a, uint32_t steps) {
+    __shared__ u32x4s_t lo_a[kStreamWaves][kLoChunks];
+    __shared__ u32x4s_t hi_a[kStreamWaves][kHiChunks];
+    __shared__ u32x4s_t sc_a[kStreamWaves][kScChunks];
+    __shared__ u32x4s_t d_a[kStreamWaves][kDChunks];
+    __shared__ float4 xs[292];  // four slices of 72, one float4 of padding each
+
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches
+    const uint32_t rho = lane >> 2, j = lane & 3u;
+    const uint32_t waves = gridDim.x * kStreamWaves;
+    const uint32_t token = a.last_token ? a.tokens - 1 : 0;
+
+    // x in LDS, clamped where the product is clipped; lane j reads its slice
+    // (groups 9j .. 9j + 8) a group at a time, lanes of one j the same words.
+    // Slices sit 73 float4 apart, so the four a read takes start in
+    // different banks.
+    {
+        const float4* src = reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(token) * 1152);
+        for (uint32_t v = threadIdx.x; v < 288; v += 256) xs[v + v / 72] = clamp_input(a, src[v]);
+        __syncthreads();
+    }
+    struct Stage {
+        u32x4s_t *lo, *hi, *sc, *d;
+    };
+    const Stage sa{lo_a[wave], hi_a[wave], sc_a[wave], d_a[wave]};
+
+
+    auto issue = [&](uint32_t step, const Stage& st) {
+        u32x4s_t *lo = st.lo, *hi = st.hi, *sc = st.sc, *d = st.d;
+        const Piece w = piece_of(a, step * kStepRows);
+        const uint64_t n = w.blocks;
+        copy_stream<kLoChunks>(w.piece + 576ull * w.row, lo, lane);
+        copy_stream<kHiChunks>(w.piece + 128 * n + 288ull * w.row, hi, lane);
+        copy_stream<kScChunks>(w.piece + 192 * n + 72ull * w.row, sc, lane);
+        copy_stream<kDChunks>(w.piece + 208 * n + 9ull * w.row, d, lane);
+    };
+    const uint32_t lg = 36 * rho + 9 * j;  // the lane's first group within a step
+    // The stage's reads are written as instructions the compiler does not
+    // look into: it would otherwise wait for every copy in flight into any
+    // stage before them (it cannot tell the two stages' copies apart across
+    // the loop). The waits around them are explicit: the copies' before,
+    // lgkmcnt(0) after.
+    auto take = [&](StepRun& run, const Stage& st) {
+        const uint32_t lo_at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(st.lo)) + 16 * lg;
+        const uint32_t hi_at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(st.hi)) + 8 * lg;
+        const uint32_t sc_at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(st.sc)) + 2 * lg;
+        const uint32_t d_at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(st.d)) + 2 * (lg >> 3);
+#define CHM_LDS_B128(dst, addr, off) \
+    __asm__ __volatile__("ds_read_b128 %0, %1 offset:" #off : "=v"(dst) : "v"(addr))
+#define CHM_LDS_B64(dst, addr, off) __asm__ __volatile__("ds_read_b64 %0, %1 offset:" #off : "=v"(dst) : "v"(addr))
+#define CHM_LDS_U16(dst, addr, off) __asm__ __volatile__("ds_read_u16 %0, %1 offset:" #off : "=v"(dst) : "v"(addr))
+        CHM_LDS_B128(run.lo[0], lo_at, 0);
+        CHM_LDS_B128(run.lo[1], lo_at, 16);
+        CHM_LDS_B128(run.lo[2], lo_at, 32);
+        CHM_LDS_B128(run.lo[3], lo_at, 48);
+        CHM_LDS_B128(run.lo[4], lo_at, 64);
+        CHM_LDS_B128(run.lo[5], lo_at, 80);
+        CHM_LDS_B128(run.lo[6], lo_at, 96);
+        CHM_LDS_B128(run.lo[7], lo_at, 112);
+        CHM_LDS_B128(run.lo[8], lo_at, 128);
+        CHM_LDS_B64(run.hi[0], hi_at, 0);
+        CHM_LDS_B64(run.hi[1], hi_at, 8);
+        CHM_LDS_B64(run.hi[2], hi_at, 16);
+        CHM_LDS_B64(run.hi[3], hi_at, 24);
+        CHM_LDS_B64(run.hi[4], hi_at, 32);
+        CHM_LDS_B64(run.hi[5], hi_at, 40);
+        CHM_LDS_B64(run.hi[6], hi_at, 48);
+        CHM_LDS_B64(run.hi[7], hi_at, 56);
+        CHM_LDS_B64(run.hi[8], hi_at, 64);
+        CHM_LDS_U16(run.sc[0], sc_at, 0);
+        CHM_LDS_U16(run.sc[1], sc_at, 2);
+        CHM_LDS_U16(run.sc[2], sc_at, 4);
+        CHM_LDS_U16(run.sc[3], sc_at, 6);
+        CHM_LDS_U16(run.sc[4], sc_at, 8);
+        CHM_LDS_U16(run.sc[5], sc_at, 10);
+        CHM_LDS_U16(run.sc[6], sc_at, 12);
+        CHM_LDS_U16(run.sc[7], sc_at, 14);
+        CHM_LDS_U16(run.sc[8], sc_at, 16);
+        CHM_LDS_U16(run.d_first, d_at, 0);
+        CHM_LDS_U16(run.d_next, d_at, 2);
+        // The reads have landed before anything uses their registers: the
+        // wait claims to modify every one of them, so no use can move above it.
+        __asm__ __volatile__("s_waitcnt lgkmcnt(0)"
+                             : "+v"(run.lo[0]), "+v"(run.lo[1]), "+v"(run.lo[2]), "+v"(run.lo[3]), "+v"(run.lo[4]),
+                               "+v"(run.lo[5]), "+v"(run.lo[6]), "+v"(run.lo[7]), "+v"(run.lo[8])
+                             :
+                             : "memory");
+        __asm__ __volatile__(""
+                             : "+v"(run.hi[0]), "+v"(run.hi[1]), "+v"(run.hi[2]), "+v"(run.hi[3]), "+v"(run.hi[4]),
+                               "+v"(run.hi[5]), "+v"(run.hi[6]), "+v"(run.hi[7]), "+v"(run.hi[8]));
+        __asm__ __volatile__(""
+                             : "+v"(run.sc[0]), "+v"(run.sc[1]), "+v"(run.sc[2]), "+v"(run.sc[3]), "+v"(run.sc[4]),
+                               "+v"(run.sc[5]), "+v"(run.sc[6]), "+v"(run.sc[7]), "+v"(run.sc[8]), "+v"(run.d_first),
+                               "+v"(run.d_next));
+#undef CHM_LDS_B128
+#undef CHM_LDS_B64
+#undef CHM_LDS_U16
+    };
+    // One step: the lane's nine groups, its eight range sums, the row's total
+    // by the quad chain, the output.
+    auto decode = [&](uint32_t step, const StepRun& run) {
+        float sums[8];
+        float s = 0.0f;
+        // x a group ahead: group i + 1's words are read before group i's
+        // products, so the reads' latency runs under them.
+        float4 xa[2][8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) xa[0][v] = xs[73 * j + v];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) {
+            if (i + 1 < 9) {
+#pragma unroll
+                for (int v = 0; v < 8; ++v) xa[(i + 1) & 1][v] = xs[73 * j + 8 * (i + 1) + v];
+            }
+            float xg[32];
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+                const float4 q = xa[i & 1][v];
+                xg[4 * v] = q.x, xg[4 * v + 1] = q.y, xg[4 * v + 2] = q.z, xg[4 * v + 3] = q.w;
+            }
+            const uint32_t lw[4] = {run.lo[i][0], run.lo[i][1], run.lo[i][2], run.lo[i][3]};
+            const uint32_t hw[2] = {run.hi[i][0], run.hi[i][1]};
+            const uint32_t dbits = ((lg + i) >> 3) == (lg >> 3) ? run.d_first : run.d_next;
+            s = chain_q6_k(lw, hw, run.sc[i], dbits, xg, s);
+            // Range 8j + m is group 9j + m alone for m < 7, and groups
+            // 9j + 7 and 9j + 8 for m = 7 (floor(36 r / 32) at r = 8j + m):
+            // the same for every lane.
+            if (i < 7 || i == 8) {
+                sums[i < 7 ? i : 7] = s;
+                s = 0.0f;
+            }
+        }
+        // The quad chain: total = ((0 + sums of lane 0) + sums of lane 1) ...
+        float total = 0.0f;
+#pragma unroll
+        for (int step_lane = 0; step_lane < 4; ++step_lane) {
+            float t = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, total), 0x90, 0xF, 0xF,
+                                                                           false));  // quad_perm [0, 0, 1, 2]
+            if (step_lane == 0) t = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) t = t + sums[k];
+            if (j == static_cast<uint32_t>(step_lane)) total = t;
+        }
+        const uint32_t p = step * kStepRows + rho;
+        float partner = 0.0f;
+        if (FULL && a.epilogue == kGated) partner = __shfl_xor(total, 4);
+        if (j == 3 && p < a.rows) emit<FULL>(a, p, 0, a.last_token ? a.tokens - 1 : 0, total, partner);
+    };
+
+    // One step in flight a wave (two waves a SIMD): the next step's copy is
+    // issued as soon as this one is out of the stage.
+    uint32_t step = blockIdx.x * kStreamWaves + wave;
+    if (step >= steps) return;
+    issue(step, sa);
+    while (true) {
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+        __asm__ __volatile__("" ::: "memory");
+        StepRun run;
+        take(run, sa);
+        const uint32_t next = step + waves;
+        if (next < steps) issue(next, sa);
+        decode(step, run);
+        if (next >= steps) break;
+        step = next;
+    }
+}
+
+// Whether the streamed kernel takes the product: Q6_K, K = 1,152, every
+// member's rows and first row a whole number of steps (so a step lies in one
+// member and starts on a super-block), and a plain or any epilogue.
+bool gemv_stream_takes(const Product& a, uint32_t format) {
+    if (format != kQ6_K || a.groups != 36) return false;
+    for (uint32_t m = 0; m < a.members; ++m)
+        if (a.m[m].rows % kStepRows != 0 || a.m[m].row_offset % kStepRows != 0) return false;
+    if (a.epilogue == kGated) return false;  // gated rows interleave the members
+    return true;
+}
+
+hipError_t launch_gemv_stream(const Product& a, uint32_t compute_units, hipStream_t stream) {
+    const uint32_t steps = a.rows / kStepRows;
+    const uint32_t blocks = std::min<uint32_t>(2 * compute_units, (steps + kStreamWaves - 1) / kStreamWaves);
+    if (plain_epilogue(a))
+        hipLaunchKernelGGL((gemv_stream<false>), dim3(blocks), dim3(256), 0, stream, a, steps);
+    else
+        hipLaunchKernelGGL((gemv_stream<true>), dim3(blocks), dim3(256), 0, stream, a, steps);
+    return hipGetLastError();
+}
+
+}  // namespace chm

@@ -288,3 +288,63 @@ def test_errors_are_statuses_with_messages(run, fixture_tensors):
     xb.free()
     yb.free()
     w.free()
+
+
+# ---- Q6_K at K = 1,152 in whole 16-row steps (the streamed decode) ------------
+
+
+@pytest.mark.parametrize("rows", [16, 48, 1024, 4096])
+def test_q6_k_1152_streamed_steps(oracle, run, rows):
+    """Rows a multiple of 16 take the LDS-streamed decode: the same bits as
+    the oracle, decoded alone and as the head's last token."""
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+    from tests.support.gpu import bits_equal, first_difference
+
+    rng = np.random.default_rng(rows)
+    stored = synthetic.q6_k(rng, rows, 1152)
+    x = synthetic.activations(rng, 3, 1152)
+    w = run.weight(Q6_K, rows, 1152, stored)
+    want = oracle.matmul_f32(Q6_K, stored, rows, 1152, x, threads=8)
+    got = run.write(w, x[:1], 1)
+    assert bits_equal(got[0], want[0]), first_difference(got[0], want[0])
+    last = run.write(w, x, 3, rows=mm.Rows.LastToken)
+    assert bits_equal(last[0], want[2]), first_difference(last[0], want[2])
+    w.free()
+
+
+def test_q6_k_1152_streamed_members_and_epilogues(oracle, run):
+    """QKV of three K = 1,152 weights, members at row offsets, GatedByInput and
+    a Write with every option, all through the streamed decode."""
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+    from tests.support.gpu import bits_equal, first_difference
+
+    rng = np.random.default_rng(1152)
+    sizes = [1024, 256, 256]
+    stored = [synthetic.q6_k(rng, r, 1152) for r in sizes]
+    x = synthetic.activations(rng, 1, 1152)
+    ws = [run.weight(Q6_K, r, 1152, s) for r, s in zip(sizes, stored)]
+    want = [oracle.matmul_f32(Q6_K, s, r, 1152, x) for r, s in zip(sizes, stored)]
+    got = run.product([mm.Member(w) for w in ws], x, 1, sizes, epilogue=mm.Epilogue.QKV)
+    for i in range(3):
+        assert bits_equal(got[i], want[i]), f"member {i}: {first_difference(got[i], want[i])}"
+    # Rows 32 .. 543 of the first weight, then rows 16 .. 111 of the second, at output rows 0 and 512.
+    members = [mm.Member(ws[0], row_offset=32, rows=512), mm.Member(ws[1], row_offset=16, rows=96, output_row=512)]
+    got = run.product(members, x, 1, [608])[0]
+    expect = np.concatenate([want[0][:, 32:544], want[1][:, 16:112]], axis=1)
+    assert bits_equal(got, expect), first_difference(got, expect)
+    u = np.random.default_rng(7).standard_normal((1, 1024), dtype=np.float32)
+    got = run.product([mm.Member(ws[0])], x, 1, [1024], epilogue=mm.Epilogue.GatedByInput, gate_input=u,
+                      gate_input_stride=1024, activation=mm.Activation.GeluTanh)[0]
+    expect = oracle.gated_by_input(want[0], u, activation=1)
+    assert bits_equal(got, expect), first_difference(got, expect)
+    clip = np.array([-1.0, 1.25, -0.02, 0.03], np.float32)
+    bias = np.linspace(-0.01, 0.01, 1024, dtype=np.float32)
+    got = run.product([mm.Member(ws[0])], x, 1, [1024], clip=clip, bias=bias, activated=True,
+                      activation=mm.Activation.SiLU)[0]
+    totals = oracle.matmul_f32(Q6_K, stored[0], 1024, 1152, oracle.clamp(x, clip[0], clip[1]))
+    expect = oracle.finish(totals, clip=clip, bias=bias, activated=True, activation=0)
+    assert bits_equal(got, expect), first_difference(got, expect)
+    for w in ws:
+        w.free()
