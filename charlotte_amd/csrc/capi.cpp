@@ -14,6 +14,7 @@
 #include <string>
 #include <vector>
 
+#include "gguf.hpp"
 #include "layout.hpp"
 #include "product.hpp"
 
@@ -24,6 +25,10 @@ struct charlotte_hip_matmul_context {
     void* workspace = nullptr;  // the matrix-core path's, the caller's memory
     uint64_t workspace_bytes = 0;
     std::string error;
+};
+
+struct charlotte_hip_matmul_gguf {
+    chm::GgufFile file;
 };
 
 struct charlotte_hip_matmul_weight {
@@ -364,6 +369,97 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
     }
     if (e != hipSuccess) return hip_fail(ctx, e, "launch");
     return ok(ctx);
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_gguf_open(const char* path, charlotte_hip_matmul_gguf** out,
+                                                           uint32_t* read_error) {
+    if (!path || !out) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    *out = nullptr;
+    auto* g = new (std::nothrow) charlotte_hip_matmul_gguf;
+    if (!g) return CHARLOTTE_HIP_MATMUL_OUT_OF_MEMORY;
+    int os_error = 0;
+    const chm::GgufError e = g->file.open(path, &os_error);
+    if (read_error) *read_error = static_cast<uint32_t>(e);
+    if (os_error != 0) {
+        delete g;
+        return CHARLOTTE_HIP_MATMUL_IO_ERROR;
+    }
+    if (e != chm::GgufError::kOk) {
+        delete g;
+        return CHARLOTTE_HIP_MATMUL_BAD_FILE;
+    }
+    *out = g;
+    return CHARLOTTE_HIP_MATMUL_OK;
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_gguf_read(const void* bytes, uint64_t size,
+                                                           charlotte_hip_matmul_gguf** out, uint32_t* read_error) {
+    if (!out || (!bytes && size)) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    *out = nullptr;
+    auto* g = new (std::nothrow) charlotte_hip_matmul_gguf;
+    if (!g) return CHARLOTTE_HIP_MATMUL_OUT_OF_MEMORY;
+    static const uint8_t kEmpty = 0;
+    const chm::GgufError e = g->file.index.read(bytes ? static_cast<const uint8_t*>(bytes) : &kEmpty, size);
+    if (read_error) *read_error = static_cast<uint32_t>(e);
+    if (e != chm::GgufError::kOk) {
+        delete g;
+        return CHARLOTTE_HIP_MATMUL_BAD_FILE;
+    }
+    *out = g;
+    return CHARLOTTE_HIP_MATMUL_OK;
+}
+
+const char* charlotte_hip_matmul_gguf_error_string(uint32_t read_error) {
+    return chm::gguf_error_string(static_cast<chm::GgufError>(read_error));
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_gguf_close(charlotte_hip_matmul_gguf* file) {
+    delete file;
+    return CHARLOTTE_HIP_MATMUL_OK;
+}
+
+uint64_t charlotte_hip_matmul_gguf_tensor_count(const charlotte_hip_matmul_gguf* file) {
+    return file ? file->file.index.tensors.size() : 0;
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_gguf_tensor_at(const charlotte_hip_matmul_gguf* file, uint64_t index,
+                                                                charlotte_hip_matmul_gguf_tensor* out) {
+    if (!file || !out || index >= file->file.index.tensors.size()) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    const chm::GgufTensor& t = file->file.index.tensors[index];
+    out->name = t.name.c_str();
+    out->gguf_type = t.type;
+    out->dimension_count = t.dimension_count;
+    for (int d = 0; d < 4; ++d) out->dimensions[d] = t.dimensions[d];
+    out->element_count = t.elements;
+    out->offset = t.offset;
+    out->bytes = t.bytes;
+    return CHARLOTTE_HIP_MATMUL_OK;
+}
+
+int64_t charlotte_hip_matmul_gguf_find(const charlotte_hip_matmul_gguf* file, const char* name) {
+    return file && name ? file->file.index.find(name) : -1;
+}
+
+const void* charlotte_hip_matmul_gguf_bytes(const charlotte_hip_matmul_gguf* file) {
+    return file ? file->file.index.bytes : nullptr;
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_gguf_upload(charlotte_hip_matmul_context* ctx,
+                                                             const charlotte_hip_matmul_gguf* file, uint64_t index,
+                                                             charlotte_hip_matmul_weight** out) {
+    if (!ctx) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    if (!file || !out || index >= file->file.index.tensors.size())
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gguf upload: no such tensor");
+    const chm::GgufTensor& t = file->file.index.tensors[index];
+    if (!known(t.type))
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_UNSUPPORTED_TYPE,
+                    "gguf upload: " + t.name + " is GGUF type " + std::to_string(t.type));
+    const uint64_t columns = t.dimensions[0];
+    const uint64_t rows = columns ? t.elements / columns : 0;
+    const charlotte_hip_matmul_status s = charlotte_hip_matmul_weight_upload(
+        ctx, t.type, rows, columns, file->file.index.bytes + t.offset, t.bytes, out);
+    if (s != CHARLOTTE_HIP_MATMUL_OK) ctx->error = "gguf upload of " + t.name + ": " + ctx->error;
+    return s;
 }
 
 }  // extern "C"

@@ -33,6 +33,8 @@ class Status(enum.IntEnum):
     HIP_ERROR = 5
     NO_DEVICE = 6
     UNSUPPORTED = 7
+    BAD_FILE = 8
+    IO_ERROR = 9
 
 
 class TensorType(enum.IntEnum):
@@ -118,6 +120,18 @@ class _Desc(ctypes.Structure):
     ]
 
 
+class _GgufTensor(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("gguf_type", ctypes.c_uint32),
+        ("dimension_count", ctypes.c_uint32),
+        ("dimensions", ctypes.c_uint64 * 4),
+        ("element_count", ctypes.c_uint64),
+        ("offset", ctypes.c_uint64),
+        ("bytes", ctypes.c_uint64),
+    ]
+
+
 # Every symbol the header declares, with its ctypes signature.
 _c = ctypes
 SIGNATURES = {
@@ -146,6 +160,21 @@ SIGNATURES = {
     ),
     "charlotte_hip_matmul_split_tokens": (_c.c_uint32, [_c.c_uint32, _c.c_uint64, _c.c_uint64, _Gate]),
     "charlotte_hip_matmul_range_sum_floats": (_c.c_uint64, [_c.c_uint32, _c.c_uint64, _c.c_uint64, _Gate]),
+    "charlotte_hip_matmul_gguf_open": (_c.c_int, [_c.c_char_p, _c.POINTER(_c.c_void_p), _c.POINTER(_c.c_uint32)]),
+    "charlotte_hip_matmul_gguf_read": (
+        _c.c_int,
+        [_c.c_void_p, _c.c_uint64, _c.POINTER(_c.c_void_p), _c.POINTER(_c.c_uint32)],
+    ),
+    "charlotte_hip_matmul_gguf_error_string": (_c.c_char_p, [_c.c_uint32]),
+    "charlotte_hip_matmul_gguf_close": (_c.c_int, [_c.c_void_p]),
+    "charlotte_hip_matmul_gguf_tensor_count": (_c.c_uint64, [_c.c_void_p]),
+    "charlotte_hip_matmul_gguf_tensor_at": (_c.c_int, [_c.c_void_p, _c.c_uint64, _c.POINTER(_GgufTensor)]),
+    "charlotte_hip_matmul_gguf_find": (_c.c_int64, [_c.c_void_p, _c.c_char_p]),
+    "charlotte_hip_matmul_gguf_bytes": (_c.c_void_p, [_c.c_void_p]),
+    "charlotte_hip_matmul_gguf_upload": (
+        _c.c_int,
+        [_c.c_void_p, _c.c_void_p, _c.c_uint64, _c.POINTER(_c.c_void_p)],
+    ),
 }
 
 
@@ -315,3 +344,108 @@ def launch(ctx: Context, m: MatmulLaunch, tokens: int, gate: SplitGate = kNever,
         m._desc = m.desc()
     ctx.check(lib.charlotte_hip_matmul_launch(ctx.handle, ctypes.byref(m._desc), _gate(gate), range_sums,
                                               range_sums_bytes, tokens, stream))
+
+
+# ---- GGUF files (gguf::read_index, src/core/gguf/reader.cpp) -----------------
+
+# gguf::ReadError (src/core/gguf/types.h:112-141), numbered alike.
+class ReadError(enum.IntEnum):
+    Ok = 0
+    NeedMoreBytes = 1
+    ShortRead = 2
+    BadMagic = 3
+    UnsupportedVersion = 4
+    CountTooLarge = 5
+    StringTooLong = 6
+    ArrayTooLong = 7
+    UnknownValueType = 8
+    UnknownTensorType = 9
+    RowNotWholeBlocks = 10
+    TooManyDimensions = 11
+    NegativeDimension = 12
+    ElementCountOverflow = 13
+    OffsetOverflow = 14
+    TensorDataOutOfBounds = 15
+    DuplicateTensorName = 16
+    TensorNameTooLong = 17
+    MisalignedTensorData = 18
+    OverlappingTensorData = 19
+    BadAlignment = 20
+    EmptyKey = 21
+    DuplicateMetadataKey = 22
+    NestedArray = 23
+    WrongElementType = 24
+
+
+class GgufError(RuntimeError):
+    def __init__(self, status, read_error):
+        self.status = Status(status)
+        self.read_error = ReadError(read_error)
+        super().__init__(f"{self.status.name}: {self.read_error.name}: "
+                         f"{lib.charlotte_hip_matmul_gguf_error_string(read_error).decode()}")
+
+
+@dataclass(frozen=True)
+class GgufTensor:
+    """gguf::TensorEntry (src/core/gguf/types.h:191-243): offsets absolute."""
+
+    index: int
+    name: str
+    gguf_type: int
+    dimensions: tuple
+    element_count: int
+    offset: int
+    bytes: int
+
+
+class GgufFile:
+    """A GGUF v3 file's validated tensor index (charlotte_hip_matmul_gguf_*):
+    opened from a path (mapped) or read from bytes in memory."""
+
+    def __init__(self, path=None, data: Optional[bytes] = None):
+        h = ctypes.c_void_p()
+        err = ctypes.c_uint32()
+        if path is not None:
+            s = lib.charlotte_hip_matmul_gguf_open(os.fsencode(path), ctypes.byref(h), ctypes.byref(err))
+        else:
+            self._data = ctypes.create_string_buffer(bytes(data), len(data)) if len(data) else None
+            s = lib.charlotte_hip_matmul_gguf_read(self._data, len(data), ctypes.byref(h), ctypes.byref(err))
+        if s != 0:
+            raise GgufError(s, err.value)
+        self.handle = h
+        self.tensors = []
+        for i in range(lib.charlotte_hip_matmul_gguf_tensor_count(h)):
+            t = _GgufTensor()
+            assert lib.charlotte_hip_matmul_gguf_tensor_at(h, i, ctypes.byref(t)) == 0
+            self.tensors.append(GgufTensor(i, t.name.decode(), t.gguf_type, tuple(t.dimensions[: t.dimension_count]),
+                                           t.element_count, t.offset, t.bytes))
+
+    def find(self, name) -> int:
+        return lib.charlotte_hip_matmul_gguf_find(self.handle, name.encode())
+
+    def data(self, tensor: GgufTensor) -> bytes:
+        base = lib.charlotte_hip_matmul_gguf_bytes(self.handle)
+        return ctypes.string_at(base + tensor.offset, tensor.bytes)
+
+    def upload(self, ctx: "Context", name) -> "Weight":
+        i = self.find(name)
+        if i < 0:
+            raise KeyError(name)
+        t = self.tensors[i]
+        h = ctypes.c_void_p()
+        ctx.check(lib.charlotte_hip_matmul_gguf_upload(ctx.handle, self.handle, i, ctypes.byref(h)))
+        w = Weight.__new__(Weight)
+        w.ctx, w.type, w.rows, w.columns, w.handle = ctx, TensorType(t.gguf_type), t.element_count // t.dimensions[0], \
+            t.dimensions[0], h
+        return w
+
+    def close(self):
+        if self.handle:
+            lib.charlotte_hip_matmul_gguf_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()

@@ -25,6 +25,8 @@
  *   charlotte_hip_matmul_repack_q6_k formats::detail::repack_q6_k
  *                                                          src/core/formats/q6_k/q6_k_repack.cpp:52-87
  *   charlotte_hip_matmul_status     kernels::ProgramError  src/core/kernels/program.h:159-169
+ *   charlotte_hip_matmul_gguf_*     gguf::read_index, gguf::TensorEntry, gguf::ReadError
+ *                                                          src/core/gguf/reader.h:14-29, types.h:112-141, 191-243
  *
  * Conventions: every function returns a status and never throws; a failure
  * names its subject in charlotte_hip_matmul_last_error(ctx). A context owns
@@ -62,7 +64,9 @@ typedef enum {
     CHARLOTTE_HIP_MATMUL_OUT_OF_MEMORY = 4,
     CHARLOTTE_HIP_MATMUL_HIP_ERROR = 5,         /* the HIP runtime refused a call; its message is in last_error */
     CHARLOTTE_HIP_MATMUL_NO_DEVICE = 6,
-    CHARLOTTE_HIP_MATMUL_UNSUPPORTED = 7        /* an epilogue, option or combination not built */
+    CHARLOTTE_HIP_MATMUL_UNSUPPORTED = 7,       /* an epilogue, option or combination not built */
+    CHARLOTTE_HIP_MATMUL_BAD_FILE = 8,          /* a GGUF file that fails validation: see read_error */
+    CHARLOTTE_HIP_MATMUL_IO_ERROR = 9           /* a file that cannot be opened or mapped */
 } charlotte_hip_matmul_status;
 
 /* GGUF tensor types the kernels read (src/core/gguf/types.h:41-43). */
@@ -230,6 +234,50 @@ uint32_t charlotte_hip_matmul_split_tokens(uint32_t epilogue, uint64_t rows, uin
                                            charlotte_hip_matmul_split_gate gate);
 uint64_t charlotte_hip_matmul_range_sum_floats(uint32_t epilogue, uint64_t rows, uint64_t columns,
                                                charlotte_hip_matmul_split_gate gate);
+
+/* ---- GGUF files (gguf::read_index, src/core/gguf/reader.cpp) -------------------- */
+
+/* A GGUF v3 file's tensor index: every tensor's name, format, shape and
+ * absolute byte range, validated against the file (a defined format whose
+ * blocks tile a row, offsets aligned to general.alignment, ranges inside the
+ * file and disjoint, names unique and at most 64 bytes, ...). A file that
+ * fails returns BAD_FILE and sets *read_error to the reference's ReadError
+ * number (src/core/gguf/types.h:112-141); charlotte_hip_matmul_gguf_error_string
+ * names it. Host only. */
+typedef struct charlotte_hip_matmul_gguf charlotte_hip_matmul_gguf;
+
+typedef struct {
+    const char* name;           /* owned by the file handle */
+    uint32_t gguf_type;
+    uint32_t dimension_count;
+    uint64_t dimensions[4];     /* dimensions[0]: a row's length (K) */
+    uint64_t element_count;
+    uint64_t offset;            /* absolute, in the file */
+    uint64_t bytes;
+} charlotte_hip_matmul_gguf_tensor;
+
+/* The file at `path`, mapped read-only until closed. */
+charlotte_hip_matmul_status charlotte_hip_matmul_gguf_open(const char* path, charlotte_hip_matmul_gguf** out,
+                                                           uint32_t* read_error);
+/* The same over `size` bytes in memory, borrowed until closed. */
+charlotte_hip_matmul_status charlotte_hip_matmul_gguf_read(const void* bytes, uint64_t size,
+                                                           charlotte_hip_matmul_gguf** out, uint32_t* read_error);
+const char* charlotte_hip_matmul_gguf_error_string(uint32_t read_error);
+charlotte_hip_matmul_status charlotte_hip_matmul_gguf_close(charlotte_hip_matmul_gguf* file);
+uint64_t charlotte_hip_matmul_gguf_tensor_count(const charlotte_hip_matmul_gguf* file);
+charlotte_hip_matmul_status charlotte_hip_matmul_gguf_tensor_at(const charlotte_hip_matmul_gguf* file, uint64_t index,
+                                                                charlotte_hip_matmul_gguf_tensor* out);
+/* A tensor's index by name, or -1. */
+int64_t charlotte_hip_matmul_gguf_find(const charlotte_hip_matmul_gguf* file, const char* name);
+/* The file's first byte (tensor bytes are at their offsets from it). */
+const void* charlotte_hip_matmul_gguf_bytes(const charlotte_hip_matmul_gguf* file);
+/* Tensor `index` as a weight on ctx's device: its blocks laid out as
+ * charlotte_hip_matmul_weight_upload lays them out, rows = element_count /
+ * dimensions[0], columns = dimensions[0]. UNSUPPORTED_TYPE for a format the
+ * kernels do not read. */
+charlotte_hip_matmul_status charlotte_hip_matmul_gguf_upload(charlotte_hip_matmul_context* ctx,
+                                                             const charlotte_hip_matmul_gguf* file, uint64_t index,
+                                                             charlotte_hip_matmul_weight** out);
 
 #ifdef __cplusplus
 }

@@ -348,3 +348,30 @@ def test_q6_k_1152_streamed_members_and_epilogues(oracle, run):
     assert bits_equal(got, expect), first_difference(got, expect)
     for w in ws:
         w.free()
+
+
+# ---- weights read from a GGUF file ----------------------------------------------
+
+
+def test_weights_uploaded_from_a_gguf_file(oracle, run, source, fixture_tensors):
+    """The reference fixture's tensors, read and laid out by the library from
+    the file itself, give the oracle's bits."""
+    import os
+
+    from charlotte_amd import matmul as mm
+    from tests.support.gpu import bits_equal, first_difference
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "matmul_rows.gguf")
+    with mm.GgufFile(path) as f:
+        for name in ("w_q4_0", "w_q6_k", "qkv_q", "ffn_gate"):
+            t = fixture_tensors[name]
+            w = f.upload(run.ctx, name)
+            x = _rows_of(source, t.columns, 9)
+            want = oracle.matmul_f32(t.type, t.data, t.rows, t.columns, x)
+            for tokens in (1, 9):
+                got = run.write(w, x, tokens)
+                assert bits_equal(got, want[:tokens]), f"{name} tokens={tokens}: {first_difference(got, want[:tokens])}"
+            w.free()
+        with pytest.raises(mm.MatmulError) as e:
+            f.upload(run.ctx, "w_f32")
+        assert e.value.status == mm.Status.UNSUPPORTED_TYPE and "w_f32" in str(e.value)
