@@ -14,6 +14,7 @@
 #include <string>
 #include <vector>
 
+#include "gather.hpp"
 #include "gguf.hpp"
 #include "layout.hpp"
 #include "product.hpp"
@@ -58,7 +59,14 @@ Status hip_fail(charlotte_hip_matmul_context* ctx, hipError_t e, const char* wha
                 std::string(what) + ": " + hipGetErrorString(e));
 }
 
-bool known(uint32_t type) { return type == CHARLOTTE_HIP_MATMUL_Q4_0 || type == CHARLOTTE_HIP_MATMUL_Q6_K; }
+// Formats a weight may hold; the products read all but F32, a gather's table.
+bool known(uint32_t type) {
+    return type == CHARLOTTE_HIP_MATMUL_F32 || type == CHARLOTTE_HIP_MATMUL_Q4_0 || type == CHARLOTTE_HIP_MATMUL_Q4_1 ||
+           type == CHARLOTTE_HIP_MATMUL_Q8_0 || type == CHARLOTTE_HIP_MATMUL_Q6_K;
+}
+bool product_reads(uint32_t type) { return known(type) && type != CHARLOTTE_HIP_MATMUL_F32; }
+// The matrix-core prefill's formats.
+bool mfma_reads(uint32_t type) { return type == CHARLOTTE_HIP_MATMUL_Q4_0 || type == CHARLOTTE_HIP_MATMUL_Q6_K; }
 
 // The shape checks of a weight: rows of whole 32-weight groups
 // (matmul.h:668-671, format.h:138-160) in a tensor of whole blocks.
@@ -284,6 +292,9 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
     chm::Product a{};
     const charlotte_hip_matmul_weight* head = d.members[0].weight;
     if (!head) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member 0 has no weight");
+    if (!product_reads(head->type))
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_UNSUPPORTED_TYPE,
+                    "launch: GGUF type " + std::to_string(head->type) + " (the products read Q4_0, Q4_1, Q8_0, Q6_K)");
     uint64_t rows = 0;
     for (uint32_t i = 0; i < d.member_count; ++i) {
         const charlotte_hip_matmul_member& m = d.members[i];
@@ -360,7 +371,11 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
         const uint64_t need = chm::mfma_workspace_bytes(tokens, a.groups);
         const bool room = ctx->workspace && ctx->workspace_bytes >= need;
         const bool mfma = ctx->gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_SPLIT_F16_MFMA ||
-                          (ctx->gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_AUTO && !sums && room && tokens >= kMfmaLeast);
+                          (ctx->gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_AUTO && !sums && room && tokens >= kMfmaLeast &&
+                           mfma_reads(head->type));
+        if (mfma && !mfma_reads(head->type))
+            return fail(ctx, CHARLOTTE_HIP_MATMUL_UNSUPPORTED,
+                        "launch: the matrix-core path reads Q4_0 and Q6_K, not GGUF type " + std::to_string(head->type));
         if (mfma && !room)
             return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT,
                         "launch: the matrix-core path needs a workspace of " + std::to_string(need) + " bytes");
@@ -368,6 +383,74 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
                  : chm::launch_gemm_canonical(a, head->type, ctx->compute_units, sums, s);
     }
     if (e != hipSuccess) return hip_fail(ctx, e, "launch");
+    return ok(ctx);
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_gather(charlotte_hip_matmul_context* ctx,
+                                                        const charlotte_hip_matmul_gather_desc* desc,
+                                                        uint32_t tokens, void* stream) {
+    if (!ctx) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    if (!desc) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gather: no descriptor");
+    const charlotte_hip_matmul_gather_desc& d = *desc;
+    const charlotte_hip_matmul_weight* t = d.table;
+    if (!t) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gather: no table");
+    if (t->ctx != ctx) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gather: a table of another context");
+    if (tokens == 0) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gather: a step of no tokens");
+    if (!d.fed && !d.ids) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gather: no identifiers");
+    if (!d.hidden || reinterpret_cast<uintptr_t>(d.hidden) % 16 != 0)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gather: hidden missing or not 16-byte aligned");
+    if (d.first_row + t->rows > 0x100000000ull)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gather: rows past 2^32");
+    if (static_cast<uint64_t>(tokens) * (t->columns / 32) * 8 > 0xFFFFFFFFull * 256)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gather: too many rows a step");
+    chm::Gather g{};
+    g.piece = t->piece;
+    g.blocks = t->blocks;
+    g.ids = d.ids;
+    g.fed = d.fed;
+    g.hidden = d.hidden;
+    g.tokens = tokens;
+    g.groups = static_cast<uint32_t>(t->columns / 32);
+    g.first_row = static_cast<uint32_t>(d.first_row);
+    g.row_count = static_cast<uint32_t>(t->rows);
+    g.media = d.media ? 1u : 0u;
+    g.media_token = d.media_token;
+    g.scale = d.scale;
+    if (hipError_t e = hipSetDevice(ctx->device); e != hipSuccess) return hip_fail(ctx, e, "gather: hipSetDevice");
+    if (hipError_t e = chm::launch_gather(g, t->type, static_cast<hipStream_t>(stream)); e != hipSuccess)
+        return hip_fail(ctx, e, "gather");
+    return ok(ctx);
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_gather_positions(charlotte_hip_matmul_context* ctx,
+                                                                  const charlotte_hip_matmul_weight* table,
+                                                                  uint32_t positions, uint32_t grid_columns,
+                                                                  uint32_t tokens, float* output, void* stream) {
+    if (!ctx) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    if (!table) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gather positions: no table");
+    if (table->ctx != ctx)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gather positions: a table of another context");
+    if (table->type != CHARLOTTE_HIP_MATMUL_F32)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_UNSUPPORTED_TYPE, "gather positions: the table is not F32");
+    if (positions == 0 || table->rows != 2ull * positions)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gather positions: the table is not 2 x positions rows");
+    if (grid_columns == 0 || grid_columns > positions || tokens == 0 ||
+        tokens > static_cast<uint64_t>(grid_columns) * positions)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gather positions: a grid the table does not cover");
+    if (!output || reinterpret_cast<uintptr_t>(output) % 16 != 0)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gather positions: output missing or not 16-byte aligned");
+    chm::Gather g{};
+    g.piece = table->piece;
+    g.blocks = table->blocks;
+    g.hidden = output;
+    g.tokens = tokens;
+    g.groups = static_cast<uint32_t>(table->columns / 32);
+    g.positions = positions;
+    g.grid_columns = grid_columns;
+    if (hipError_t e = hipSetDevice(ctx->device); e != hipSuccess)
+        return hip_fail(ctx, e, "gather positions: hipSetDevice");
+    if (hipError_t e = chm::launch_gather_positions(g, static_cast<hipStream_t>(stream)); e != hipSuccess)
+        return hip_fail(ctx, e, "gather positions");
     return ok(ctx);
 }
 

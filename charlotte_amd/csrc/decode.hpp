@@ -13,7 +13,8 @@
 //     scale at most 18);
 //   - the chain s = fma(w_l, x_l, s) runs in k order, as formats.hpp's.
 // About 2.9 VALU operations a Q4_0 weight and 3.4 a Q6_K weight, against
-// formats.hpp's 5 to 6. The bits are the same: each w is the exact weight.
+// formats.hpp's 5 to 6. The bits are the same: each w is the exact weight
+// (Q4_1's, q d + m, rounded once as the reference's).
 #pragma once
 
 #include "formats.hpp"
@@ -83,6 +84,41 @@ __device__ __forceinline__ float chain_q6_k(const uint32_t lo[4], const uint32_t
     return s;
 }
 
+// Four weights of unsigned byte codes: w = fma(code, scale, offset), the
+// codes converted by v_cvt_f32_ubyte0..3, one instruction each.
+__device__ __forceinline__ float chain4_bytes(uint32_t codes, float scale, float offset, const float* x, float s) {
+    s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(codes & 0xFFu), scale, offset), x[0], s);
+    s = __builtin_fmaf(__builtin_fmaf(static_cast<float>((codes >> 8) & 0xFFu), scale, offset), x[1], s);
+    s = __builtin_fmaf(__builtin_fmaf(static_cast<float>((codes >> 16) & 0xFFu), scale, offset), x[2], s);
+    s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(codes >> 24), scale, offset), x[3], s);
+    return s;
+}
+
+// A Q4_1 group: 4 code dwords, its d (low 16 bits) and m (high) word.
+// w = q d + m: low nibbles fma(q, d, m); high nibbles as bytes 16q,
+// fma(16q, d / 16, m) — (16q)(d / 16) = q d exactly — so one rounding either
+// way, the add's.
+__device__ __forceinline__ float chain_q4_1(const uint32_t w[4], uint32_t dm, const float* x, float s) {
+    const float d = half_to_float(dm & 0xFFFFu), m = half_to_float(dm >> 16);
+    const float d16 = d * 0.0625f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s = chain4_bytes(w[c] & 0x0F0F0F0Fu, d, m, x + 4 * c, s);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s = chain4_bytes(w[c] & 0xF0F0F0F0u, d16, m, x + 16 + 4 * c, s);
+    return s;
+}
+
+// A Q8_0 group: 8 code dwords, its fp16 d bits. Each int8 code q biased to
+// q + 128 (the sign bit flipped), lifted to 1024 + q + 128, and
+// fma(1152 + q, d, -1152 d) = q d, exact (1152 d and q d are exact).
+__device__ __forceinline__ float chain_q8_0(const uint32_t w[8], uint32_t d_bits, const float* x, float s) {
+    const float d = half_to_float(d_bits);
+    const float offset = -1152.0f * d;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) s = chain4(w[c] ^ 0x80808080u, d, offset, x + 4 * c, s);
+    return s;
+}
+
 // A group's raw bytes as a kernel holds them between load and use.
 template <uint32_t F>
 struct Raw;
@@ -100,6 +136,41 @@ struct Raw<kQ4_0> {
         d = *reinterpret_cast<const uint16_t*>(piece + 16 * n + 2 * gi);
     }
     __device__ __forceinline__ float chain(const float* x, float s) const { return chain_q4_0(w, d, x, s); }
+};
+
+template <>
+struct Raw<kQ4_1> {
+    uint32_t w[4];
+    uint32_t dm;
+    __device__ __forceinline__ void load(const uint8_t* piece, uint64_t n, uint64_t gi) {
+        const uint4 c = *reinterpret_cast<const uint4*>(piece + 16 * gi);
+        w[0] = c.x;
+        w[1] = c.y;
+        w[2] = c.z;
+        w[3] = c.w;
+        dm = *reinterpret_cast<const uint32_t*>(piece + 16 * n + 4 * gi);
+    }
+    __device__ __forceinline__ float chain(const float* x, float s) const { return chain_q4_1(w, dm, x, s); }
+};
+
+template <>
+struct Raw<kQ8_0> {
+    uint32_t w[8];
+    uint32_t d;
+    __device__ __forceinline__ void load(const uint8_t* piece, uint64_t n, uint64_t gi) {
+        const uint4* c = reinterpret_cast<const uint4*>(piece + 32 * gi);
+        const uint4 a = c[0], b = c[1];
+        w[0] = a.x;
+        w[1] = a.y;
+        w[2] = a.z;
+        w[3] = a.w;
+        w[4] = b.x;
+        w[5] = b.y;
+        w[6] = b.z;
+        w[7] = b.w;
+        d = *reinterpret_cast<const uint16_t*>(piece + 32 * n + 2 * gi);
+    }
+    __device__ __forceinline__ float chain(const float* x, float s) const { return chain_q8_0(w, d, x, s); }
 };
 
 template <>

@@ -1,5 +1,5 @@
-// The two weight formats as the kernels read them from a piece's streams,
-// and the one multiply-add order every canonical kernel shares.
+// The weight formats as the kernels read them from a piece's streams, and
+// the one multiply-add order every canonical kernel shares.
 //
 // A piece of n blocks holds each stream whole, one after another
 // (src/core/formats/device_layout.h:111-136):
@@ -12,12 +12,21 @@
 //                               weights m, m + 8, m + 16, m + 24 at bits 0, 2, 4, 6
 //         scales  [192n, 208n)  int8, two a group: weights 0..15, then 16..31
 //         d       [208n, 210n)  fp16 a super-block of 8 groups
+//   Q4_1  codes   [0, 16n)      as Q4_0's
+//         d, m    [16n, 20n)    fp16 d then fp16 m, one dword a block
+//   Q8_0  codes   [0, 32n)      32 int8 a block, weight j at byte j
+//         scales  [32n, 34n)    fp16 d a block
+//   F32   floats  [0, 4n)       a "block" is one weight (the gather's tables)
 // Groups are counted flat over the piece — group gi is row gi / G's group
 // gi % G — so a Q6_K row need not be whole super-blocks (q6_k.wgsl:13-42).
 //
 // Every weight decodes exactly: (q - 8) d and (d sc)(q - 32) are products of
 // at most 24 significant bits, so fma(q, d, -8d) and fma(q, d sc, -32 d sc)
 // return them exactly, one instruction a weight after the code's conversion.
+// Q8_0's q d is exact likewise. Q4_1's q d + m rounds once, at the add: q d
+// (4 + 11 significant bits) is exact, so fma(q, d, m) is both of the
+// reference's admissible answers, the multiply-add rounded twice and fused
+// (q4_1_reference.h), which are always the same bits.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -25,11 +34,15 @@
 
 namespace chm {
 
-enum Format : uint32_t { kQ4_0 = 2, kQ6_K = 14 };
+enum Format : uint32_t { kF32 = 0, kQ4_0 = 2, kQ4_1 = 3, kQ8_0 = 8, kQ6_K = 14 };
 
-// Bytes a stored block, and weights a block.
-constexpr uint32_t block_bytes(uint32_t f) { return f == kQ4_0 ? 18u : f == kQ6_K ? 210u : 0u; }
-constexpr uint32_t block_weights(uint32_t f) { return f == kQ4_0 ? 32u : f == kQ6_K ? 256u : 0u; }
+// Bytes a stored block, and weights a block (src/core/gguf/types.h:65-101).
+constexpr uint32_t block_bytes(uint32_t f) {
+    return f == kF32 ? 4u : f == kQ4_0 ? 18u : f == kQ4_1 ? 20u : f == kQ8_0 ? 34u : f == kQ6_K ? 210u : 0u;
+}
+constexpr uint32_t block_weights(uint32_t f) {
+    return f == kF32 ? 1u : f == kQ4_0 || f == kQ4_1 || f == kQ8_0 ? 32u : f == kQ6_K ? 256u : 0u;
+}
 
 // binary16 bits -> binary32, exact for every finite input, subnormals
 // included (the f16 denormal mode is left at its IEEE default).
@@ -80,6 +93,45 @@ __device__ __forceinline__ Q6_KGroup load_q6_k(const uint8_t* piece, uint64_t n,
     return g;
 }
 
+struct Q4_1Group {
+    uint32_t w[4];
+    float d, m;
+};
+
+struct Q8_0Group {
+    uint32_t w[8];
+    float d;
+};
+
+__device__ __forceinline__ Q4_1Group load_q4_1(const uint8_t* piece, uint64_t n, uint64_t gi) {
+    Q4_1Group g;
+    const uint4 c = *reinterpret_cast<const uint4*>(piece + 16 * gi);
+    const uint32_t dm = *reinterpret_cast<const uint32_t*>(piece + 16 * n + 4 * gi);
+    g.w[0] = c.x;
+    g.w[1] = c.y;
+    g.w[2] = c.z;
+    g.w[3] = c.w;
+    g.d = half_to_float(dm & 0xFFFFu);
+    g.m = half_to_float(dm >> 16);
+    return g;
+}
+
+__device__ __forceinline__ Q8_0Group load_q8_0(const uint8_t* piece, uint64_t n, uint64_t gi) {
+    Q8_0Group g;
+    const uint4* c = reinterpret_cast<const uint4*>(piece + 32 * gi);
+    const uint4 a = c[0], b = c[1];
+    g.w[0] = a.x;
+    g.w[1] = a.y;
+    g.w[2] = a.z;
+    g.w[3] = a.w;
+    g.w[4] = b.x;
+    g.w[5] = b.y;
+    g.w[6] = b.z;
+    g.w[7] = b.w;
+    g.d = half_to_float(*reinterpret_cast<const uint16_t*>(piece + 32 * n + 2 * gi));
+    return g;
+}
+
 // Weight l (0..31) of a group, exact.
 __device__ __forceinline__ float weight(const Q4_0Group& g, int l) {
     const uint32_t q = (g.w[(l & 15) >> 2] >> (8 * (l & 3) + 4 * (l >> 4))) & 0xFu;
@@ -102,10 +154,24 @@ __device__ __forceinline__ float chain(const G& g, const float* x, float s) {
     return s;
 }
 
+__device__ __forceinline__ float weight(const Q4_1Group& g, int l) {
+    const uint32_t q = (g.w[(l & 15) >> 2] >> (8 * (l & 3) + 4 * (l >> 4))) & 0xFu;
+    return __builtin_fmaf(static_cast<float>(q), g.d, g.m);
+}
+
+__device__ __forceinline__ float weight(const Q8_0Group& g, int l) {
+    const int32_t q = static_cast<int8_t>((g.w[l >> 2] >> (8 * (l & 3))) & 0xFFu);
+    return static_cast<float>(q) * g.d;
+}
+
 template <uint32_t F>
 __device__ __forceinline__ float chain_group(const uint8_t* piece, uint64_t n, uint64_t gi, const float* x, float s) {
     if constexpr (F == kQ4_0) {
         return chain(load_q4_0(piece, n, gi), x, s);
+    } else if constexpr (F == kQ4_1) {
+        return chain(load_q4_1(piece, n, gi), x, s);
+    } else if constexpr (F == kQ8_0) {
+        return chain(load_q8_0(piece, n, gi), x, s);
     } else {
         return chain(load_q6_k(piece, n, gi), x, s);
     }
@@ -118,10 +184,54 @@ __device__ __forceinline__ void unpack(const uint8_t* piece, uint64_t n, uint64_
         const Q4_0Group g = load_q4_0(piece, n, gi);
 #pragma unroll
         for (int l = 0; l < 32; ++l) out[l] = weight(g, l);
+    } else if constexpr (F == kQ4_1) {
+        const Q4_1Group g = load_q4_1(piece, n, gi);
+#pragma unroll
+        for (int l = 0; l < 32; ++l) out[l] = weight(g, l);
+    } else if constexpr (F == kQ8_0) {
+        const Q8_0Group g = load_q8_0(piece, n, gi);
+#pragma unroll
+        for (int l = 0; l < 32; ++l) out[l] = weight(g, l);
+    } else if constexpr (F == kF32) {
+        const float4* f = reinterpret_cast<const float4*>(piece + 128 * gi);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            const float4 q = f[v];
+            out[4 * v] = q.x;
+            out[4 * v + 1] = q.y;
+            out[4 * v + 2] = q.z;
+            out[4 * v + 3] = q.w;
+        }
     } else {
         const Q6_KGroup g = load_q6_k(piece, n, gi);
 #pragma unroll
         for (int l = 0; l < 32; ++l) out[l] = weight(g, l);
+    }
+}
+
+// Weights 16 h .. 16 h + 15 (h = 0, 1) of group gi, exact: what one of a
+// group's two staging lanes decodes in the prefill tile.
+template <uint32_t F>
+__device__ __forceinline__ void unpack_half(const uint8_t* piece, uint64_t n, uint64_t gi, uint32_t h, float* w) {
+    if constexpr (F == kQ4_0) {
+        const Q4_0Group q = load_q4_0(piece, n, gi);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) w[j] = weight(q, 16 * h + j);
+    } else if constexpr (F == kQ4_1) {
+        const Q4_1Group q = load_q4_1(piece, n, gi);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) w[j] = weight(q, 16 * h + j);
+    } else if constexpr (F == kQ8_0) {
+        const uint4 c = *reinterpret_cast<const uint4*>(piece + 32 * gi + 16 * h);
+        const float d = half_to_float(*reinterpret_cast<const uint16_t*>(piece + 32 * n + 2 * gi));
+        const uint32_t words[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            w[j] = static_cast<float>(static_cast<int32_t>(static_cast<int8_t>((words[j >> 2] >> (8 * (j & 3))) & 0xFFu))) * d;
+    } else {
+        const Q6_KGroup q = load_q6_k(piece, n, gi);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) w[j] = weight(q, 16 * h + j);
     }
 }
 

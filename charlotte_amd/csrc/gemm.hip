@@ -75,15 +75,7 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
             float w[16];
             if (slive) {
                 const uint64_t gi = static_cast<uint64_t>(spiece.row) * G + g;
-                if constexpr (F == kQ4_0) {
-                    const Q4_0Group q = load_q4_0(spiece.piece, spiece.blocks, gi);
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) w[j] = weight(q, 16 * shalf + j);
-                } else {
-                    const Q6_KGroup q = load_q6_k(spiece.piece, spiece.blocks, gi);
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) w[j] = weight(q, 16 * shalf + j);
-                }
+                unpack_half<F>(spiece.piece, spiece.blocks, gi, shalf, w);
             } else {
 #pragma unroll
                 for (int j = 0; j < 16; ++j) w[j] = 0.0f;
@@ -215,12 +207,25 @@ hipError_t launch_gemm_canonical(const Product& a, uint32_t format, uint32_t com
         chunks = 2;
         while (chunks < 32 && token_tiles * row_tiles * chunks < 2 * compute_units) chunks *= 2;
     }
-    if (format == kQ4_0) {
-        wide ? go<kQ4_0, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-             : go<kQ4_0, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
-    } else {
-        wide ? go<kQ6_K, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-             : go<kQ6_K, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
+    switch (format) {
+        case kQ4_0:
+            wide ? go<kQ4_0, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
+                 : go<kQ4_0, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
+            break;
+        case kQ4_1:
+            wide ? go<kQ4_1, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
+                 : go<kQ4_1, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
+            break;
+        case kQ8_0:
+            wide ? go<kQ8_0, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
+                 : go<kQ8_0, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
+            break;
+        case kQ6_K:
+            wide ? go<kQ6_K, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
+                 : go<kQ6_K, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
+            break;
+        default:
+            return hipErrorInvalidValue;
     }
     if (range_sums) {
         const uint64_t outputs = static_cast<uint64_t>(a.tokens) * a.rows;

@@ -162,11 +162,18 @@ __global__ __launch_bounds__(256, CHM_RANGES_MIN_BLOCKS) void gemv_ranges(Produc
     }
 }
 
-// Q6_K's 9 groups from a lane's run: lo, hi, scales contiguous from group gi0,
-// and the two super-blocks' d the run touches (9 groups from gi0 = 9m span
-// super-blocks gi0 / 8 and gi0 / 8 + 1).
+// A lane's run of SPAN groups from gi0. Q4_0 and Q6_K load a run's streams in
+// few wide loads (below); Q4_1 and Q8_0 load each group as the L = 32 kernel
+// does.
 template <uint32_t F, int SPAN>
-struct Run;
+struct Run {
+    Raw<F> g[SPAN];
+    __device__ __forceinline__ void load(const uint8_t* piece, uint64_t n, uint64_t gi0) {
+#pragma unroll
+        for (int i = 0; i < SPAN; ++i) g[i].load(piece, n, gi0 + i);
+    }
+    __device__ __forceinline__ float chain(int i, uint64_t, const float* x, float s) const { return g[i].chain(x, s); }
+};
 
 template <int SPAN>
 struct Run<kQ4_0, SPAN> {
@@ -190,6 +197,9 @@ struct Run<kQ4_0, SPAN> {
     }
 };
 
+// Q6_K's 9 groups from a lane's run: lo, hi, scales contiguous from group gi0,
+// and the two super-blocks' d the run touches (9 groups from gi0 = 9m span
+// super-blocks gi0 / 8 and gi0 / 8 + 1).
 template <int SPAN>
 struct Run<kQ6_K, SPAN> {
     // The lane's run of SPAN groups in few wide loads:
@@ -487,8 +497,13 @@ hipError_t launch_gemv(const Product& a, uint32_t format, uint32_t compute_units
     if (CHM_GEMV_STREAM && gemv_stream_takes(a, format)) return launch_gemv_stream(a, compute_units, stream);
     GemvPlan plan;
     if (!gemv_plan(a.rows, a.groups, compute_units, &plan)) return hipErrorInvalidValue;
-    if (format == kQ4_0) return launch_format<kQ4_0>(a, plan, compute_units, stream);
-    return launch_format<kQ6_K>(a, plan, compute_units, stream);
+    switch (format) {
+        case kQ4_0: return launch_format<kQ4_0>(a, plan, compute_units, stream);
+        case kQ4_1: return launch_format<kQ4_1>(a, plan, compute_units, stream);
+        case kQ8_0: return launch_format<kQ8_0>(a, plan, compute_units, stream);
+        case kQ6_K: return launch_format<kQ6_K>(a, plan, compute_units, stream);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace chm

@@ -106,14 +106,25 @@ int chx_unpack(uint32_t type, const void* piece, uint64_t blocks_in_piece, uint6
     if (reinterpret_cast<uintptr_t>(piece) % 16 != 0) return hipErrorInvalidValue;
     const dim3 grid(static_cast<uint32_t>((groups + 63) / 64));
     const auto* p = static_cast<const uint8_t*>(piece);
-    if (type == chm::kQ4_0) {
-        hipLaunchKernelGGL((unpack_kernel<chm::kQ4_0>), grid, dim3(64), 0, static_cast<hipStream_t>(s), p,
-                           blocks_in_piece, groups, out);
-    } else if (type == chm::kQ6_K) {
-        hipLaunchKernelGGL((unpack_kernel<chm::kQ6_K>), grid, dim3(64), 0, static_cast<hipStream_t>(s), p,
-                           blocks_in_piece, groups, out);
-    } else {
-        return hipErrorInvalidValue;
+    const auto stream = static_cast<hipStream_t>(s);
+    switch (type) {
+        case chm::kF32:
+            hipLaunchKernelGGL((unpack_kernel<chm::kF32>), grid, dim3(64), 0, stream, p, blocks_in_piece, groups, out);
+            break;
+        case chm::kQ4_0:
+            hipLaunchKernelGGL((unpack_kernel<chm::kQ4_0>), grid, dim3(64), 0, stream, p, blocks_in_piece, groups, out);
+            break;
+        case chm::kQ4_1:
+            hipLaunchKernelGGL((unpack_kernel<chm::kQ4_1>), grid, dim3(64), 0, stream, p, blocks_in_piece, groups, out);
+            break;
+        case chm::kQ8_0:
+            hipLaunchKernelGGL((unpack_kernel<chm::kQ8_0>), grid, dim3(64), 0, stream, p, blocks_in_piece, groups, out);
+            break;
+        case chm::kQ6_K:
+            hipLaunchKernelGGL((unpack_kernel<chm::kQ6_K>), grid, dim3(64), 0, stream, p, blocks_in_piece, groups, out);
+            break;
+        default:
+            return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }

@@ -3,7 +3,8 @@
 // 194-205; formats/q6_k/q6_k_repack.cpp:52-87).
 //
 // Q4_0: a piece is every block's 16 code bytes, then every block's fp16
-// scale. Q6_K: each super-block repacked so a 32-weight group's bits lie
+// scale; Q4_1 its 16 code bytes, then its d and m, a dword a block; Q8_0 its
+// 32 code bytes, then its fp16 scale; F32 the floats as stored. Q6_K: each super-block repacked so a 32-weight group's bits lie
 // together — its low nibbles in 16 bytes (byte j: weight j's nibble, then
 // weight j + 16's), its high pairs in 8 (byte m: weights m, m + 8, m + 16,
 // m + 24 at bits 0, 2, 4, 6) — the piece being every block's lo, then hi, then
@@ -63,6 +64,17 @@ static void gather_q4_0_range(const uint8_t* stored, uint64_t begin, uint64_t en
     }
 }
 
+// Codes, then the block's leading `head` bytes (its scales), for the formats
+// whose streams are the stored block's fields (device_layout.h:121-123).
+static void split_range(const uint8_t* stored, uint64_t begin, uint64_t end, uint64_t n, uint32_t head,
+                        uint32_t codes, uint8_t* device) {
+    const uint32_t block = head + codes;
+    for (uint64_t b = begin; b < end; ++b) {
+        std::memcpy(device + codes * b, stored + block * b + head, codes);
+        std::memcpy(device + codes * n + head * b, stored + block * b, head);
+    }
+}
+
 // Blocks a thread takes at least, so small tensors stay on one thread.
 constexpr uint64_t kBlocksAThread = 1u << 14;
 
@@ -92,6 +104,15 @@ bool lay_out(uint32_t format, const uint8_t* stored, uint64_t blocks, uint8_t* d
     std::memset(device + stored_bytes, 0, total - stored_bytes);
     if (format == 2) {
         over_threads(blocks, [&](uint64_t b0, uint64_t b1) { gather_q4_0_range(stored, b0, b1, blocks, device); });
+        return true;
+    }
+    if (format == 3 || format == 8) {
+        const uint32_t head = format == 3 ? 4 : 2, codes = format == 3 ? 16 : 32;
+        over_threads(blocks, [&](uint64_t b0, uint64_t b1) { split_range(stored, b0, b1, blocks, head, codes, device); });
+        return true;
+    }
+    if (format == 0) {
+        std::memcpy(device, stored, 4 * blocks);
         return true;
     }
     if (format == 14) {

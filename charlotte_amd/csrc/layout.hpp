@@ -10,8 +10,13 @@ namespace chm {
 
 struct Product;
 
-constexpr uint32_t block_bytes_host(uint32_t f) { return f == 2 ? 18u : f == 14 ? 210u : 0u; }
-constexpr uint32_t block_weights_host(uint32_t f) { return f == 2 ? 32u : f == 14 ? 256u : 0u; }
+// GGUF types 0 F32, 2 Q4_0, 3 Q4_1, 8 Q8_0, 14 Q6_K (src/core/gguf/types.h:65-101).
+constexpr uint32_t block_bytes_host(uint32_t f) {
+    return f == 0 ? 4u : f == 2 ? 18u : f == 3 ? 20u : f == 8 ? 34u : f == 14 ? 210u : 0u;
+}
+constexpr uint32_t block_weights_host(uint32_t f) {
+    return f == 0 ? 1u : f == 2 || f == 3 || f == 8 ? 32u : f == 14 ? 256u : 0u;
+}
 
 uint64_t layout_bytes(uint32_t format, uint64_t blocks);
 bool lay_out(uint32_t format, const uint8_t* stored, uint64_t blocks, uint8_t* device);

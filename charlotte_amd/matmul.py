@@ -38,8 +38,16 @@ class Status(enum.IntEnum):
 
 
 class TensorType(enum.IntEnum):
+    F32 = 0
     Q4_0 = 2
+    Q4_1 = 3
+    Q8_0 = 8
     Q6_K = 14
+
+
+# Weights a block of each type (src/core/gguf/types.h:65-101).
+BLOCK_WEIGHTS = {TensorType.F32: 1, TensorType.Q4_0: 32, TensorType.Q4_1: 32, TensorType.Q8_0: 32,
+                 TensorType.Q6_K: 256}
 
 
 class Epilogue(enum.IntEnum):
@@ -120,6 +128,19 @@ class _Desc(ctypes.Structure):
     ]
 
 
+class _GatherDesc(ctypes.Structure):
+    _fields_ = [
+        ("table", ctypes.c_void_p),
+        ("first_row", ctypes.c_uint64),
+        ("ids", ctypes.c_void_p),
+        ("fed", ctypes.c_void_p),
+        ("media", ctypes.c_uint32),
+        ("media_token", ctypes.c_uint32),
+        ("scale", ctypes.c_float),
+        ("hidden", ctypes.c_void_p),
+    ]
+
+
 class _GgufTensor(ctypes.Structure):
     _fields_ = [
         ("name", ctypes.c_char_p),
@@ -160,6 +181,11 @@ SIGNATURES = {
     ),
     "charlotte_hip_matmul_split_tokens": (_c.c_uint32, [_c.c_uint32, _c.c_uint64, _c.c_uint64, _Gate]),
     "charlotte_hip_matmul_range_sum_floats": (_c.c_uint64, [_c.c_uint32, _c.c_uint64, _c.c_uint64, _Gate]),
+    "charlotte_hip_matmul_gather": (_c.c_int, [_c.c_void_p, _c.POINTER(_GatherDesc), _c.c_uint32, _c.c_void_p]),
+    "charlotte_hip_matmul_gather_positions": (
+        _c.c_int,
+        [_c.c_void_p, _c.c_void_p, _c.c_uint32, _c.c_uint32, _c.c_uint32, _c.c_void_p, _c.c_void_p],
+    ),
     "charlotte_hip_matmul_gguf_open": (_c.c_int, [_c.c_char_p, _c.POINTER(_c.c_void_p), _c.POINTER(_c.c_uint32)]),
     "charlotte_hip_matmul_gguf_read": (
         _c.c_int,
@@ -214,7 +240,7 @@ def layout_bytes(gguf_type, rows, columns):
 
 def lay_out(gguf_type, stored: bytes, blocks: int) -> bytes:
     """File-order blocks -> the device layout, on the host."""
-    per = {TensorType.Q4_0: 32, TensorType.Q6_K: 256}[TensorType(gguf_type)]
+    per = BLOCK_WEIGHTS[TensorType(gguf_type)]
     out = ctypes.create_string_buffer(layout_bytes(gguf_type, 1, per * blocks) if blocks else 0)
     src = ctypes.create_string_buffer(bytes(stored), len(stored))
     s = lib.charlotte_hip_matmul_lay_out(int(gguf_type), src, blocks, out)
@@ -344,6 +370,27 @@ def launch(ctx: Context, m: MatmulLaunch, tokens: int, gate: SplitGate = kNever,
         m._desc = m.desc()
     ctx.check(lib.charlotte_hip_matmul_launch(ctx.handle, ctypes.byref(m._desc), _gate(gate), range_sums,
                                               range_sums_bytes, tokens, stream))
+
+
+# ---- the embedding gather (src/core/kernels/gather/gather.h:126-145) ------------
+
+
+def gather(ctx: Context, table: Weight, ids: int, tokens: int, hidden: int, first_row=0, fed=0, media=False,
+           media_token=0, scale=1.0, stream=None):
+    """Rows of `hidden` from the table rows of the step's tokens (gather.wgsl:21-58).
+
+    `ids`, `fed` and `hidden` are device pointers; `fed` (or 0) is a fed step's
+    draw record, whose first word is every row's token."""
+    d = _GatherDesc(table.handle, first_row, ids, fed, int(bool(media)), media_token, scale, hidden)
+    ctx.check(lib.charlotte_hip_matmul_gather(ctx.handle, ctypes.byref(d), tokens, stream))
+
+
+def gather_positions(ctx: Context, table: Weight, positions: int, grid_columns: int, tokens: int, output: int,
+                     stream=None):
+    """A vision step's learned positions (gather.wgsl:65-84): row r is table row
+    r % grid_columns plus table row positions + r // grid_columns."""
+    ctx.check(lib.charlotte_hip_matmul_gather_positions(ctx.handle, table.handle, positions, grid_columns, tokens,
+                                                        output, stream))
 
 
 # ---- GGUF files (gguf::read_index, src/core/gguf/reader.cpp) -----------------

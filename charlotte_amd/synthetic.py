@@ -10,6 +10,10 @@ order — what a GGUF file holds and charlotte_hip_matmul_weight_upload takes.
         weight l of group k = 4h + r low nibble at nibble r/2 of
         ql[64h + 32(r%2) + l], high pair at bits 2r of qh[32h + l] (ggml's
         block_q6_K).
+  Q4_1: d = fp16(|N(0,1)| * 0.02), m = fp16(-8 d), codes uniform 0..15;
+        block = d, m, then 16 code bytes as Q4_0's.
+  Q8_0: d = fp16(|N(0,1)| * 0.0005), codes uniform -128..127;
+        block = d then 32 int8 codes.
   x:    f32 N(0,1).
 """
 
@@ -49,8 +53,33 @@ def q6_k(rng: np.random.Generator, rows: int, columns: int) -> bytes:
     return q6_k_from_codes(codes, scales, d)
 
 
+def q4_1(rng: np.random.Generator, rows: int, columns: int) -> bytes:
+    n = rows * columns // 32
+    d = (np.abs(rng.standard_normal(n, dtype=np.float32)) * np.float32(0.02)).astype(np.float16)
+    m = (d.astype(np.float32) * np.float32(-8.0)).astype(np.float16)
+    codes = rng.integers(0, 16, size=(n, 32), dtype=np.uint8)
+    blocks = np.empty((n, 20), np.uint8)
+    blocks[:, 0:2] = d.view(np.uint8).reshape(n, 2)
+    blocks[:, 2:4] = m.view(np.uint8).reshape(n, 2)
+    blocks[:, 4:20] = codes[:, :16] | (codes[:, 16:] << 4)
+    return blocks.tobytes()
+
+
+def q8_0(rng: np.random.Generator, rows: int, columns: int) -> bytes:
+    n = rows * columns // 32
+    d = (np.abs(rng.standard_normal(n, dtype=np.float32)) * np.float32(0.0005)).astype(np.float16)
+    blocks = np.empty((n, 34), np.uint8)
+    blocks[:, 0:2] = d.view(np.uint8).reshape(n, 2)
+    blocks[:, 2:34] = rng.integers(-128, 128, size=(n, 32), dtype=np.int16).astype(np.int8).view(np.uint8)
+    return blocks.tobytes()
+
+
+_MAKERS = {2: q4_0, 3: q4_1, 8: q8_0, 14: q6_k}
+_BLOCKS = {2: (32, 18), 3: (32, 20), 8: (32, 34), 14: (256, 210)}
+
+
 def weight(rng, gguf_type: int, rows: int, columns: int) -> bytes:
-    return q4_0(rng, rows, columns) if gguf_type == 2 else q6_k(rng, rows, columns)
+    return _MAKERS[gguf_type](rng, rows, columns)
 
 
 def activations(rng: np.random.Generator, tokens: int, columns: int) -> np.ndarray:
@@ -58,4 +87,5 @@ def activations(rng: np.random.Generator, tokens: int, columns: int) -> np.ndarr
 
 
 def stored_bytes(gguf_type: int, rows: int, columns: int) -> int:
-    return rows * columns // 32 * 18 if gguf_type == 2 else rows * columns // 256 * 210
+    per, nbytes = _BLOCKS[gguf_type]
+    return rows * columns // per * nbytes

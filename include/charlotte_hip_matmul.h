@@ -4,10 +4,11 @@
  *
  *   y[t][o] = sum_k W[o][k] * x[t][k]
  *
- * W stays in its GGUF format (Q4_0, or Q6_K repacked) in device memory and is
- * decoded in the kernels' load path; x and y are f32. One token runs the
- * decode form (a matrix-vector product bound by HBM), more tokens the prefill
- * form (a tiled matrix product).
+ * W stays in its GGUF format (Q4_0, Q4_1, Q8_0, or Q6_K repacked) in device
+ * memory and is decoded in the kernels' load path; x and y are f32. One token
+ * runs the decode form (a matrix-vector product bound by HBM), more tokens the
+ * prefill form (a tiled matrix product). The embedding gather decodes table
+ * rows through the same formats (and F32).
  *
  * What each part replaces in the reference (paths relative to its root):
  *   charlotte_hip_matmul_desc       kernels::MatmulLaunch  src/core/kernels/matmul/matmul.h:602-632
@@ -27,6 +28,10 @@
  *   charlotte_hip_matmul_status     kernels::ProgramError  src/core/kernels/program.h:159-169
  *   charlotte_hip_matmul_gguf_*     gguf::read_index, gguf::TensorEntry, gguf::ReadError
  *                                                          src/core/gguf/reader.h:14-29, types.h:112-141, 191-243
+ *   charlotte_hip_matmul_gather     kernels::gather_launches + Program::run
+ *                                                          src/core/kernels/gather/gather.h:126-136, gather.wgsl:21-58
+ *   charlotte_hip_matmul_gather_positions
+ *                                   kernels::position_launch  gather.h:138-145, gather.wgsl:65-84
  *
  * Conventions: every function returns a status and never throws; a failure
  * names its subject in charlotte_hip_matmul_last_error(ctx). A context owns
@@ -69,9 +74,13 @@ typedef enum {
     CHARLOTTE_HIP_MATMUL_IO_ERROR = 9           /* a file that cannot be opened or mapped */
 } charlotte_hip_matmul_status;
 
-/* GGUF tensor types the kernels read (src/core/gguf/types.h:41-43). */
+/* GGUF tensor types the kernels read (src/core/gguf/types.h:39-47). The
+ * products read the four quantized formats; F32 is a gather's table only. */
 enum {
+    CHARLOTTE_HIP_MATMUL_F32 = 0,
     CHARLOTTE_HIP_MATMUL_Q4_0 = 2,
+    CHARLOTTE_HIP_MATMUL_Q4_1 = 3,
+    CHARLOTTE_HIP_MATMUL_Q8_0 = 8,
     CHARLOTTE_HIP_MATMUL_Q6_K = 14
 };
 
@@ -139,10 +148,11 @@ uint64_t charlotte_hip_matmul_workspace_bytes(uint32_t tokens, uint64_t columns)
  * the stored bytes rounded up to 4 (device_layout.h:59-63). 0 when the type is
  * not one of the above or the shape is not whole blocks. */
 uint64_t charlotte_hip_matmul_layout_bytes(uint32_t gguf_type, uint64_t rows, uint64_t columns);
-/* File-order blocks -> the piece's streams, in host memory: Q4_0 as its codes
- * then its scales (device_layout.h:121), Q6_K repacked, then its lo, hi,
- * scales and d streams (device_layout.h:124-127, q6_k.h:11-21). `device` holds
- * layout_bytes(...) bytes. */
+/* File-order blocks -> the piece's streams, in host memory: Q4_0 and Q8_0 as
+ * their codes then their scales, Q4_1 as its codes then its d and m words
+ * (device_layout.h:121-123), Q6_K repacked, then its lo, hi, scales and d
+ * streams (device_layout.h:124-127, q6_k.h:11-21), F32 as stored. `device`
+ * holds layout_bytes(...) bytes. */
 charlotte_hip_matmul_status charlotte_hip_matmul_lay_out(uint32_t gguf_type, const void* stored_blocks,
                                                          uint64_t blocks, void* device);
 /* The Q6_K repack alone, block i's stream s at streams[s] + i * width(s),
@@ -234,6 +244,43 @@ uint32_t charlotte_hip_matmul_split_tokens(uint32_t epilogue, uint64_t rows, uin
                                            charlotte_hip_matmul_split_gate gate);
 uint64_t charlotte_hip_matmul_range_sum_floats(uint32_t epilogue, uint64_t rows, uint64_t columns,
                                                charlotte_hip_matmul_split_gate gate);
+
+/* ---- the embedding gather (src/core/kernels/gather/gather.h) ------------------- */
+
+/* Each token of a step becomes its row of the token embedding table, decoded
+ * and multiplied by `scale`, in `hidden` (gather.wgsl:21-58). `table` is a
+ * piece of the table holding vocabulary rows first_row .. first_row +
+ * table rows - 1, in any format above; a table split into pieces takes one
+ * call a piece, each writing the rows whose token it holds and leaving the
+ * others as they are. With scale 1 every weight is the format's decode bit
+ * for bit; with another, the decoded weight times the scale, rounded once
+ * (llama.cpp's decode-then-scale). */
+typedef struct {
+    const charlotte_hip_matmul_weight* table;
+    uint64_t first_row;
+    const uint32_t* ids;   /* device: the step's `tokens` identifiers (unread when fed) */
+    /* device or NULL: a fed step's draw record (sampler.h); its first word is
+     * every row's token in place of ids, never compared with media_token */
+    const uint32_t* fed;
+    uint32_t media;        /* nonzero: a row whose identifier is media_token is left as it is */
+    uint32_t media_token;
+    float scale;
+    float* hidden;         /* device, 16-byte aligned: tokens rows of the table's columns floats */
+} charlotte_hip_matmul_gather_desc;
+
+charlotte_hip_matmul_status charlotte_hip_matmul_gather(charlotte_hip_matmul_context* ctx,
+                                                        const charlotte_hip_matmul_gather_desc* desc,
+                                                        uint32_t tokens, void* stream);
+
+/* The position form (gather.wgsl:65-84): patch row r of a vision step, at
+ * column x = r % grid_columns and row y = r / grid_columns of its grid, is
+ * the table's row x plus its row positions + y, written to `output`. `table`
+ * is F32 of 2 x positions rows; grid_columns <= positions and tokens <=
+ * grid_columns * positions. */
+charlotte_hip_matmul_status charlotte_hip_matmul_gather_positions(charlotte_hip_matmul_context* ctx,
+                                                                  const charlotte_hip_matmul_weight* table,
+                                                                  uint32_t positions, uint32_t grid_columns,
+                                                                  uint32_t tokens, float* output, void* stream);
 
 /* ---- GGUF files (gguf::read_index, src/core/gguf/reader.cpp) -------------------- */
 

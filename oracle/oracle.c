@@ -83,9 +83,52 @@ void orc_dequantize_q6_k(const uint8_t* blocks, uint64_t nblocks, float* out) {
     }
 }
 
+/* ggml's dequantize_row_q4_1 as tests/support/q4_1_reference.h:27-54 mirrors
+ * it: a 20-byte block is fp16 d, fp16 m, then 16 code bytes; weight j is
+ * (qs[j] & 0xF) * d + m and weight j + 16 is (qs[j] >> 4) * d + m. The
+ * reference keeps two answers, the multiply and the add each rounded
+ * (`rounded`) and one fma (`fused`); `fused` may be NULL. Either is written
+ * out explicitly here. (The 4-bit code times the 11-bit d is exact in f32, so
+ * the two agree on every block; the tests check that rather than assume it.) */
+void orc_dequantize_q4_1(const uint8_t* blocks, uint64_t nblocks, float* rounded, float* fused) {
+    for (uint64_t b = 0; b < nblocks; ++b) {
+        const uint8_t* block = blocks + b * 20;
+        const float d = orc_fp16_to_fp32(le16(block));
+        const float m = orc_fp16_to_fp32(le16(block + 2));
+        for (int j = 0; j < 16; ++j) {
+            const float lo = (float)(block[4 + j] & 0x0F);
+            const float hi = (float)(block[4 + j] >> 4);
+            const float lo_d = lo * d;
+            const float hi_d = hi * d;
+            rounded[b * 32 + j] = lo_d + m;
+            rounded[b * 32 + j + 16] = hi_d + m;
+            if (fused) {
+                fused[b * 32 + j] = fmaf(lo, d, m);
+                fused[b * 32 + j + 16] = fmaf(hi, d, m);
+            }
+        }
+    }
+}
+
+/* ggml's dequantize_row_q8_0 as tests/support/q8_0_reference.h:14-27 mirrors
+ * it: a 34-byte block is fp16 d, then 32 signed 8-bit codes; weight j is
+ * qs[j] * d. */
+void orc_dequantize_q8_0(const uint8_t* blocks, uint64_t nblocks, float* out) {
+    for (uint64_t b = 0; b < nblocks; ++b) {
+        const uint8_t* block = blocks + b * 34;
+        const float d = orc_fp16_to_fp32(le16(block));
+        for (int j = 0; j < 32; ++j) out[b * 32 + j] = (float)(int8_t)block[2 + j] * d;
+    }
+}
+
+/* src/core/gguf/types.h:65-101: weights a block and bytes a block. F32's
+ * "block" is one float. */
 static int block_shape(uint32_t type, uint64_t* elements, uint64_t* bytes) {
     switch (type) {
+        case ORC_F32: *elements = 1; *bytes = 4; return 0;
         case ORC_Q4_0: *elements = 32; *bytes = 18; return 0;
+        case ORC_Q4_1: *elements = 32; *bytes = 20; return 0;
+        case ORC_Q8_0: *elements = 32; *bytes = 34; return 0;
         case ORC_Q6_K: *elements = 256; *bytes = 210; return 0;
         default: return -1;
     }
@@ -98,8 +141,16 @@ int orc_dequantize_range(uint32_t type, const uint8_t* blocks, uint64_t first, u
     const uint64_t b0 = first / per_block, b1 = (first + count - 1) / per_block;
     float* tmp = malloc((size_t)((b1 - b0 + 1) * per_block * sizeof(float)));
     if (!tmp) return -2;
-    if (type == ORC_Q4_0) orc_dequantize_q4_0(blocks + b0 * block_bytes, b1 - b0 + 1, tmp);
-    else orc_dequantize_q6_k(blocks + b0 * block_bytes, b1 - b0 + 1, tmp);
+    const uint8_t* at = blocks + b0 * block_bytes;
+    const uint64_t n = b1 - b0 + 1;
+    switch (type) {
+        case ORC_F32: memcpy(tmp, at, (size_t)(n * 4)); break;
+        case ORC_Q4_0: orc_dequantize_q4_0(at, n, tmp); break;
+        /* tests/gpu/matmul_test.cpp:153 decodes Q4_1 by its rounded answer */
+        case ORC_Q4_1: orc_dequantize_q4_1(at, n, tmp, NULL); break;
+        case ORC_Q8_0: orc_dequantize_q8_0(at, n, tmp); break;
+        default: orc_dequantize_q6_k(at, n, tmp); break;
+    }
     memcpy(out, tmp + (first - b0 * per_block), (size_t)count * sizeof(float));
     free(tmp);
     return 0;
@@ -163,6 +214,29 @@ int orc_lay_out(uint32_t type, const uint8_t* blocks, uint64_t nblocks, uint8_t*
                         device + 208 * nblocks);
         return 0;
     }
+    if (type == ORC_Q4_1) {
+        /* kQ4_1 = {{4, 16}, {0, 4}}: the codes, then d and m together, one
+         * word a block (device_layout.h:122). */
+        for (uint64_t b = 0; b < nblocks; ++b) {
+            memcpy(device + 16 * b, blocks + 20 * b + 4, 16);
+            memcpy(device + 16 * nblocks + 4 * b, blocks + 20 * b, 4);
+        }
+        return 0;
+    }
+    if (type == ORC_Q8_0) {
+        /* kQ8_0 = {{2, 32}, {0, 2}}: the codes, then the scales
+         * (device_layout.h:123). */
+        for (uint64_t b = 0; b < nblocks; ++b) {
+            memcpy(device + 32 * b, blocks + 34 * b + 2, 32);
+            memcpy(device + 32 * nblocks + 2 * b, blocks + 34 * b, 2);
+        }
+        return 0;
+    }
+    if (type == ORC_F32) {
+        /* kF32 = {{0, 4}}: the floats as stored (device_layout.h:118). */
+        memcpy(device, blocks, (size_t)(4 * nblocks));
+        return 0;
+    }
     return -1;
 }
 
@@ -193,6 +267,31 @@ int orc_unpack_group(uint32_t type, const uint8_t* device, uint64_t n, uint64_t 
             const int pair = (hi[l % 8] >> (2 * (l / 8))) & 3;
             out[l] = (l < 16 ? first : second) * (float)((low | (pair << 4)) - 32);
         }
+        return 0;
+    }
+    if (type == ORC_Q4_1) {
+        /* src/core/formats/q4_1/q4_1.wgsl:6-17; the rounded answer. */
+        const uint8_t* codes = device + 16 * group;
+        const float d = orc_fp16_to_fp32(le16(device + 16 * n + 4 * group));
+        const float m = orc_fp16_to_fp32(le16(device + 16 * n + 4 * group + 2));
+        for (int j = 0; j < 16; ++j) {
+            const float lo_d = (float)(codes[j] & 0xF) * d;
+            const float hi_d = (float)(codes[j] >> 4) * d;
+            out[j] = lo_d + m;
+            out[j + 16] = hi_d + m;
+        }
+        return 0;
+    }
+    if (type == ORC_Q8_0) {
+        /* src/core/formats/q8_0/q8_0.wgsl:6-17. */
+        const uint8_t* codes = device + 32 * group;
+        const float d = orc_fp16_to_fp32(le16(device + 32 * n + 2 * group));
+        for (int j = 0; j < 32; ++j) out[j] = (float)(int8_t)codes[j] * d;
+        return 0;
+    }
+    if (type == ORC_F32) {
+        /* src/core/formats/f32/f32.wgsl:5-13: floats 32g .. 32g + 31. */
+        memcpy(out, device + 128 * group, 128);
         return 0;
     }
     return -1;
@@ -256,7 +355,7 @@ static void* f32_rows(void* arg) {
 
 int orc_matmul_f32(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t columns, const float* x,
                    uint32_t tokens, float* y, uint32_t threads) {
-    if (columns % 32 != 0 || (type != ORC_Q4_0 && type != ORC_Q6_K)) return -1;
+    if (columns % 32 != 0 || (type != ORC_Q4_0 && type != ORC_Q6_K && type != ORC_Q4_1 && type != ORC_Q8_0)) return -1;
     if (threads < 1) threads = 1;
     if (threads > 256) threads = 256;
     struct f32_job jobs[256];
@@ -402,6 +501,52 @@ void orc_gated(const float* gate, const float* up, uint64_t count, const float* 
 /* matmul.wgsl:347-351 (gated_by_input): the activation of the total times u. */
 void orc_gated_by_input(const float* totals, const float* u, uint64_t count, uint32_t activation, float* out) {
     for (uint64_t i = 0; i < count; ++i) out[i] = orc_activate(activation, totals[i]) * u[i];
+}
+
+/* ---- the embedding gather ------------------------------------------------ */
+
+/* src/core/kernels/gather/gather.wgsl:21-58 over a piece of `row_count` table
+ * rows of `columns` weights holding vocabulary rows first_row ..: row i of
+ * `hidden` is its token's row, each weight decoded, then multiplied by
+ * `scale` (tests/gpu/gather_test.cpp:130-152: the format's CPU reference times
+ * the scale). A token is fed[0] when `fed` is not NULL, else ids[i]; with
+ * `media`, a row whose id is media_token is left as it was; a token outside
+ * the piece leaves its row as it was. */
+int orc_gather(uint32_t type, const uint8_t* stored_rows, uint64_t row_count, uint64_t columns, uint64_t first_row,
+               const uint32_t* ids, uint32_t tokens, const uint32_t* fed, int media, uint32_t media_token,
+               float scale, float* hidden) {
+    uint64_t per_block, block_bytes;
+    if (block_shape(type, &per_block, &block_bytes) != 0 || columns % per_block != 0) return -1;
+    const uint64_t row_bytes = columns / per_block * block_bytes;
+    float* w = malloc((size_t)(columns * sizeof(float)));
+    if (!w) return -2;
+    for (uint32_t i = 0; i < tokens; ++i) {
+        uint32_t token;
+        if (fed) {
+            token = fed[0];
+        } else {
+            token = ids[i];
+            if (media && token == media_token) continue;
+        }
+        if (token < first_row || token - first_row >= row_count) continue;
+        orc_dequantize_range(type, stored_rows + (token - first_row) * row_bytes, 0, columns, w);
+        for (uint64_t c = 0; c < columns; ++c) hidden[(uint64_t)i * columns + c] = w[c] * scale;
+    }
+    free(w);
+    return 0;
+}
+
+/* gather.wgsl:65-84 (the position form): patch row r, at x = r % grid_columns
+ * and y = r / grid_columns, is table row x plus table row positions + y. */
+int orc_gather_positions(const float* table, uint64_t columns, uint32_t positions, uint32_t grid_columns,
+                         uint32_t tokens, float* out) {
+    if (grid_columns == 0) return -1;
+    for (uint32_t r = 0; r < tokens; ++r) {
+        const uint64_t x = r % grid_columns, y = r / grid_columns;
+        for (uint64_t c = 0; c < columns; ++c)
+            out[(uint64_t)r * columns + c] = table[x * columns + c] + table[(positions + y) * columns + c];
+    }
+    return 0;
 }
 
 double orc_now(void) {

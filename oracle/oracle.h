@@ -14,6 +14,13 @@
  *   orc_dequantize_q4_0     known answers of tests/quant_q4_0_test.cpp:87-145;
  *                           closed form; oracle/_ref on the edge-scale blocks
  *                           of tests/gpu/unpack_q4_0_test.cpp:24-37.
+ *   orc_dequantize_q4_1     oracle/_ref (tests/support/q4_1_reference.h) on the
+ *                           edge-scale blocks of tests/gpu/unpack_q4_1_test.cpp:
+ *                           24-46, both answers; numpy's float32 (unfused)
+ *                           evaluation; rounded == fused over every finite d.
+ *   orc_dequantize_q8_0     oracle/_ref (q8_0_reference.h); closed form in numpy;
+ *                           the reference fixture embedding_q8_0.gguf's
+ *                           expected rows (tests/gpu/gather_test.cpp:149).
  *   orc_dequantize_q6_k     closed form (6-bit code, int8 scale, fp16 d) built
  *                           from the stored fields independently in the test;
  *                           oracle/_ref on tests/gpu/unpack_q6_k_test.cpp:24-41.
@@ -22,7 +29,12 @@
  *                           tests/formats_q6_k_repack_test.cpp:24-69; byte
  *                           equality with oracle/_ref's repack_q6_k.
  *   orc_unpack_group        equality with the file-order dequant over every
- *                           group (the device layout is lossless).
+ *                           group (the device layout is lossless), each format.
+ *   orc_gather,
+ *   orc_gather_positions    rows against the file-order dequant of the fixture
+ *                           tables tests/fixtures/gguf/embedding_*.gguf, with
+ *                           the skip rules of gather.wgsl:34-52 checked on
+ *                           hand-built steps (untouched rows keep a sentinel).
  *   orc_matmul_f32          order of addition pinned by hand-built cases whose
  *                           bits differ between orders (test_oracle.py), plus
  *                           within gamma(2K) of orc_matmul_f64.
@@ -48,13 +60,17 @@ extern "C" {
 #endif
 
 /* GGUF tensor types (src/core/gguf/types.h:41-43). */
-enum { ORC_F32 = 0, ORC_Q4_0 = 2, ORC_Q6_K = 14 };
+enum { ORC_F32 = 0, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q8_0 = 8, ORC_Q6_K = 14 };
 
 float orc_fp16_to_fp32(uint16_t h);
 
 /* File-order blocks -> f32 weights, flat. */
 void orc_dequantize_q4_0(const uint8_t* blocks, uint64_t nblocks, float* out);
 void orc_dequantize_q6_k(const uint8_t* blocks, uint64_t nblocks, float* out);
+/* Q4_1's two admissible answers: multiply and add each rounded, and one fma
+ * (`fused` may be NULL). */
+void orc_dequantize_q4_1(const uint8_t* blocks, uint64_t nblocks, float* rounded, float* fused);
+void orc_dequantize_q8_0(const uint8_t* blocks, uint64_t nblocks, float* out);
 /* Weights [first, first + count) of a tensor stored as `type` blocks. */
 int orc_dequantize_range(uint32_t type, const uint8_t* blocks, uint64_t first, uint64_t count, float* out);
 
@@ -96,6 +112,16 @@ void orc_finish(const float* totals, uint64_t tokens, uint64_t rows, const float
 void orc_gated(const float* gate, const float* up, uint64_t count, const float* clip, uint32_t activation,
                float* out);
 void orc_gated_by_input(const float* totals, const float* u, uint64_t count, uint32_t activation, float* out);
+
+/* The embedding gather (gather.wgsl:21-58): rows of `hidden` [tokens][columns]
+ * from a piece of `row_count` stored rows holding vocabulary rows first_row ..;
+ * rows whose token lies elsewhere, or is the media placeholder, untouched. */
+int orc_gather(uint32_t type, const uint8_t* stored_rows, uint64_t row_count, uint64_t columns, uint64_t first_row,
+               const uint32_t* ids, uint32_t tokens, const uint32_t* fed, int media, uint32_t media_token,
+               float scale, float* hidden);
+/* Its position form (gather.wgsl:65-84) over an F32 table of 2 x positions rows. */
+int orc_gather_positions(const float* table, uint64_t columns, uint32_t positions, uint32_t grid_columns,
+                         uint32_t tokens, float* out);
 
 /* Monotonic seconds, for the CPU baseline timing. */
 double orc_now(void);

@@ -5,6 +5,8 @@
 //   src/core/quant/q4_0.h            fp16_to_fp32 (lines 66-95)
 //   tests/support/q4_0_reference.h   dequantize_q4_0 (lines 25-53)
 //   tests/support/q6_k_reference.h   dequantize_q6_k (lines 17-47)
+//   tests/support/q4_1_reference.h   dequantize_q4_1 (lines 27-54)
+//   tests/support/q8_0_reference.h   dequantize_q8_0 (lines 14-27)
 //   src/core/formats/device_layout.h kQ6_KLayout.repack (lines 124-134),
 //                                    defined in q6_k/q6_k_repack.cpp:52-87
 #include <array>
@@ -16,7 +18,9 @@
 #include "core/formats/device_layout.h"
 #include "core/quant/q4_0.h"
 #include "support/q4_0_reference.h"
+#include "support/q4_1_reference.h"
 #include "support/q6_k_reference.h"
+#include "support/q8_0_reference.h"
 
 extern "C" {
 
@@ -29,6 +33,17 @@ void ref_dequantize_q4_0(const std::uint8_t* blocks, std::uint64_t n, float* out
 
 void ref_dequantize_q6_k(const std::uint8_t* blocks, std::uint64_t n, float* out) {
     const auto v = bllm::test::dequantize_q6_k(std::span<const std::uint8_t>(blocks, n * 210));
+    std::memcpy(out, v.data(), v.size() * sizeof(float));
+}
+
+void ref_dequantize_q4_1(const std::uint8_t* blocks, std::uint64_t n, float* rounded, float* fused) {
+    const auto v = bllm::test::dequantize_q4_1(std::span<const std::uint8_t>(blocks, n * 20));
+    std::memcpy(rounded, v.rounded.data(), v.rounded.size() * sizeof(float));
+    std::memcpy(fused, v.fused.data(), v.fused.size() * sizeof(float));
+}
+
+void ref_dequantize_q8_0(const std::uint8_t* blocks, std::uint64_t n, float* out) {
+    const auto v = bllm::test::dequantize_q8_0(std::span<const std::uint8_t>(blocks, n * 34));
     std::memcpy(out, v.data(), v.size() * sizeof(float));
 }
 

@@ -5,6 +5,10 @@
   then LCG scales (never inf/NaN); LCG codes throughout.
 - q6_k_edge_blocks: tests/gpu/unpack_q6_k_test.cpp:24-41 — LCG ql/qh, scales
   with -128 and 127 first, the same d edges.
+- q4_1_edge_blocks: tests/gpu/unpack_q4_1_test.cpp:24-46 — every edge as d and,
+  four apart, as m; then LCG d and m; LCG codes.
+- q8_0_edge_blocks: tests/gpu/unpack_q8_0_test.cpp:22-39 — the same d edges,
+  codes -128 and 127 first in every block, LCG codes.
 - lcg_bytes: tests/formats_q6_k_repack_test.cpp:44-49's stored bytes.
 - q4_0_block: tests/quant_q4_0_test.cpp:70-84's make_block.
 
@@ -58,6 +62,39 @@ def q6_k_edge_blocks(count, seed=0x7F4A7C15):
     return bytes(out)
 
 
+def _finite(h):
+    return h & 0xBBFF if (h & 0x7C00) == 0x7C00 else h
+
+
+def q4_1_edge_blocks(count, seed=0x9E3779B9):
+    lcg = Lcg(seed)
+    n = len(EDGE_SCALES)
+
+    def finite(i):
+        return _finite(EDGE_SCALES[i] if i < n else (lcg.next() >> 16))
+
+    out = bytearray()
+    for b in range(count):
+        d = finite(b)
+        m = finite((b + 4) % n if b < n else b)
+        for h in (d, m):
+            out += bytes([h & 0xFF, h >> 8])
+        out += bytes((lcg.next() >> 24) & 0xFF for _ in range(16))
+    return bytes(out)
+
+
+def q8_0_edge_blocks(count, seed=0x1B873593):
+    lcg = Lcg(seed)
+    out = bytearray()
+    for b in range(count):
+        d = _finite(EDGE_SCALES[b] if b < len(EDGE_SCALES) else (lcg.next() >> 16))
+        out += bytes([d & 0xFF, d >> 8])
+        for j in range(32):
+            q = (lcg.next() >> 24) & 0xFF
+            out.append(0x80 if j == 0 else 0x7F if j == 1 else q)
+    return bytes(out)
+
+
 def lcg_bytes(count, seed=0x2545F491):
     lcg = Lcg(seed)
     return bytes((lcg.next() >> 24) & 0xFF for _ in range(count))
@@ -84,6 +121,24 @@ def numpy_q4_0(blocks):
     qs = b[:, 2:]
     codes = np.concatenate([qs & 0xF, qs >> 4], axis=1).astype(np.int32) - 8
     return (codes.astype(np.float32) * d[:, None]).reshape(-1)
+
+
+def numpy_q4_1(blocks):
+    """ggml's block_q4_1 (d, m, qs[16]) in numpy float32: the product and the
+    sum each rounded (numpy never fuses)."""
+    b = np.frombuffer(blocks, np.uint8).reshape(-1, 20)
+    d = half(b[:, 0].astype(np.uint16) | (b[:, 1].astype(np.uint16) << 8))
+    m = half(b[:, 2].astype(np.uint16) | (b[:, 3].astype(np.uint16) << 8))
+    qs = b[:, 4:]
+    codes = np.concatenate([qs & 0xF, qs >> 4], axis=1).astype(np.float32)
+    return ((codes * d[:, None]).astype(np.float32) + m[:, None]).astype(np.float32).reshape(-1)
+
+
+def numpy_q8_0(blocks):
+    b = np.frombuffer(blocks, np.uint8).reshape(-1, 34)
+    d = half(b[:, 0].astype(np.uint16) | (b[:, 1].astype(np.uint16) << 8))
+    codes = b[:, 2:].view(np.int8).astype(np.float32)
+    return (codes * d[:, None]).astype(np.float32).reshape(-1)
 
 
 def q6_k_codes(blocks):

@@ -13,12 +13,13 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 ORACLE_DIR = os.path.join(ROOT, "oracle")
 
-Q4_0, Q6_K = 2, 14
-BLOCK = {Q4_0: (32, 18), Q6_K: (256, 210)}
+F32, Q4_0, Q4_1, Q8_0, Q6_K = 0, 2, 3, 8, 14
+BLOCK = {F32: (1, 4), Q4_0: (32, 18), Q4_1: (32, 20), Q8_0: (32, 34), Q6_K: (256, 210)}
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _f32p = ctypes.POINTER(ctypes.c_float)
 _f64p = ctypes.POINTER(ctypes.c_double)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
 
 
 def _ptr(a, t):
@@ -37,8 +38,13 @@ class Oracle:
         lib = ctypes.CDLL(path)
         lib.orc_fp16_to_fp32.restype = ctypes.c_float
         lib.orc_fp16_to_fp32.argtypes = [ctypes.c_uint16]
-        for f in (lib.orc_dequantize_q4_0, lib.orc_dequantize_q6_k):
+        for f in (lib.orc_dequantize_q4_0, lib.orc_dequantize_q6_k, lib.orc_dequantize_q8_0):
             f.argtypes = [_u8p, ctypes.c_uint64, _f32p]
+        lib.orc_dequantize_q4_1.argtypes = [_u8p, ctypes.c_uint64, _f32p, _f32p]
+        lib.orc_gather.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64, _u32p,
+                                   ctypes.c_uint32, _u32p, ctypes.c_int, ctypes.c_uint32, ctypes.c_float, _f32p]
+        lib.orc_gather_positions.argtypes = [_f32p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
+                                             ctypes.c_uint32, _f32p]
         lib.orc_dequantize_range.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64, _f32p]
         lib.orc_layout_bytes.restype = ctypes.c_uint64
         lib.orc_layout_bytes.argtypes = [ctypes.c_uint32, ctypes.c_uint64]
@@ -70,12 +76,46 @@ class Oracle:
         return self.lib.orc_fp16_to_fp32(h)
 
     def dequantize(self, gtype, blocks):
+        """File-order blocks -> weights (Q4_1: its rounded answer)."""
         b = _bytes(blocks)
         per, nbytes = BLOCK[gtype]
         n = b.size // nbytes
         out = np.empty(n * per, np.float32)
-        f = self.lib.orc_dequantize_q4_0 if gtype == Q4_0 else self.lib.orc_dequantize_q6_k
+        if gtype == Q4_1:
+            self.lib.orc_dequantize_q4_1(_ptr(b, _u8p), n, _ptr(out, _f32p), None)
+            return out
+        f = {F32: None, Q4_0: self.lib.orc_dequantize_q4_0, Q8_0: self.lib.orc_dequantize_q8_0,
+             Q6_K: self.lib.orc_dequantize_q6_k}[gtype]
+        if f is None:
+            return np.frombuffer(b.tobytes(), np.float32).copy()
         f(_ptr(b, _u8p), n, _ptr(out, _f32p))
+        return out
+
+    def dequantize_q4_1(self, blocks):
+        """Q4_1's two answers: (rounded, fused)."""
+        b = _bytes(blocks)
+        n = b.size // 20
+        rounded, fused = np.empty(n * 32, np.float32), np.empty(n * 32, np.float32)
+        self.lib.orc_dequantize_q4_1(_ptr(b, _u8p), n, _ptr(rounded, _f32p), _ptr(fused, _f32p))
+        return rounded, fused
+
+    def gather(self, gtype, stored_rows, row_count, columns, ids, hidden, first_row=0, fed=None, media=False,
+               media_token=0, scale=1.0):
+        """Writes the step's rows into `hidden` (float32 [tokens][columns]) in place."""
+        b = _bytes(stored_rows)
+        ids = np.ascontiguousarray(ids, np.uint32)
+        f = None if fed is None else np.ascontiguousarray(fed, np.uint32)
+        assert hidden.dtype == np.float32 and hidden.flags.c_contiguous and hidden.size >= ids.size * columns
+        assert self.lib.orc_gather(gtype, _ptr(b, _u8p), row_count, columns, first_row, _ptr(ids, _u32p), ids.size,
+                                   None if f is None else _ptr(f, _u32p), int(media), media_token, scale,
+                                   _ptr(hidden, _f32p)) == 0
+        return hidden
+
+    def gather_positions(self, table, columns, positions, grid_columns, tokens):
+        t = np.ascontiguousarray(table, np.float32)
+        out = np.zeros((tokens, columns), np.float32)
+        assert self.lib.orc_gather_positions(_ptr(t, _f32p), columns, positions, grid_columns, tokens,
+                                             _ptr(out, _f32p)) == 0
         return out
 
     def layout_bytes(self, gtype, nblocks):
@@ -180,8 +220,9 @@ class Reference:
         lib = ctypes.CDLL(path)
         lib.ref_fp16_to_fp32.restype = ctypes.c_float
         lib.ref_fp16_to_fp32.argtypes = [ctypes.c_uint16]
-        for f in (lib.ref_dequantize_q4_0, lib.ref_dequantize_q6_k):
+        for f in (lib.ref_dequantize_q4_0, lib.ref_dequantize_q6_k, lib.ref_dequantize_q8_0):
             f.argtypes = [_u8p, ctypes.c_uint64, _f32p]
+        lib.ref_dequantize_q4_1.argtypes = [_u8p, ctypes.c_uint64, _f32p, _f32p]
         lib.ref_repack_q6_k.argtypes = [_u8p, ctypes.c_uint64, _u8p, _u8p, _u8p, _u8p]
         self.lib = lib
 
@@ -193,9 +234,17 @@ class Reference:
         per, nbytes = BLOCK[gtype]
         n = b.size // nbytes
         out = np.empty(n * per, np.float32)
-        f = self.lib.ref_dequantize_q4_0 if gtype == Q4_0 else self.lib.ref_dequantize_q6_k
+        f = {Q4_0: self.lib.ref_dequantize_q4_0, Q8_0: self.lib.ref_dequantize_q8_0,
+             Q6_K: self.lib.ref_dequantize_q6_k}[gtype]
         f(_ptr(b, _u8p), n, _ptr(out, _f32p))
         return out
+
+    def dequantize_q4_1(self, blocks):
+        b = _bytes(blocks)
+        n = b.size // 20
+        rounded, fused = np.empty(n * 32, np.float32), np.empty(n * 32, np.float32)
+        self.lib.ref_dequantize_q4_1(_ptr(b, _u8p), n, _ptr(rounded, _f32p), _ptr(fused, _f32p))
+        return rounded, fused
 
     def repack_q6_k(self, blocks):
         b = _bytes(blocks)

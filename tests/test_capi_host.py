@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from tests.support import blocks as B
-from tests.support.oracle_lib import Q4_0, Q6_K
+from tests.support.oracle_lib import F32, Q4_0, Q4_1, Q6_K, Q8_0
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -52,13 +52,24 @@ def test_layout_bytes():
     assert mm.layout_bytes(Q6_K, 1, 1152) == 0  # 4.5 super-blocks: not whole blocks
     assert mm.layout_bytes(Q4_0, 4, 1000) == 0  # not whole groups
     assert mm.layout_bytes(99, 4, 1024) == 0
+    assert mm.layout_bytes(Q4_1, 40, 3072) == 40 * 96 * 20
+    assert mm.layout_bytes(Q8_0, 1, 32) == 36  # 34 rounded up to 4
+    assert mm.layout_bytes(F32, 7, 256) == 7 * 256 * 4
 
 
-@pytest.mark.parametrize("gtype,count", [(Q4_0, 1), (Q4_0, 257), (Q6_K, 1), (Q6_K, 33)])
+def _edge_blocks(gtype, count):
+    if gtype == F32:
+        return np.random.default_rng(count).standard_normal(count).astype(np.float32).tobytes()
+    return {Q4_0: B.q4_0_edge_blocks, Q4_1: B.q4_1_edge_blocks, Q8_0: B.q8_0_edge_blocks,
+            Q6_K: B.q6_k_edge_blocks}[gtype](count)
+
+
+@pytest.mark.parametrize("gtype,count", [(Q4_0, 1), (Q4_0, 257), (Q6_K, 1), (Q6_K, 33), (Q4_1, 1), (Q4_1, 257),
+                                         (Q8_0, 1), (Q8_0, 257), (F32, 32), (F32, 4096)])
 def test_lay_out_matches_the_oracle(oracle, gtype, count):
     from charlotte_amd import matmul as mm
 
-    stored = B.q4_0_edge_blocks(count) if gtype == Q4_0 else B.q6_k_edge_blocks(count)
+    stored = _edge_blocks(gtype, count)
     assert np.frombuffer(mm.lay_out(gtype, stored, count), np.uint8).tolist() == oracle.lay_out(gtype, stored).tolist()
 
 
@@ -67,6 +78,15 @@ def test_lay_out_many_blocks_threads(oracle):
 
     stored = B.lcg_bytes(210 * 70000, seed=11)  # enough blocks for the threaded path
     assert mm.lay_out(Q6_K, stored, 70000) == oracle.lay_out(Q6_K, stored).tobytes()
+
+
+@pytest.mark.parametrize("gtype", [Q4_1, Q8_0])
+def test_lay_out_of_many_blocks_is_the_oracles(oracle, gtype):
+    from charlotte_amd import matmul as mm
+
+    n = 70000
+    stored = B.lcg_bytes(n * {Q4_1: 20, Q8_0: 34}[gtype], seed=5)
+    assert mm.lay_out(gtype, stored, n) == oracle.lay_out(gtype, stored).tobytes()
 
 
 def test_repack_matches_the_reference(reference):

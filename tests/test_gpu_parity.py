@@ -268,7 +268,7 @@ def test_errors_are_statuses_with_messages(run, fixture_tensors):
 
     t = fixture_tensors["w_q4_0"]
     with pytest.raises(mm.MatmulError) as e:
-        mm.Weight(run.ctx, 3, t.rows, t.columns, t.data)  # Q4_1: no kernels
+        mm.Weight(run.ctx, 6, t.rows, t.columns, t.data)  # Q5_0: no kernels
     assert e.value.status == mm.Status.UNSUPPORTED_TYPE
     with pytest.raises(mm.MatmulError) as e:
         mm.Weight(run.ctx, Q4_0, 18, 1000, bytes(18 * 1000 // 32 * 18))
@@ -363,7 +363,7 @@ def test_weights_uploaded_from_a_gguf_file(oracle, run, source, fixture_tensors)
 
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "matmul_rows.gguf")
     with mm.GgufFile(path) as f:
-        for name in ("w_q4_0", "w_q6_k", "qkv_q", "ffn_gate"):
+        for name in ("w_q4_0", "w_q6_k", "qkv_q", "ffn_gate", "w_q4_1_1152", "w_q8_0"):
             t = fixture_tensors[name]
             w = f.upload(run.ctx, name)
             x = _rows_of(source, t.columns, 9)
@@ -372,6 +372,16 @@ def test_weights_uploaded_from_a_gguf_file(oracle, run, source, fixture_tensors)
                 got = run.write(w, x, tokens)
                 assert bits_equal(got, want[:tokens]), f"{name} tokens={tokens}: {first_difference(got, want[:tokens])}"
             w.free()
+        # An F32 tensor uploads (a gather's table) but no product reads it.
+        w = f.upload(run.ctx, "w_f32")
+        x = _rows_of(source, 768, 1)
+        from charlotte_amd import harness as hx
+
+        xb, yb = hx.Buffer.of(x), hx.Buffer(4 * 40)
         with pytest.raises(mm.MatmulError) as e:
-            f.upload(run.ctx, "w_f32")
-        assert e.value.status == mm.Status.UNSUPPORTED_TYPE and "w_f32" in str(e.value)
+            mm.launch(run.ctx, mm.MatmulLaunch([mm.Member(w)], xb.ptr, [yb.ptr]), 1)
+        assert e.value.status == mm.Status.UNSUPPORTED_TYPE
+        hx.sync()
+        xb.free()
+        yb.free()
+        w.free()
