@@ -67,7 +67,13 @@ __device__ __forceinline__ void finish_rows(const Product& a, uint32_t first, ui
 
 // L = 32: lane r of a half-wave owns range r — at most SPAN groups, its
 // chain from zero over them, and no other range; its range sum goes to LDS.
-template <uint32_t F, int SPAN, bool XREG, bool FULL>
+// Rows a batch: B steps' loads are issued before any is decoded, so a wave
+// keeps B rows' bytes in flight rather than one. A product of one step a
+// wave (fewer than 8,192 rows) takes batches of one: loading rows it will not
+// use would only hold the wave.
+constexpr int batch_of(int span) { return span >= 3 ? 2 : span == 2 ? 4 : 8; }
+
+template <uint32_t F, int SPAN, bool XREG, bool FULL, int B>
 __global__ __launch_bounds__(256, CHM_RANGES_MIN_BLOCKS) void gemv_ranges(Product a, uint32_t steps, uint32_t tiles) {
     __shared__ float partials[kWaves][kWaveRows * kPad];
     extern __shared__ float4 xs4[];  // x, staged when it is not held in registers
@@ -79,15 +85,35 @@ __global__ __launch_bounds__(256, CHM_RANGES_MIN_BLOCKS) void gemv_ranges(Produc
     const uint32_t token = a.last_token ? a.tokens - 1 : 0;
     const float* x = a.x + static_cast<uint64_t>(token) * G * 32;
 
+    Raw<F> raw[B][SPAN];
+    // Every lane issues the same loads on every path — rows past the
+    // product read its last row, groups past the lane's range the row's last
+    // group, unused — so a decode waits for its own loads.
+    auto load_row = [&](Raw<F> (&r)[SPAN], uint32_t wave_first, uint32_t step) {
+        const uint32_t p = min(wave_first + step * 2 + half, a.rows - 1);
+        const Piece w = piece_of(a, p);
+        const uint64_t row0 = static_cast<uint64_t>(w.row) * G;
+#pragma unroll
+        for (int i = 0; i < SPAN; ++i) r[i].load(w.piece, w.blocks, row0 + min(g0 + i, G - 1));
+    };
+    // The first tile's first row is issued before x is read and its other
+    // rows after, so x's round trip overlaps the weights' and the first
+    // decode waits for its own row and x only. (The grid never exceeds the
+    // tiles, so every workgroup has a first tile.)
+    const uint32_t first_wave_row = (blockIdx.x * kWaves + wave) * steps * 2;
+    load_row(raw[0], first_wave_row, 0);
+
     float xr[XREG ? SPAN * 32 : 1];
     if constexpr (XREG) {
+        // All of the slice's loads first, then the clamp where the product is
+        // clipped, so the loads are in flight together.
 #pragma unroll
         for (int i = 0; i < SPAN; ++i) {
             if (g0 + i < g1) {
                 const float4* src = reinterpret_cast<const float4*>(x + (g0 + i) * 32);
 #pragma unroll
                 for (int v = 0; v < 8; ++v) {
-                    const float4 q = clamp_input(a, src[v]);
+                    const float4 q = src[v];
                     xr[i * 32 + 4 * v + 0] = q.x;
                     xr[i * 32 + 4 * v + 1] = q.y;
                     xr[i * 32 + 4 * v + 2] = q.z;
@@ -95,31 +121,39 @@ __global__ __launch_bounds__(256, CHM_RANGES_MIN_BLOCKS) void gemv_ranges(Produc
                 }
             }
         }
+        if (a.clip) {
+            const float lo = a.clip[0], hi = a.clip[1];
+#pragma unroll
+            for (int k = 0; k < SPAN * 32; ++k) xr[k] = clamp_to(xr[k], lo, hi);
+        }
     } else {
+        // At most SPAN float4 a thread (G <= 32 SPAN): every load issued
+        // (clamped inside x) before any is stored, so they go out together
+        // behind the first batch's.
         const float4* src = reinterpret_cast<const float4*>(x);
-        for (uint32_t v = threadIdx.x; v < G * 8; v += 256) xs4[v] = clamp_input(a, src[v]);
+        float4 xv[SPAN];
+#pragma unroll
+        for (int k = 0; k < SPAN; ++k) xv[k] = src[min(threadIdx.x + 256 * k, G * 8 - 1)];
+#pragma unroll
+        for (int k = 0; k < SPAN; ++k) {
+            const uint32_t v = threadIdx.x + 256 * k;
+            if (v < G * 8) xs4[v] = clamp_input(a, xv[k]);
+        }
         __syncthreads();
     }
+#pragma unroll
+    for (int b = 1; b < B; ++b) load_row(raw[b], first_wave_row, b);
 
     float* mine = partials[wave];
-    // Rows a batch: B steps' loads are issued before any is decoded, so a
-    // wave keeps B rows' bytes in flight rather than one.
-    constexpr int B = SPAN >= 3 ? 2 : SPAN == 2 ? 4 : 8;
+    bool loaded = true;  // the first batch already is
     for (uint32_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
         const uint32_t wave_first = (tile * kWaves + wave) * steps * 2;
         for (uint32_t step0 = 0; step0 < steps; step0 += B) {
-            Raw<F> raw[B][SPAN];
-            // Every lane issues the same loads on every path — rows past the
-            // product read its last row, groups past the lane's range the
-            // row's last group, unused — so a decode waits for its own loads.
+            if (!loaded) {
 #pragma unroll
-            for (int b = 0; b < B; ++b) {
-                const uint32_t p = min(wave_first + (step0 + b) * 2 + half, a.rows - 1);
-                const Piece w = piece_of(a, p);
-                const uint64_t row0 = static_cast<uint64_t>(w.row) * G;
-#pragma unroll
-                for (int i = 0; i < SPAN; ++i) raw[b][i].load(w.piece, w.blocks, row0 + min(g0 + i, G - 1));
+                for (int b = 0; b < B; ++b) load_row(raw[b], wave_first, step0 + b);
             }
+            loaded = false;
 #pragma unroll
             for (int b = 0; b < B; ++b) {
                 const uint32_t slot = (step0 + b) * 2 + half;
@@ -311,20 +345,6 @@ __global__ __launch_bounds__(256, CHM_QUARTERS_MIN_BLOCKS) void gemv_quarters(Pr
     const uint32_t g0 = SPAN * j;
     const uint32_t token = a.last_token ? a.tokens - 1 : 0;
     const float* x = a.x + static_cast<uint64_t>(token) * G * 32;
-    {
-        const float4* src = reinterpret_cast<const float4*>(x);
-        for (uint32_t v = threadIdx.x; v < G * 8; v += 256) xs4[x_slot<SPAN>(v)] = clamp_input(a, src[v]);
-    }
-    const float4* xl = xs4 + x_slot<SPAN>(8 * g0);
-    // Which of the run's groups end a range; the run's first range is 8j.
-    uint32_t ends = 0;
-#pragma unroll
-    for (int i = 0; i < SPAN; ++i) {
-        const uint32_t g = g0 + i;
-        const uint32_t r = (32 * g + 31) / G;  // the range holding g
-        if (g + 1 == range_lo(r + 1, G)) ends |= 1u << i;
-    }
-    __syncthreads();
 
     float* mine = partials[wave];
     // Step n of this wave: tile blockIdx.x + (n / steps) gridDim.x, step n % steps.
@@ -341,6 +361,35 @@ __global__ __launch_bounds__(256, CHM_QUARTERS_MIN_BLOCKS) void gemv_quarters(Pr
         const Piece w = piece_of(a, p);
         run.load(w.piece, w.blocks, static_cast<uint64_t>(w.row) * G + g0);
     };
+    // The first step's run is loaded before x is staged, so the two round
+    // trips overlap.
+    Run<F, SPAN> first;
+    load(first, 0);  // the grid never exceeds the tiles: every wave has a step
+    {
+        // G = 4 SPAN groups, 32 SPAN float4: a fixed count a thread, every
+        // load issued before any is stored.
+        constexpr int kPer = (32 * SPAN + 255) / 256;
+        const float4* src = reinterpret_cast<const float4*>(x);
+        float4 xv[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) xv[k] = src[min(threadIdx.x + 256 * k, G * 8 - 1)];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const uint32_t v = threadIdx.x + 256 * k;
+            if (v < G * 8) xs4[x_slot<SPAN>(v)] = clamp_input(a, xv[k]);
+        }
+    }
+    const float4* xl = xs4 + x_slot<SPAN>(8 * g0);
+    // Which of the run's groups end a range; the run's first range is 8j.
+    uint32_t ends = 0;
+#pragma unroll
+    for (int i = 0; i < SPAN; ++i) {
+        const uint32_t g = g0 + i;
+        const uint32_t r = (32 * g + 31) / G;  // the range holding g
+        if (g + 1 == range_lo(r + 1, G)) ends |= 1u << i;
+    }
+    __syncthreads();
+
     auto decode = [&](const Run<F, SPAN>& run, uint32_t n) {
         const uint32_t p = row_of(n);
         const uint32_t slot = (n % steps) * 16 + rho;
@@ -382,8 +431,8 @@ __global__ __launch_bounds__(256, CHM_QUARTERS_MIN_BLOCKS) void gemv_quarters(Pr
         }
     };
     if constexpr (CHM_QUARTERS_PIPELINE) {
-        Run<F, SPAN> even, odd;
-        load(even, 0);
+        Run<F, SPAN>& even = first;
+        Run<F, SPAN> odd;
         for (uint32_t n = 0; n < total_steps; n += 2) {
             load(odd, n + 1);
             decode(even, n);
@@ -393,9 +442,8 @@ __global__ __launch_bounds__(256, CHM_QUARTERS_MIN_BLOCKS) void gemv_quarters(Pr
         }
     } else {
         for (uint32_t n = 0; n < total_steps; ++n) {
-            Run<F, SPAN> run;
-            load(run, n);
-            decode(run, n);
+            if (n > 0) load(first, n);
+            decode(first, n);
         }
     }
 }
@@ -441,6 +489,16 @@ static uint32_t resident(K kernel, size_t lds) {
     return static_cast<uint32_t>(blocks);
 }
 
+template <uint32_t F, int SPAN, bool XREG, bool FULL, int B>
+static void launch_ranges(const Product& a, uint32_t steps, uint32_t tiles, size_t lds, uint32_t compute_units,
+                          hipStream_t stream) {
+    thread_local size_t cached_lds = ~size_t{0};
+    thread_local uint32_t per_cu = 1;
+    if (cached_lds != lds) per_cu = resident(gemv_ranges<F, SPAN, XREG, FULL, B>, lds), cached_lds = lds;
+    const dim3 grid(std::min(tiles, per_cu * compute_units));
+    hipLaunchKernelGGL((gemv_ranges<F, SPAN, XREG, FULL, B>), grid, dim3(256), lds, stream, a, steps, tiles);
+}
+
 // A grid of at most the workgroups the GPU holds at once, each looping over
 // tiles, so no tail round runs part-empty.
 template <uint32_t F, int L, int SPAN, bool XREG, bool FULL>
@@ -449,11 +507,11 @@ static void go_epilogue(const Product& a, uint32_t steps, uint32_t compute_units
     const uint32_t tiles = (a.rows + rows_a_tile - 1) / rows_a_tile;
     const size_t lds = XREG ? 0 : (static_cast<size_t>(a.groups) * 32 + (L == 4 ? 16 : 0)) * sizeof(float);
     if constexpr (L == 32) {
-        thread_local size_t cached_lds = ~size_t{0};
-        thread_local uint32_t per_cu = 1;
-        if (cached_lds != lds) per_cu = resident(gemv_ranges<F, SPAN, XREG, FULL>, lds), cached_lds = lds;
-        const dim3 grid(std::min(tiles, per_cu * compute_units));
-        hipLaunchKernelGGL((gemv_ranges<F, SPAN, XREG, FULL>), grid, dim3(256), lds, stream, a, steps, tiles);
+        if (steps == 1) {
+            launch_ranges<F, SPAN, XREG, FULL, 1>(a, steps, tiles, lds, compute_units, stream);
+        } else {
+            launch_ranges<F, SPAN, XREG, FULL, batch_of(SPAN)>(a, steps, tiles, lds, compute_units, stream);
+        }
     } else {
         thread_local size_t cached_lds = ~size_t{0};
         thread_local uint32_t per_cu = 1;

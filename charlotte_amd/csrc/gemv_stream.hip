@@ -76,15 +76,6 @@ __global__ __launch_bounds__(256, 2) void gemv_stream(Product a, uint32_t steps)
     const uint32_t waves = gridDim.x * kStreamWaves;
     const uint32_t token = a.last_token ? a.tokens - 1 : 0;
 
-    // x in LDS, clamped where the product is clipped; lane j reads its slice
-    // (groups 9j .. 9j + 8) a group at a time, lanes of one j the same words.
-    // Slices sit 73 float4 apart, so the four a read takes start in
-    // different banks.
-    {
-        const float4* src = reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(token) * 1152);
-        for (uint32_t v = threadIdx.x; v < 288; v += 256) xs[v + v / 72] = clamp_input(a, src[v]);
-        __syncthreads();
-    }
     struct Stage {
         u32x4s_t *lo, *hi, *sc, *d;
     };
@@ -215,9 +206,35 @@ __global__ __launch_bounds__(256, 2) void gemv_stream(Product a, uint32_t steps)
 
     // One step in flight a wave (two waves a SIMD): the next step's copy is
     // issued as soon as this one is out of the stage.
+    // The first step's copy is issued before x is staged, so the two round
+    // trips overlap (the barrier below waits for both).
     uint32_t step = blockIdx.x * kStreamWaves + wave;
+    if (step < steps) issue(step, sa);
+    // x in LDS, clamped where the product is clipped; lane j reads its slice
+    // (groups 9j .. 9j + 8) a group at a time, lanes of one j the same words.
+    // Slices sit 73 float4 apart, so the four a read takes start in
+    // different banks.
+    // The stores are written as instructions the compiler does not look
+    // into: it would otherwise wait for the copy just issued before any LDS
+    // store (it cannot tell x from the stage). Their wait is explicit.
+    {
+        const float4* src = reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(token) * 1152);
+        const float4 x0 = src[threadIdx.x], x1 = src[min(threadIdx.x + 256, 287u)];
+        const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(xs));
+        auto bits = [](float4 q) {
+            return u32x4s_t{__float_as_uint(q.x), __float_as_uint(q.y), __float_as_uint(q.z), __float_as_uint(q.w)};
+        };
+        const u32x4s_t c0 = bits(clamp_input(a, x0));
+        const uint32_t v0 = threadIdx.x, v1 = threadIdx.x + 256;
+        __asm__ __volatile__("ds_write_b128 %0, %1" : : "v"(base + 16 * (v0 + v0 / 72)), "v"(c0));
+        if (v1 < 288) {
+            const u32x4s_t c1 = bits(clamp_input(a, x1));
+            __asm__ __volatile__("ds_write_b128 %0, %1" : : "v"(base + 16 * (v1 + v1 / 72)), "v"(c1));
+        }
+        __asm__ __volatile__("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
     if (step >= steps) return;
-    issue(step, sa);
     while (true) {
         __builtin_amdgcn_s_waitcnt(kVmcnt0);
         __asm__ __volatile__("" ::: "memory");
