@@ -65,8 +65,8 @@ bool known(uint32_t type) {
            type == CHARLOTTE_HIP_MATMUL_Q8_0 || type == CHARLOTTE_HIP_MATMUL_Q6_K;
 }
 bool product_reads(uint32_t type) { return known(type) && type != CHARLOTTE_HIP_MATMUL_F32; }
-// The matrix-core prefill's formats.
-bool mfma_reads(uint32_t type) { return type == CHARLOTTE_HIP_MATMUL_Q4_0 || type == CHARLOTTE_HIP_MATMUL_Q6_K; }
+// The matrix-core prefill's formats: every product format.
+bool mfma_reads(uint32_t type) { return product_reads(type); }
 
 // The shape checks of a weight: rows of whole 32-weight groups
 // (matmul.h:668-671, format.h:138-160) in a tensor of whole blocks.
@@ -373,9 +373,6 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
         const bool mfma = ctx->gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_SPLIT_F16_MFMA ||
                           (ctx->gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_AUTO && !sums && room && tokens >= kMfmaLeast &&
                            mfma_reads(head->type));
-        if (mfma && !mfma_reads(head->type))
-            return fail(ctx, CHARLOTTE_HIP_MATMUL_UNSUPPORTED,
-                        "launch: the matrix-core path reads Q4_0 and Q6_K, not GGUF type " + std::to_string(head->type));
         if (mfma && !room)
             return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT,
                         "launch: the matrix-core path needs a workspace of " + std::to_string(need) + " bytes");

@@ -2,8 +2,11 @@
 // tolerance, not bit-exact — the canonical VALU tile keeps the reference's
 // order; this one trades it for throughput.
 //
-// The weights' codes are exact in binary16 (Q4_0 q - 8, Q6_K q - 32); the
-// block scale stays out of the product and is applied in f32 after it. The
+// The weights' codes are exact in binary16 (Q4_0 q - 8, Q6_K q - 32, Q8_0 q,
+// Q4_1 q); the block scale stays out of the product and is applied in f32
+// after it. Q4_1's minimum m multiplies the group's sum of inputs, which one
+// more product against all-ones codes gives for every row at once:
+// total = fma(d, P, fma(m, S, total)), S = ones . hi + ones . lo. The
 // input is split in two binary16 parts per token: x 2^s = hi + lo with
 // hi = f16(x 2^s), lo = f16(x 2^s - hi), s a power of two per token putting
 // its largest |x| in [2^14, 2^15) — so neither part overflows, and lo keeps
@@ -22,7 +25,8 @@
 // weight rows by T x 16 tokens; v_mfma_f32_16x16x32_f16 (Q4_0) and
 // v_mfma_f32_16x16x16_f16 (Q6_K, one a half: its scale differs) with the
 // input as the A operand, so a lane's four outputs are four tokens of one
-// weight row and need one scale. A workgroup's four waves share its tokens:
+// weight row and need one scale. Q8_0 and Q4_1 go as Q4_0 does, their codes
+// group by group. A workgroup's four waves share its tokens:
 // their split input is staged once through LDS; each wave's codes go from the
 // piece straight into registers. Both are loaded a batch of groups ahead.
 #include <type_traits>
@@ -112,6 +116,18 @@ struct Codes<kQ6_K> {
     uint32_t d;
 };
 
+template <>
+struct Codes<kQ8_0> {
+    uint32_t c0, c1;  // codes 4q .. 4q+3 and 16+4q .. 16+4q+3
+    uint32_t d;
+};
+
+template <>
+struct Codes<kQ4_1> {
+    uint32_t code;
+    uint32_t dm;  // d low, m high
+};
+
 // Where a lane's row of a wave's row block reads: the piece and the row's
 // first group.
 struct RowAt {
@@ -127,6 +143,13 @@ __device__ __forceinline__ Codes<F> load_codes(const RowAt& w, uint32_t g, uint3
     if constexpr (F == kQ4_0) {
         c.code = *reinterpret_cast<const uint32_t*>(w.piece + 16 * gi + 4 * q);
         c.d = *reinterpret_cast<const uint16_t*>(w.piece + 16 * w.blocks + 2 * gi);
+    } else if constexpr (F == kQ8_0) {
+        c.c0 = *reinterpret_cast<const uint32_t*>(w.piece + 32 * gi + 4 * q);
+        c.c1 = *reinterpret_cast<const uint32_t*>(w.piece + 32 * gi + 16 + 4 * q);
+        c.d = *reinterpret_cast<const uint16_t*>(w.piece + 32 * w.blocks + 2 * gi);
+    } else if constexpr (F == kQ4_1) {
+        c.code = *reinterpret_cast<const uint32_t*>(w.piece + 16 * gi + 4 * q);
+        c.dm = *reinterpret_cast<const uint32_t*>(w.piece + 16 * w.blocks + 4 * gi);
     } else {
         const uint64_t n = w.blocks;
         c.lo = *reinterpret_cast<const uint32_t*>(w.piece + 16 * gi + 4 * q);
@@ -145,9 +168,23 @@ __device__ __forceinline__ Codes<F> load_codes(const RowAt& w, uint32_t g, uint3
 //   v_permlane32_swap, two v_permlane16_swap) then gives lane (c, q) code
 //   dword q of each of the four groups — what group_product takes. One 16-byte
 //   and one 8-byte load a row block a batch instead of eight narrow ones.
-//   Q6_K: group by group, as load_codes reads them.
+//   Q6_K, Q8_0, Q4_1: group by group, as load_codes reads them.
 template <uint32_t F, int R>
-struct Batch;
+struct Batch {
+    Codes<F> c[kBatch][R];
+    __device__ __forceinline__ void load(const RowAt (&rows)[R], uint32_t b, uint32_t G, uint32_t q, bool) {
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+#pragma unroll
+            for (int r = 0; r < R; ++r) c[j][r] = load_codes<F>(rows[r], min(b * kBatch + j, G - 1), q);
+    }
+    __device__ __forceinline__ void codes(Codes<F> (&wc)[kBatch][R]) const {
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+#pragma unroll
+            for (int r = 0; r < R; ++r) wc[j][r] = c[j][r];
+    }
+};
 
 template <int R>
 struct Batch<kQ4_0, R> {
@@ -189,23 +226,6 @@ struct Batch<kQ4_0, R> {
     }
 };
 
-template <int R>
-struct Batch<kQ6_K, R> {
-    Codes<kQ6_K> c[kBatch][R];
-    __device__ __forceinline__ void load(const RowAt (&rows)[R], uint32_t b, uint32_t G, uint32_t q, bool) {
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j)
-#pragma unroll
-            for (int r = 0; r < R; ++r) c[j][r] = load_codes<kQ6_K>(rows[r], min(b * kBatch + j, G - 1), q);
-    }
-    __device__ __forceinline__ void codes(Codes<kQ6_K> (&wc)[kBatch][R]) const {
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j)
-#pragma unroll
-            for (int r = 0; r < R; ++r) wc[j][r] = c[j][r];
-    }
-};
-
 __device__ __forceinline__ half2_t lift_less(uint32_t codes, uint32_t selector, _Float16 bias) {
     half2_t v = lift(codes, selector);
     const half2_t b = {bias, bias};
@@ -222,16 +242,44 @@ template <uint32_t F, int R, int T>
 __device__ __forceinline__ void group_product(float4_t (&tot)[R][T], const half8_t (&xh)[T], const half8_t (&xl)[T],
                                               const Codes<F> (&cw)[R], uint32_t q) {
     const float4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
-    if constexpr (F == kQ4_0) {
+    if constexpr (F == kQ4_0 || F == kQ8_0 || F == kQ4_1) {
+        // Codes of weights 4q .. 4q+3, then 16+4q .. 16+4q+3, as binary16.
         half8_t b[R];
-        float s[R];
+        float s[R], m[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t lo = cw[r].code & 0x0F0F0F0Fu, hi = (cw[r].code >> 4) & 0x0F0F0F0Fu;
-            const half2_t b0 = lift_less(lo, kLowPair, 1032.0f16), b1 = lift_less(lo, kHighPair, 1032.0f16);
-            const half2_t b2 = lift_less(hi, kLowPair, 1032.0f16), b3 = lift_less(hi, kHighPair, 1032.0f16);
+            uint32_t first, second;
+            _Float16 bias;
+            if constexpr (F == kQ8_0) {
+                // int8 q with its sign bit flipped is q + 128: lifted to 1152 + q
+                first = cw[r].c0 ^ 0x80808080u, second = cw[r].c1 ^ 0x80808080u, bias = 1152.0f16;
+                s[r] = half_to_float(cw[r].d);
+            } else if constexpr (F == kQ4_1) {
+                first = cw[r].code & 0x0F0F0F0Fu, second = (cw[r].code >> 4) & 0x0F0F0F0Fu, bias = 1024.0f16;
+                s[r] = half_to_float(cw[r].dm & 0xFFFFu);
+                m[r] = half_to_float(cw[r].dm >> 16);
+            } else {
+                first = cw[r].code & 0x0F0F0F0Fu, second = (cw[r].code >> 4) & 0x0F0F0F0Fu, bias = 1032.0f16;
+                s[r] = half_to_float(cw[r].d);
+            }
+            const half2_t b0 = lift_less(first, kLowPair, bias), b1 = lift_less(first, kHighPair, bias);
+            const half2_t b2 = lift_less(second, kLowPair, bias), b3 = lift_less(second, kHighPair, bias);
             b[r] = half8_t{b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
-            s[r] = half_to_float(cw[r].d);
+        }
+        if constexpr (F == kQ4_1) {
+            // Each token's sum of the group's inputs, the same for every row.
+            const half8_t ones = {1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16};
+            float4_t sum[T];
+#pragma unroll
+            for (int t = 0; t < T; ++t) sum[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[t], ones, z, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < T; ++t) sum[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[t], ones, sum[t], 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) tot[r][t][k] = __builtin_fmaf(m[r], sum[t][k], tot[r][t][k]);
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -492,10 +540,13 @@ hipError_t launch_gemm_mfma(const Product& a, uint32_t format, uint32_t compute_
     uint8_t* xp = static_cast<uint8_t*>(workspace);
     float* inv = reinterpret_cast<float*>(xp + m * a.groups * 128);
     hipLaunchKernelGGL(prepare_x, dim3(static_cast<uint32_t>(m)), dim3(256), 0, stream, a, xp, inv);
-    if (format == kQ4_0)
-        launch_format<kQ4_0>(a, xp, inv, compute_units, stream);
-    else
-        launch_format<kQ6_K>(a, xp, inv, compute_units, stream);
+    switch (format) {
+        case kQ4_0: launch_format<kQ4_0>(a, xp, inv, compute_units, stream); break;
+        case kQ4_1: launch_format<kQ4_1>(a, xp, inv, compute_units, stream); break;
+        case kQ8_0: launch_format<kQ8_0>(a, xp, inv, compute_units, stream); break;
+        case kQ6_K: launch_format<kQ6_K>(a, xp, inv, compute_units, stream); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -223,24 +223,31 @@ def test_synthetic_decode_at_size(oracle, run, gtype, rows, columns):
     w.free()
 
 
-def test_the_matrix_cores_refuse_what_they_do_not_read(oracle, run, fixture_tensors):
-    """The split-f16 matrix-core path reads Q4_0 and Q6_K: asked for Q8_0 it
-    refuses; under AUTO with a workspace, Q8_0 prefill stays canonical (the
-    oracle's bits)."""
+@pytest.mark.parametrize("name", ["w_q8_0", "w_q4_1_1152", "w_q4_1_3072", "w_glu"])
+def test_the_matrix_cores_take_the_fixture_within_tolerance(oracle, run, source, fixture_tensors, name):
+    """The split-f16 matrix-core prefill over Q8_0 and Q4_1 (Q4_1's minimum
+    through the group's input sum): max |err| / max |y| <= 1e-5 against the
+    f64 product; AUTO takes it once a workspace holds the step."""
     from charlotte_amd import harness as hx
     from charlotte_amd import matmul as mm
 
-    t = fixture_tensors["w_q8_0"]
-    w = run.weight(t.type, t.rows, 1024, t.data)
-    x = np.random.default_rng(2).standard_normal((64, 1024)).astype(np.float32)
-    ws = hx.Buffer(mm.workspace_bytes(64, 1024))
-    run.ctx.set_workspace(ws.ptr, mm.workspace_bytes(64, 1024))
+    t = fixture_tensors[name]
+    w = run.weight(t.type, t.rows, t.columns, t.data)
+    x = source[: 64 * t.columns].reshape(64, t.columns)
+    y64, _ = oracle.matmul_f64(t.type, t.data, t.rows, t.columns, x)
+    exact = oracle.matmul_f32(t.type, t.data, t.rows, t.columns, x, threads=8)
+    ws = hx.Buffer(mm.workspace_bytes(64, t.columns))
+    run.ctx.set_workspace(ws.ptr, mm.workspace_bytes(64, t.columns))
     try:
-        _check(run.write(w, x, 64), oracle.matmul_f32(t.type, t.data, t.rows, 1024, x), "AUTO Q8_0")
-        run.ctx.set_gemm_path(mm.GemmPath.SPLIT_F16_MFMA)
-        with pytest.raises(mm.MatmulError) as e:
-            run.write(w, x, 64)
-        assert e.value.status == mm.Status.UNSUPPORTED and "matrix-core" in str(e.value)
+        for path in (mm.GemmPath.SPLIT_F16_MFMA, mm.GemmPath.AUTO):
+            run.ctx.set_gemm_path(path)
+            for tokens in (16, 33, 64):
+                got = run.write(w, x, tokens)
+                err = np.abs(got.astype(np.float64) - y64[:tokens]).max()
+                assert err <= 1e-5 * np.abs(y64[:tokens]).max(), f"{name} {path} tokens={tokens}: {err}"
+                assert (np.argmax(got, 1) == np.argmax(exact[:tokens], 1)).all()
+        # Below 16 tokens AUTO keeps the canonical tile: the oracle's bits.
+        _check(run.write(w, x, 9), exact[:9], f"{name} AUTO 9 tokens")
     finally:
         run.ctx.set_gemm_path(mm.GemmPath.AUTO)
         run.ctx.set_workspace(0, 0)

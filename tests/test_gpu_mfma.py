@@ -12,7 +12,7 @@ epilogues and its input scaling (tiny, huge and zero token rows).
 import numpy as np
 import pytest
 
-from tests.support.oracle_lib import Q4_0, Q6_K
+from tests.support.oracle_lib import Q4_0, Q4_1, Q6_K, Q8_0
 
 pytestmark = pytest.mark.gpu
 
@@ -63,6 +63,7 @@ def _within(got, y64, canonical, what):
 
 @pytest.mark.parametrize("gtype,rows,columns", [
     (Q4_0, 200, 64), (Q4_0, 1000, 1024), (Q4_0, 333, 2048), (Q4_0, 520, 3072), (Q6_K, 300, 1152), (Q6_K, 256, 2048),
+    (Q8_0, 200, 1024), (Q8_0, 333, 1152), (Q4_1, 300, 1152), (Q4_1, 256, 3072), (Q4_1, 100, 64),
 ])
 @pytest.mark.parametrize("tokens", [2, 16, 17, 100, 300])
 def test_mfma_write_within_tolerance(oracle, run, gtype, rows, columns, tokens):
