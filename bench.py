@@ -214,8 +214,9 @@ def run_c3(S, steps, warmup, rng, fused=True):
             "tokens_per_s": 1e3 / ms}
 
 
-def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None):
-    """plan: products (build_products) over `tokens` tokens, on prefill path `path`."""
+def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=None):
+    """plan: products (build_products) over `tokens` tokens, on prefill path `path`; with `gate`, the
+    split along K where the gate takes the step (range sums sized for the largest product)."""
     from charlotte_amd import synthetic
 
     mm = S.mm
@@ -223,6 +224,11 @@ def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None):
     S.ctx.set_gemm_path(path)
     launches, xs, _, flops = build_products(S, rng, plan, tokens)
     launches = [(m, tokens) for m in launches]
+    gate = gate or mm.kNever
+    sums, sums_bytes = 0, 0
+    if gate is not mm.kNever:
+        sums_bytes = 4 * 32 * tokens * max(sum(mem.rows or mem.weight.rows for mem in m.members) for m, _ in launches)
+        sums = S.buffer(nbytes=sums_bytes).ptr
     head_bytes = 0
     if head is not None:
         rows, columns = head
@@ -235,7 +241,7 @@ def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None):
 
     def body():
         for m, t in launches:
-            mm.launch(S.ctx, m, t, stream=S.stream.handle)
+            mm.launch(S.ctx, m, t, gate, sums, sums_bytes, stream=S.stream.handle)
 
     ms = S.time_graph(body, steps, warmup)
     tflops = flops / (ms * 1e-3) / 1e12
@@ -296,7 +302,7 @@ def main():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--only", default="c1,c2,c3,c4,c5")
+    p.add_argument("--only", default="c1,c2,c3,c4,c5,c6")
     p.add_argument("--no-cpu", action="store_true")
     args = p.parse_args()
     if args.gpus != 1:
@@ -337,6 +343,17 @@ def main():
             for tag, path in paths:
                 out["c5" + tag] = run_gemm(S, "c5" + tag, layer_plan(2048, 512, 2048, 8192, True) * 16, 2048,
                                            max(args.steps // 4, 3), args.warmup, rng, path, head=(128256, 2048))
+        if "c6" in only:
+            # A short prefill step (32 tokens) through Llama 3.2 1B's down
+            # projection: one 64-token tile a 128-row block, 16 workgroups,
+            # unless split along K (the reference's measured gate, 2/1 up to
+            # 64 workgroups) or run on the matrix cores.
+            plan = [("write", [(2048, 8192)])]
+            out["c6_split"] = run_gemm(S, "c6_split", plan, 32, args.steps, args.warmup, rng,
+                                       S.mm.GemmPath.CANONICAL, gate=S.mm.kSplitGate)
+            out["c6_tiled"] = run_gemm(S, "c6_tiled", plan, 32, args.steps, args.warmup, rng, S.mm.GemmPath.CANONICAL)
+            out["c6_mfma"] = run_gemm(S, "c6_mfma", plan, 32, args.steps, args.warmup, rng,
+                                      S.mm.GemmPath.SPLIT_F16_MFMA)
     finally:
         S.close()
 

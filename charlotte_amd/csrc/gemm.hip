@@ -5,8 +5,9 @@
 // 256 lanes takes a tile of BM tokens x 128 rows and walks K one 32-weight
 // group at a time: the group's 128 rows are decoded once into LDS (exact
 // f32), the tokens' 32 inputs staged beside them, then each lane runs its
-// micro-tile of TM tokens x 8 rows, 32 multiply-adds in k order per output,
-// each output keeping its range sum and its total: at a range's last group
+// micro-tile of TM tokens x 8 rows (BM = 32, 64 or 128: TM = 2, 4 or 8),
+// 32 multiply-adds in k order per output, each output keeping its range sum
+// and its total: at a range's last group
 // the total adds the range sum and the range sum restarts from zero. So every
 // output's order of addition is decode's, whatever BM. Workgroups are
 // numbered token tile first, so the tiles that read one weight tile run
@@ -34,6 +35,11 @@ template <uint32_t F, int BM, bool SPLIT, bool FULL>
 __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_tiles, uint32_t row_tiles,
                                                       uint32_t chunks, float* range_sums) {
     constexpr int TM = BM / 16;  // a lane's tokens
+    // Token i of a lane's micro-tile: 2 ty + i (BM = 32); 4 ty + i % 4, and
+    // + 64 for i >= 4 (BM = 64, 128).
+    auto token_at = [&](uint32_t ty, int i) -> uint32_t {
+        return TM == 2 ? 2 * ty + i : 4 * ty + (i & 3) + 64 * (i >> 2);
+    };
     __shared__ float4 Ws[32][kRowsATile / 4];
     __shared__ float4 Xs[32][BM / 4];
     const uint32_t t = threadIdx.x, tx = t & 15u, ty = t >> 4;
@@ -49,7 +55,7 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
     const uint32_t sp = n0 + srow;
     const bool slive = sp < a.rows;
     const Piece spiece = piece_of(a, slive ? sp : 0);
-    constexpr int XPer = BM / 8;                 // floats a lane stages: 16 or 8
+    constexpr int XPer = BM / 8;                 // floats a lane stages: 16, 8 or 4
     const uint32_t xtok = t % BM, xpart = t / BM;
     const bool xlive = m0 + xtok < a.tokens;
     const float* xsrc = a.x + static_cast<uint64_t>(m0 + xtok) * K + xpart * XPer;
@@ -108,11 +114,17 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
             const float4 wa = Ws[k][tx], wb = Ws[k][16 + tx];
             const float w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
             float x[TM];
-            const float4 xa = Xs[k][ty];
-            x[0] = xa.x;
-            x[1] = xa.y;
-            x[2] = xa.z;
-            x[3] = xa.w;
+            if constexpr (TM == 2) {
+                const float2 xa = reinterpret_cast<const float2*>(Xs[k])[ty];
+                x[0] = xa.x;
+                x[1] = xa.y;
+            } else {
+                const float4 xa = Xs[k][ty];
+                x[0] = xa.x;
+                x[1] = xa.y;
+                x[2] = xa.z;
+                x[3] = xa.w;
+            }
             if constexpr (TM == 8) {
                 const float4 xb = Xs[k][16 + ty];
                 x[4] = xb.x;
@@ -129,7 +141,7 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
             if constexpr (SPLIT) {
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
-                    const uint32_t token = m0 + 4 * ty + (i & 3) + 64 * (i >> 2);
+                    const uint32_t token = m0 + token_at(ty, i);
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         const uint32_t p = n0 + 4 * tx + (j & 3) + 64 * (j >> 2);
@@ -155,7 +167,7 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
     // gated product's gate and up totals meet in one lane.
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-        const uint32_t token = m0 + 4 * ty + (i & 3) + 64 * (i >> 2);
+        const uint32_t token = m0 + token_at(ty, i);
         if (token >= a.tokens) continue;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -200,7 +212,8 @@ hipError_t launch_gemm_canonical(const Product& a, uint32_t format, uint32_t com
                                  hipStream_t stream) {
     const uint32_t row_tiles = (a.rows + kRowsATile - 1) / kRowsATile;
     const bool wide = ((a.tokens + 127) / 128) * row_tiles >= 2 * compute_units;
-    const uint32_t bm = wide ? 128 : 64;
+    const bool narrow = a.tokens <= 32;  // a short step: no lanes on absent tokens
+    const uint32_t bm = wide ? 128 : narrow ? 32 : 64;
     const uint32_t token_tiles = (a.tokens + bm - 1) / bm;
     uint32_t chunks = 1;
     if (range_sums) {
@@ -210,19 +223,23 @@ hipError_t launch_gemm_canonical(const Product& a, uint32_t format, uint32_t com
     switch (format) {
         case kQ4_0:
             wide ? go<kQ4_0, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-                 : go<kQ4_0, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
+                 : narrow ? go<kQ4_0, 32>(a, token_tiles, row_tiles, chunks, range_sums, stream)
+                          : go<kQ4_0, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
             break;
         case kQ4_1:
             wide ? go<kQ4_1, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-                 : go<kQ4_1, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
+                 : narrow ? go<kQ4_1, 32>(a, token_tiles, row_tiles, chunks, range_sums, stream)
+                          : go<kQ4_1, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
             break;
         case kQ8_0:
             wide ? go<kQ8_0, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-                 : go<kQ8_0, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
+                 : narrow ? go<kQ8_0, 32>(a, token_tiles, row_tiles, chunks, range_sums, stream)
+                          : go<kQ8_0, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
             break;
         case kQ6_K:
             wide ? go<kQ6_K, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-                 : go<kQ6_K, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
+                 : narrow ? go<kQ6_K, 32>(a, token_tiles, row_tiles, chunks, range_sums, stream)
+                          : go<kQ6_K, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
             break;
         default:
             return hipErrorInvalidValue;
