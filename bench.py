@@ -13,6 +13,10 @@ A step is one pass of the hot path over one batch of synthetic input:
       head on the last row
   c4, c5 run on the matrix cores (split-f16, within tolerance) and again on the
   canonical VALU tile (bit-exact), reported as c4_canonical, c5_canonical.
+  c6  a short prefill step, 32 tokens through Llama-3.2-1B's down projection
+      (2048x8192 Q4_0): split along K (c6_split), tiled (c6_tiled), matrix cores
+  c7  the embedding gather from Qwen3-0.6B's Q6_K table (151936x1024): a
+      512-token step and a decode step
 Inputs are seeded synthetic data (BASELINE's distributions) resident in HBM
 before timing; a GEMV's weights rotate over copies totalling > 2x the 256 MB
 MALL so every step reads HBM. Each config's launches are captured once in a
@@ -252,6 +256,29 @@ def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=No
             "tokens_per_s": tokens / (ms * 1e-3), "launches": len(launches), "head_gemv_bytes": head_bytes}
 
 
+def run_gather(S, name, gtype, rows, columns, tokens, steps, warmup, rng):
+    """The embedding gather of a step of `tokens` identifiers from a table of `rows` x `columns`:
+    bytes = the rows read (stored size) + the hidden rows written (4 a weight)."""
+    from charlotte_amd import synthetic
+
+    mm = S.mm
+    t0 = time.time()
+    table = mm.Weight(S.ctx, gtype, rows, columns, synthetic.weight(rng, gtype, rows, columns))
+    S.weights.append(table)
+    ids = S.buffer(rng.integers(0, rows, tokens).astype(np.uint32))
+    hidden = S.buffer(nbytes=4 * tokens * columns)
+
+    def body():
+        mm.gather(S.ctx, table, ids.ptr, tokens, hidden.ptr, stream=S.stream.handle)
+
+    ms = S.time_graph(body, steps, warmup)
+    nbytes = tokens * (synthetic.stored_bytes(gtype, 1, columns) + 4 * columns + 4)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"{name}: {tokens} rows of {rows}x{columns} (type {gtype}), setup {time.time() - t0:.1f}s: "
+        f"{ms * 1e3:.2f} us/step, {gbs:.0f} GB/s")
+    return {"ms_per_step": ms, "bytes": nbytes, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "tokens": tokens}
+
+
 def cpu_baseline_c2(stored, x, rows, columns, seconds=10.0):
     """The oracle's reference-order f32 GEMV (the CPU restatement of the
     reference's order of addition, oracle/liborc.so) over all of C2 on the
@@ -302,7 +329,7 @@ def main():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--only", default="c1,c2,c3,c4,c5,c6")
+    p.add_argument("--only", default="c1,c2,c3,c4,c5,c6,c7")
     p.add_argument("--no-cpu", action="store_true")
     args = p.parse_args()
     if args.gpus != 1:
@@ -354,11 +381,17 @@ def main():
             out["c6_tiled"] = run_gemm(S, "c6_tiled", plan, 32, args.steps, args.warmup, rng, S.mm.GemmPath.CANONICAL)
             out["c6_mfma"] = run_gemm(S, "c6_mfma", plan, 32, args.steps, args.warmup, rng,
                                       S.mm.GemmPath.SPLIT_F16_MFMA)
+        if "c7" in only:
+            # The embedding gather of Qwen3 0.6B's tied Q6_K table: a
+            # 512-token prefill step and a decode step.
+            for tokens in (512, 1):
+                out[f"c7_gather_{tokens}"] = run_gather(S, f"c7_gather_{tokens}", 14, 151936, 1024, tokens,
+                                                        args.steps, args.warmup, rng)
     finally:
         S.close()
 
     result = {"metric": METRIC, "unit": "GB/s", "higher_is_better": True, "n_gpus": 1, "scaling": "weak",
-              "vs_baseline": None, "dtype": "q6_k x f32 -> f32", "data": "synthetic (seeded; BASELINE distributions)"}
+              "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded; BASELINE distributions)"}
     if c2 is not None:
         cpu = None
         if not args.no_cpu:
@@ -369,7 +402,8 @@ def main():
             "value": round(c2["GB/s"], 1), "steps": max(args.steps, 20), "warmup": args.warmup,
             "ms_per_step": c2["ms_per_step"],
             "config": {"workload": "c2: Q6_K LM-head GEMV y[1,262144] = x[1,1152] W^T (Gemma-3-1B), repacked Q6_K",
-                       "rows": 262144, "columns": 1152, "weight_copies": c2["copies"]},
+                       "weights": "Q6_K (repacked), x and y f32", "rows": 262144, "columns": 1152,
+                       "weight_copies": c2["copies"]},
             "roofline": {"bound": "hbm", "achieved": round(c2["GB/s"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(c2["frac"], 4), "traffic": measured_traffic()},
             "cpu_baseline": cpu,
