@@ -4,7 +4,9 @@
 
 A step is one pass of the hot path over one batch of synthetic input:
   c1  Q4_0 decode GEMV 3072x1024 (Qwen3-0.6B FFN up)
-  c2  Q6_K LM-head GEMV 262144x1152, repacked (Gemma-3-1B)   <- the headline
+  c2  Q6_K LM-head GEMV 262144x1152, repacked (Gemma-3-1B)   <- the headline,
+      canonical order (bit-exact); again on the INT8_LIMBS decode (x as three
+      int8 limbs on the dot instructions, within 1e-5) as c2_limbs
   c3  Qwen3-0.6B decode sweep: 28 layers x 7 Q4_0 GEMVs + Q6_K head 151936x1024,
       launched as the reference's graph does (QKV and gate/up fused: 113 launches)
       and unfused (197)
@@ -351,6 +353,12 @@ def main():
         if "c2" in only:
             c2 = run_gemv(S, "c2", 14, 262144, 1152, max(args.steps, 20), args.warmup, np.random.default_rng(2))
             c2_x = c2["x"].read(np.float32)
+            S.ctx.set_gemv_path(S.mm.GemvPath.INT8_LIMBS)
+            r = run_gemv(S, "c2_limbs", 14, 262144, 1152, max(args.steps, 20), args.warmup,
+                         np.random.default_rng(2))
+            S.ctx.set_gemv_path(S.mm.GemvPath.CANONICAL)
+            out["c2_limbs"] = {k: v for k, v in r.items() if k not in ("stored", "x", "weights")}
+            out["c2_limbs"]["path"] = "INT8_LIMBS: within 1e-5 of the canonical order, not its bits"
         if "c1" in only:
             r = run_gemv(S, "c1", 2, 3072, 1024, max(args.steps, 100), args.warmup, np.random.default_rng(1))
             out["c1"] = {k: v for k, v in r.items() if k not in ("stored", "x", "weights")}

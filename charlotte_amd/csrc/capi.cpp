@@ -23,6 +23,7 @@ struct charlotte_hip_matmul_context {
     int device = 0;
     uint32_t compute_units = 0;
     charlotte_hip_matmul_gemm_path gemm_path = CHARLOTTE_HIP_MATMUL_GEMM_AUTO;
+    charlotte_hip_matmul_gemv_path gemv_path = CHARLOTTE_HIP_MATMUL_GEMV_CANONICAL;
     void* workspace = nullptr;  // the matrix-core path's, the caller's memory
     uint64_t workspace_bytes = 0;
     std::string error;
@@ -124,6 +125,15 @@ charlotte_hip_matmul_status charlotte_hip_matmul_set_gemm_path(charlotte_hip_mat
         path != CHARLOTTE_HIP_MATMUL_GEMM_SPLIT_F16_MFMA)
         return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gemm path: " + std::to_string(path));
     ctx->gemm_path = path;
+    return ok(ctx);
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_set_gemv_path(charlotte_hip_matmul_context* ctx,
+                                                               charlotte_hip_matmul_gemv_path path) {
+    if (!ctx) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    if (path != CHARLOTTE_HIP_MATMUL_GEMV_CANONICAL && path != CHARLOTTE_HIP_MATMUL_GEMV_INT8_LIMBS)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gemv path: " + std::to_string(path));
+    ctx->gemv_path = path;
     return ok(ctx);
 }
 
@@ -352,7 +362,7 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
         return fail(ctx, CHARLOTTE_HIP_MATMUL_UNSUPPORTED,
                     "launch: decode of K = " + std::to_string(head->columns) + " (built for K up to 8,192)");
     if (decode) {
-        e = chm::launch_gemv(a, head->type, ctx->compute_units, s);
+        e = chm::launch_gemv(a, head->type, ctx->compute_units, ctx->gemv_path == CHARLOTTE_HIP_MATMUL_GEMV_INT8_LIMBS, s);
     } else {
         // The split form takes the steps the gate allows whose range sums fit
         // the buffer; a product with options, or gated, never splits

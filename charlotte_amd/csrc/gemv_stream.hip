@@ -20,9 +20,17 @@
 // 8j .. 8j + 7; lane 0 adds its eight to zero, passes the partial total to
 // lane 1 (a quad permute), which adds its eight, and so on — the canonical
 // order, so the bits are every other kernel's.
+//
+// The LIMBS form (the GEMV path INT8_LIMBS, limbs.hpp) streams the same
+// bytes but stages x as int8 limb records and decodes a group with 24
+// v_dot4_i32_i8 in place of 32 exact weights and their fma chain — about
+// half the VALU work a step, which the copies feel twice: fewer instruction
+// cycles, and a higher clock (the SIMDs' load throttles it). A lane's nine
+// groups sum into one float from zero; the quad adds its four by two DPP
+// moves. Not the canonical bits: within 1e-5 of them.
 #include <algorithm>
 
-#include "decode.hpp"
+#include "limbs.hpp"
 #include "product.hpp"
 
 namespace chm {
@@ -34,7 +42,6 @@ constexpr uint32_t kStepGroups = kStepRows * 36;  // 576
 // bytes: 72 super-blocks).
 constexpr uint32_t kLoChunks = kStepGroups, kHiChunks = kStepGroups / 2, kScChunks = kStepGroups / 8, kDChunks = 9;
 
-typedef uint32_t u32x4s_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* lds_void;
 
 // vmcnt(0) alone, in s_waitcnt's gfx9 encoding (the other counters at
@@ -54,7 +61,6 @@ __device__ __forceinline__ void copy_stream(const uint8_t* from, u32x4s_t* to, u
 
 // A lane's share of a step, as held in registers between the stage and the
 // decode: its nine groups' lo and hi, their scale pairs, the two d's.
-typedef uint32_t u32x2s_t __attribute__((ext_vector_type(2)));
 struct StepRun {
     u32x4s_t lo[9];
     u32x2s_t hi[9];
@@ -62,13 +68,16 @@ struct StepRun {
     uint32_t d_first, d_next;
 };
 
-template <bool FULL>
+template <bool FULL, bool LIMBS>
 __global__ __launch_bounds__(256, 2) void gemv_stream(Product a, uint32_t steps) {
     __shared__ u32x4s_t lo_a[kStreamWaves][kLoChunks];
     __shared__ u32x4s_t hi_a[kStreamWaves][kHiChunks];
     __shared__ u32x4s_t sc_a[kStreamWaves][kScChunks];
     __shared__ u32x4s_t d_a[kStreamWaves][kDChunks];
-    __shared__ float4 xs[292];  // four slices of 72, one float4 of padding each
+    // x: four slices of 72 float4 and one of padding each; or (LIMBS) four
+    // slices of 9 group records and 4 dwords of padding each (the same size)
+    __shared__ u32x4s_t x_stage[292];
+    float4* const xs = reinterpret_cast<float4*>(x_stage);
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches
@@ -155,7 +164,7 @@ __global__ __launch_bounds__(256, 2) void gemv_stream(Product a, uint32_t steps)
     };
     // One step: the lane's nine groups, its eight range sums, the row's total
     // by the quad chain, the output.
-    auto decode = [&](uint32_t step, const StepRun& run) {
+    auto decode_exact = [&](uint32_t step, const StepRun& run) {
         float sums[8];
         float s = 0.0f;
         // x a group ahead: group i + 1's words are read before group i's
@@ -199,9 +208,34 @@ __global__ __launch_bounds__(256, 2) void gemv_stream(Product a, uint32_t steps)
             if (j == static_cast<uint32_t>(step_lane)) total = t;
         }
         const uint32_t p = step * kStepRows + rho;
-        float partner = 0.0f;
-        if (FULL && a.epilogue == kGated) partner = __shfl_xor(total, 4);
-        if (j == 3 && p < a.rows) emit<FULL>(a, p, 0, a.last_token ? a.tokens - 1 : 0, total, partner);
+        if (j == 3 && p < a.rows) emit<FULL>(a, p, 0, a.last_token ? a.tokens - 1 : 0, total, 0.0f);
+    };
+    // LIMBS: the lane's nine groups into one sum from zero, record i + 1 read
+    // while group i's products run; the quad's four sums added by DPP
+    // (lanes 0 + 1 and 2 + 3, then the pairs: every lane the same total).
+    auto decode_limbs = [&](uint32_t step, const StepRun& run) {
+        const u32x4s_t* records = x_stage + 73 * j;
+        u32x4s_t g[2][8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) g[0][v] = records[v];
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 9; ++i) {
+            if (i + 1 < 9) {
+#pragma unroll
+                for (int v = 0; v < 8; ++v) g[(i + 1) & 1][v] = records[8 * (i + 1) + v];
+            }
+            const uint32_t lw[4] = {run.lo[i][0], run.lo[i][1], run.lo[i][2], run.lo[i][3]};
+            const uint32_t hw[2] = {run.hi[i][0], run.hi[i][1]};
+            const uint32_t dbits = ((lg + i) >> 3) == (lg >> 3) ? run.d_first : run.d_next;
+            s = group_limbs_q6_k(lw, hw, run.sc[i], half_to_float(dbits), g[i & 1], s);
+        }
+        float total = s + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, s), 0xB1, 0xF, 0xF,
+                                                                              false));  // quad_perm [1, 0, 3, 2]
+        total = total + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, total), 0x4E, 0xF,
+                                                                           0xF, false));  // quad_perm [2, 3, 0, 1]
+        const uint32_t p = step * kStepRows + rho;
+        if (j == 3 && p < a.rows) emit<FULL>(a, p, 0, a.last_token ? a.tokens - 1 : 0, total, 0.0f);
     };
 
     // One step in flight a wave (two waves a SIMD): the next step's copy is
@@ -217,7 +251,20 @@ __global__ __launch_bounds__(256, 2) void gemv_stream(Product a, uint32_t steps)
     // The stores are written as instructions the compiler does not look
     // into: it would otherwise wait for the copy just issued before any LDS
     // store (it cannot tell x from the stage). Their wait is explicit.
-    {
+    if constexpr (LIMBS) {
+        // group g's record: slice g / 9, record g % 9; four lanes a group
+        const uint32_t t = threadIdx.x;
+        if (t < 4 * 36) {
+            const uint32_t group = t >> 2, part = t & 3u;
+            const float4* src =
+                reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(token) * 1152 + 32 * group + 8 * part);
+            const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(x_stage));
+            stage_limbs(clamp_input(a, src[0]), clamp_input(a, src[1]), part,
+                        base + 16 * (73 * (group / 9) + 8 * (group % 9)));
+        }
+        __asm__ __volatile__("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+    } else {
         const float4* src = reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(token) * 1152);
         const float4 x0 = src[threadIdx.x], x1 = src[min(threadIdx.x + 256, 287u)];
         const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(xs));
@@ -242,7 +289,10 @@ __global__ __launch_bounds__(256, 2) void gemv_stream(Product a, uint32_t steps)
         take(run, sa);
         const uint32_t next = step + waves;
         if (next < steps) issue(next, sa);
-        decode(step, run);
+        if constexpr (LIMBS)
+            decode_limbs(step, run);
+        else
+            decode_exact(step, run);
         if (next >= steps) break;
         step = next;
     }
@@ -259,13 +309,20 @@ bool gemv_stream_takes(const Product& a, uint32_t format) {
     return true;
 }
 
-hipError_t launch_gemv_stream(const Product& a, uint32_t compute_units, hipStream_t stream) {
+hipError_t launch_gemv_stream(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream) {
     const uint32_t steps = a.rows / kStepRows;
     const uint32_t blocks = std::min<uint32_t>(2 * compute_units, (steps + kStreamWaves - 1) / kStreamWaves);
-    if (plain_epilogue(a))
-        hipLaunchKernelGGL((gemv_stream<false>), dim3(blocks), dim3(256), 0, stream, a, steps);
-    else
-        hipLaunchKernelGGL((gemv_stream<true>), dim3(blocks), dim3(256), 0, stream, a, steps);
+    const bool plain = plain_epilogue(a);
+    if (limbs) {
+        if (plain)
+            hipLaunchKernelGGL((gemv_stream<false, true>), dim3(blocks), dim3(256), 0, stream, a, steps);
+        else
+            hipLaunchKernelGGL((gemv_stream<true, true>), dim3(blocks), dim3(256), 0, stream, a, steps);
+    } else if (plain) {
+        hipLaunchKernelGGL((gemv_stream<false, false>), dim3(blocks), dim3(256), 0, stream, a, steps);
+    } else {
+        hipLaunchKernelGGL((gemv_stream<true, false>), dim3(blocks), dim3(256), 0, stream, a, steps);
+    }
     return hipGetLastError();
 }
 

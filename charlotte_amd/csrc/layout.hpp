@@ -23,7 +23,8 @@ bool lay_out(uint32_t format, const uint8_t* stored, uint64_t blocks, uint8_t* d
 void repack_q6_k(const uint8_t* stored, uint64_t blocks, uint8_t* lo, uint8_t* hi, uint8_t* scales, uint8_t* d);
 
 bool gemv_supports(uint32_t groups);
-hipError_t launch_gemv(const Product& a, uint32_t format, uint32_t compute_units, hipStream_t stream);
+bool gemv_limbs_takes(const Product& a, uint32_t format);
+hipError_t launch_gemv(const Product& a, uint32_t format, uint32_t compute_units, bool limbs, hipStream_t stream);
 hipError_t launch_gemm_canonical(const Product& a, uint32_t format, uint32_t compute_units, float* range_sums,
                                  hipStream_t stream);
 uint64_t mfma_workspace_bytes(uint32_t tokens, uint32_t groups);

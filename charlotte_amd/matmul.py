@@ -74,6 +74,15 @@ class GemmPath(enum.IntEnum):
     SPLIT_F16_MFMA = 2
 
 
+class GemvPath(enum.IntEnum):
+    """The decode kernel: CANONICAL (bit-exact, the default) or INT8_LIMBS (x as
+    three int8 limbs on the dot instructions, within 1e-5; built for the streamed
+    Q6_K shapes, K = 1,152 and rows in 16s; other shapes decode canonically)."""
+
+    CANONICAL = 0
+    INT8_LIMBS = 1
+
+
 class MatmulError(RuntimeError):
     def __init__(self, status, message=""):
         self.status = Status(status)
@@ -160,6 +169,7 @@ SIGNATURES = {
     "charlotte_hip_matmul_context_destroy": (_c.c_int, [_c.c_void_p]),
     "charlotte_hip_matmul_last_error": (_c.c_char_p, [_c.c_void_p]),
     "charlotte_hip_matmul_set_gemm_path": (_c.c_int, [_c.c_void_p, _c.c_int]),
+    "charlotte_hip_matmul_set_gemv_path": (_c.c_int, [_c.c_void_p, _c.c_int]),
     "charlotte_hip_matmul_set_workspace": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_uint64]),
     "charlotte_hip_matmul_workspace_bytes": (_c.c_uint64, [_c.c_uint32, _c.c_uint64]),
     "charlotte_hip_matmul_layout_bytes": (_c.c_uint64, [_c.c_uint32, _c.c_uint64, _c.c_uint64]),
@@ -278,6 +288,9 @@ class Context:
 
     def set_gemm_path(self, path: GemmPath):
         self.check(lib.charlotte_hip_matmul_set_gemm_path(self.handle, int(path)))
+
+    def set_gemv_path(self, path: GemvPath):
+        self.check(lib.charlotte_hip_matmul_set_gemv_path(self.handle, int(path)))
 
     def set_workspace(self, device_ptr, nbytes):
         """The matrix-core path's working memory (device pointer, bytes); 0, 0 unsets it."""

@@ -41,7 +41,8 @@
  * are borrowed until the stream reaches the launch. No launch allocates.
  *
  * Order of addition (determinism, batch invariance): every path but the
- * matrix-core prefill adds each output's products in the reference's one
+ * matrix-core prefill and the INT8_LIMBS decode (both opt-in, within
+ * tolerance; below) adds each output's products in the reference's one
  * order, fixed by K alone (matmul.h:34-50): a row's G = K / 32 groups cut into
  * 32 ranges, range r groups floor(rG/32) .. floor((r+1)G/32), each range an
  * fma chain from zero in k order, the 32 range sums added in order to a total
@@ -117,6 +118,22 @@ typedef enum {
     CHARLOTTE_HIP_MATMUL_GEMM_SPLIT_F16_MFMA = 2
 } charlotte_hip_matmul_gemm_path;
 
+/* Which decode kernel runs (no counterpart: the reference decodes in its one
+ * order). CANONICAL, the default, adds in the order above, bit-exact and
+ * batch-invariant. INT8_LIMBS splits x, a 32-weight group at a time, into a
+ * 22-bit fixed-point value (the group's max |x| sets the exponent) cut into
+ * three int8 limbs, and sums code x limb products exactly in int32 on the dot
+ * instructions, 16 weights at a time, before the scales and an f32 sum:
+ * within max|err| / max|y| <= 1e-5 of the canonical order, not its bits, and
+ * not batch-invariant with prefill; a non-finite input makes the outputs NaN.
+ * It is built for the shapes of the streamed Q6_K decode (K = 1,152, each
+ * member's rows and first row multiples of 16, any epilogue but the gated
+ * one); every other decode runs CANONICAL whatever the setting. */
+typedef enum {
+    CHARLOTTE_HIP_MATMUL_GEMV_CANONICAL = 0,
+    CHARLOTTE_HIP_MATMUL_GEMV_INT8_LIMBS = 1
+} charlotte_hip_matmul_gemv_path;
+
 typedef struct charlotte_hip_matmul_context charlotte_hip_matmul_context;
 typedef struct charlotte_hip_matmul_weight charlotte_hip_matmul_weight;
 
@@ -128,6 +145,8 @@ charlotte_hip_matmul_status charlotte_hip_matmul_context_destroy(charlotte_hip_m
 const char* charlotte_hip_matmul_last_error(const charlotte_hip_matmul_context* ctx);
 charlotte_hip_matmul_status charlotte_hip_matmul_set_gemm_path(charlotte_hip_matmul_context* ctx,
                                                                charlotte_hip_matmul_gemm_path path);
+charlotte_hip_matmul_status charlotte_hip_matmul_set_gemv_path(charlotte_hip_matmul_context* ctx,
+                                                               charlotte_hip_matmul_gemv_path path);
 
 /* The matrix-core prefill's working memory (no counterpart in the reference,
  * whose one prefill kernel needs none): the step's input split into two

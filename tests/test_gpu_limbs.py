@@ -1,0 +1,216 @@
+"""The INT8_LIMBS decode on the GPU (x as three int8 limbs a 32-weight group,
+products on the dot instructions), held to the stated tolerance against the
+CPU oracle: max |y - y_f64| / max |y_f64| <= 1e-5, and each row's argmax the
+reference-order f32 product's wherever its top two differ by more than the
+error allows (BASELINE's bar, as the matrix-core prefill's tests hold it).
+
+The path is not bit-exact by design. These tests pin its error at the shapes
+it is built for (Q6_K, K = 1,152, rows in 16s), over inputs of every scale,
+with outliers, zeros and non-finite values, through each epilogue it takes;
+and that every other decode still runs in the canonical order, bit for bit.
+"""
+
+import numpy as np
+import pytest
+
+from tests.support.oracle_lib import Q4_0, Q6_K
+
+pytestmark = pytest.mark.gpu
+
+TOLERANCE = 1e-5
+K = 1152
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from charlotte_amd import matmul as mm
+
+    c = mm.Context(0)
+    c.set_gemv_path(mm.GemvPath.INT8_LIMBS)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def run(ctx):
+    from tests.support.gpu import Runner
+
+    return Runner(ctx)
+
+
+@pytest.fixture(scope="module")
+def canonical_run():
+    from charlotte_amd import matmul as mm
+    from tests.support.gpu import Runner
+
+    c = mm.Context(0)
+    yield Runner(c)
+    c.close()
+
+
+def _data(rows, seed, scale=1.0, columns=K, gtype=Q6_K):
+    from charlotte_amd import synthetic
+
+    rng = np.random.default_rng(seed)
+    return synthetic.weight(rng, gtype, rows, columns), synthetic.activations(rng, 1, columns) * np.float32(scale)
+
+
+def _within(got, y64, canonical, what):
+    assert np.isfinite(got).all(), f"{what}: non-finite outputs"
+    err = np.abs(got.astype(np.float64) - y64).max()
+    top = np.abs(y64).max()
+    assert err <= TOLERANCE * top, f"{what}: max err {err:.3e} vs max |y| {top:.3e} ({err / top:.2e})"
+    for t in range(got.shape[0]):
+        a, b = int(np.argmax(got[t])), int(np.argmax(canonical[t]))
+        if a != b:
+            s = np.sort(y64[t])
+            assert s[-1] - s[-2] <= 2 * err, f"{what}: row argmax {a} vs {b}"
+    return err / top
+
+
+@pytest.mark.parametrize("rows", [16, 48, 1040, 8192])
+def test_limbs_within_tolerance(oracle, run, rows):
+    stored, x = _data(rows, seed=rows)
+    w = run.weight(Q6_K, rows, K, stored)
+    got = run.write(w, x, 1)
+    y64, _ = oracle.matmul_f64(Q6_K, stored, rows, K, x)
+    canonical = oracle.matmul_f32(Q6_K, stored, rows, K, x, threads=8)
+    ratio = _within(got, y64, canonical, f"{rows} rows")
+    assert ratio < 2e-6, f"{rows} rows: error {ratio:.2e} well above the path's usual 3e-7"
+    w.free()
+
+
+@pytest.mark.parametrize("kind", ["1e-30", "1e-6", "3e4", "1e30", "outliers", "one-hot", "zero-groups", "mixed-scales"])
+def test_limbs_input_scaling(oracle, run, kind):
+    """Each group's exponent follows its own max: tiny, huge, outlier-laden,
+    one-hot, partly zero and group-to-group rescaled inputs keep the bar."""
+    rows = 512
+    stored, x = _data(rows, seed=11)
+    rng = np.random.default_rng(12)
+    if kind in ("1e-30", "1e-6", "3e4", "1e30"):
+        x = x * np.float32(float(kind))
+    elif kind == "outliers":
+        x[0, rng.choice(K, 12, replace=False)] *= np.float32(1000.0)
+    elif kind == "one-hot":
+        x[:] = 0.0
+        x[0, 777] = 2.5
+    elif kind == "zero-groups":
+        x[0, (np.arange(K) // 32) % 3 == 0] = 0.0
+    else:
+        x[0] *= np.repeat(np.float32(10.0) ** rng.integers(-12, 12, K // 32), 32).astype(np.float32)
+    w = run.weight(Q6_K, rows, K, stored)
+    got = run.write(w, x, 1)
+    y64, _ = oracle.matmul_f64(Q6_K, stored, rows, K, x)
+    canonical = oracle.matmul_f32(Q6_K, stored, rows, K, x)
+    _within(got, y64, canonical, kind)
+    w.free()
+
+
+def test_limbs_zero_input_gives_zeros(run):
+    stored, x = _data(64, seed=5)
+    w = run.weight(Q6_K, 64, K, stored)
+    got = run.write(w, np.zeros_like(x), 1)
+    assert (got == 0).all()
+    w.free()
+
+
+@pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
+def test_limbs_non_finite_input_makes_nan(run, bad):
+    stored, x = _data(64, seed=6)
+    x[0, 500] = bad
+    w = run.weight(Q6_K, 64, K, stored)
+    got = run.write(w, x, 1)
+    assert np.isnan(got).all()
+    w.free()
+
+
+def test_limbs_repeatable(run):
+    """Same inputs, same bits: the path is deterministic, if not canonical."""
+    from tests.support.gpu import bits_equal
+
+    stored, x = _data(4096, seed=21)
+    w = run.weight(Q6_K, 4096, K, stored)
+    a = run.write(w, x, 1)
+    b = run.write(w, x, 1)
+    assert bits_equal(a, b)
+    w.free()
+
+
+def test_limbs_epilogues(oracle, run):
+    """QKV members, Write with clip, bias and activation, GatedByInput and the
+    head's last-token row: the epilogue applied to the path's totals."""
+    from charlotte_amd import matmul as mm
+
+    widths = [256, 128, 128]
+    data = [_data(r, seed=90 + i) for i, r in enumerate(widths)]
+    x = data[0][1]
+    ws = [run.weight(Q6_K, r, K, d[0]) for r, d in zip(widths, data)]
+    totals64 = [oracle.matmul_f64(Q6_K, d[0], r, K, x)[0] for r, d in zip(widths, data)]
+    f32 = [oracle.matmul_f32(Q6_K, d[0], r, K, x) for r, d in zip(widths, data)]
+    got = run.product([mm.Member(w) for w in ws], x, 1, widths, epilogue=mm.Epilogue.QKV)
+    for i in range(3):
+        _within(got[i], totals64[i], f32[i], f"QKV member {i}")
+    u = np.random.default_rng(95).standard_normal((1, 256), dtype=np.float32)
+    got = run.product([mm.Member(ws[0])], x, 1, [256], epilogue=mm.Epilogue.GatedByInput, gate_input=u,
+                      gate_input_stride=256, activation=mm.Activation.SiLU)[0]
+    want = oracle.gated_by_input(totals64[0].astype(np.float32), u, activation=0)
+    _within(got, want.astype(np.float64), want, "GatedByInput")
+    for activation in (mm.Activation.SiLU, mm.Activation.GeluTanh, mm.Activation.Sigmoid):
+        clip = np.array([-1.0, 1.5, -3.0, 2.5], np.float32)
+        bias = np.linspace(-0.5, 0.5, 256, dtype=np.float32)
+        xc = oracle.clamp(x, clip[0], clip[1])
+        t64, _ = oracle.matmul_f64(Q6_K, data[0][0], 256, K, xc)
+        got = run.product([mm.Member(ws[0])], x, 1, [256], clip=clip, bias=bias, activated=True,
+                          activation=activation)[0]
+        want = oracle.finish(t64.astype(np.float32), clip=clip, bias=bias, activated=True, activation=int(activation))
+        _within(got, want.astype(np.float64), want, f"Write with options, activation {activation.name}")
+    # The head: the last of three token rows, one output row.
+    xs = np.concatenate([np.random.default_rng(96).standard_normal((2, K), dtype=np.float32), x])
+    got = run.write(ws[0], xs, 3, rows=mm.Rows.LastToken)
+    _within(got, totals64[0], f32[0], "last token")
+    for w in ws:
+        w.free()
+
+
+@pytest.mark.parametrize("gtype,rows,columns", [(Q6_K, 100, K), (Q6_K, 64, 2048), (Q4_0, 3072, 1024)])
+def test_other_decodes_stay_canonical(oracle, run, gtype, rows, columns):
+    """Shapes the path is not built for decode in the canonical order: the
+    oracle's bits, whatever the setting."""
+    from tests.support.gpu import bits_equal, first_difference
+
+    stored, x = _data(rows, seed=rows + columns, columns=columns, gtype=gtype)
+    w = run.weight(gtype, rows, columns, stored)
+    got = run.write(w, x, 1)
+    want = oracle.matmul_f32(gtype, stored, rows, columns, x)
+    assert bits_equal(got, want), first_difference(got, want)
+    w.free()
+
+
+def test_limbs_at_c2_size_against_canonical(run, canonical_run):
+    """The C2 shape (Gemma 3 1B head, 262,144 x 1,152): the limbs path within
+    the bar of the canonical path, which is the oracle's bits at every size."""
+    from charlotte_amd import synthetic
+
+    rows = 262144
+    rng = np.random.default_rng(0xC2)
+    stored = synthetic.q6_k(rng, rows, K)
+    x = synthetic.activations(rng, 1, K)
+    w = run.weight(Q6_K, rows, K, stored)
+    got = run.write(w, x, 1)
+    w.free()
+    wc = canonical_run.weight(Q6_K, rows, K, stored)
+    want = canonical_run.write(wc, x, 1)
+    wc.free()
+    assert np.isfinite(got).all()
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64)).max()
+    top = np.abs(want).max()
+    assert err <= TOLERANCE * top, f"{err:.3e} vs {top:.3e}"
+    assert int(np.argmax(got)) == int(np.argmax(want)) or np.sort(want[0])[-1] - np.sort(want[0])[-2] <= 2 * err
+
+
+def test_gemv_path_setter_refuses_an_unknown_path(ctx):
+    from charlotte_amd import matmul as mm
+
+    with pytest.raises(mm.MatmulError) as e:
+        ctx.set_gemv_path(7)
+    assert e.value.status == mm.Status.INVALID_ARGUMENT
