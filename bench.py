@@ -314,16 +314,19 @@ def run_copy(S, nbytes=256 << 20, reps=5):
     log(f"copy: {reps} x {nbytes >> 20} MiB")
 
 
-def measured_traffic():
-    """HBM bytes per launch of the headline kernel, from the rocprofv3 counter
-    runs recorded in profiles/traffic_c2.json (FETCH_SIZE and WRITE_SIZE in KiB
-    per dispatch, each scaled by what the counter reads for a copy of known
-    size); None when absent."""
+def measured_traffic(limbs=False):
+    """HBM bytes per launch of the headline kernel (or of its INT8_LIMBS form),
+    from the rocprofv3 counter runs recorded in profiles/traffic_c2.json
+    (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by what the
+    counter reads for a copy of known size); None when absent."""
     path = os.path.join(ROOT, "profiles", "traffic_c2.json")
     if not os.path.exists(path):
         return None
     t = json.load(open(path))
-    return int(round((t["fetch_kib"] * t["fetch_scale"] + t["write_kib"] * t["write_scale"]) * 1024))
+    k = t.get("limbs") if limbs else t
+    if k is None:
+        return None
+    return int(round((k["fetch_kib"] * t["fetch_scale"] + k["write_kib"] * t["write_scale"]) * 1024))
 
 
 def main():
@@ -359,6 +362,9 @@ def main():
             S.ctx.set_gemv_path(S.mm.GemvPath.CANONICAL)
             out["c2_limbs"] = {k: v for k, v in r.items() if k not in ("stored", "x", "weights")}
             out["c2_limbs"]["path"] = "INT8_LIMBS: within 1e-5 of the canonical order, not its bits"
+            out["c2_limbs"]["roofline"] = {"bound": "hbm", "achieved": round(r["GB/s"], 1), "peak": HBM_PEAK_GBS,
+                                           "unit": "GB/s", "frac": round(r["frac"], 4),
+                                           "traffic": measured_traffic(limbs=True)}
         if "c1" in only:
             r = run_gemv(S, "c1", 2, 3072, 1024, max(args.steps, 100), args.warmup, np.random.default_rng(1))
             out["c1"] = {k: v for k, v in r.items() if k not in ("stored", "x", "weights")}
