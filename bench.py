@@ -23,7 +23,9 @@ Inputs are seeded synthetic data (BASELINE's distributions) resident in HBM
 before timing; a GEMV's weights rotate over copies totalling > 2x the 256 MB
 MALL so every step reads HBM. Each config's launches are captured once in a
 HIP graph and replayed; HIP events on the launch stream bracket the K timed
-steps. One JSON line on stdout; progress on stderr.
+steps, five times over, and the median is reported (C1-C3 also eagerly, one
+launch at a time: ms_single_launch). One JSON line on stdout; progress on
+stderr. `--cpu-table` instead times the CPU baseline table of C1-C5 (host only).
 """
 
 import argparse
@@ -85,9 +87,11 @@ class Setup:
             out.append(w)
         return out
 
-    def time_graph(self, body, steps, warmup, launches_a_step=1):
+    def time_graph(self, body, steps, warmup, reps=5):
         """Capture body() (one step's launches) `steps` times into a graph; replay it
-        once untimed (warmup), then timed; return ms per step."""
+        once untimed (warmup), then `reps` times timed, each between HIP events on
+        the launch stream; return the median ms per step (the spread is kept in
+        self.last_reps)."""
         hx = self.hx
         # warmup, eager
         for _ in range(warmup):
@@ -97,15 +101,36 @@ class Setup:
         graph.launch()  # untimed replay: first-launch costs
         self.stream.sync()
         start, stop = hx.Event(), hx.Event()
-        start.record(self.stream)
-        graph.launch()
-        stop.record(self.stream)
-        stop.sync()
-        ms = start.elapsed_ms(stop) / steps
+        times = []
+        for _ in range(reps):
+            start.record(self.stream)
+            graph.launch()
+            stop.record(self.stream)
+            stop.sync()
+            times.append(start.elapsed_ms(stop) / steps)
         graph.destroy()
         start.destroy()
         stop.destroy()
-        return ms
+        self.last_reps = times
+        return float(np.median(times))
+
+    def time_single(self, body, reps=20):
+        """body() launched eagerly (no graph), each time between HIP events and
+        synchronized: the single-launch figure, launch cost included; median ms."""
+        hx = self.hx
+        body()
+        self.stream.sync()
+        start, stop = hx.Event(), hx.Event()
+        times = []
+        for _ in range(reps):
+            start.record(self.stream)
+            body()
+            stop.record(self.stream)
+            stop.sync()
+            times.append(start.elapsed_ms(stop))
+        start.destroy()
+        stop.destroy()
+        return float(np.median(times))
 
     def close(self):
         for w in self.weights:
@@ -137,11 +162,14 @@ def run_gemv(S, name, gtype, rows, columns, steps, warmup, rng, copies=None):
 
     log(f"{name}: {rows}x{columns} {'Q4_0' if gtype == 2 else 'Q6_K'}, {copies} copies, setup {time.time() - t0:.1f}s")
     ms = S.time_graph(body, steps, warmup)
+    spread = [round(t * 1e3, 2) for t in S.last_reps]
+    single = S.time_single(body)
     nbytes = gemv_bytes(gtype, rows, columns)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f"{name}: {ms * 1e3:.2f} us/launch, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
+    log(f"{name}: {ms * 1e3:.2f} us/launch (median of {spread} us), {gbs:.0f} GB/s "
+        f"({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s); single launch {single * 1e3:.2f} us")
     return {"ms_per_step": ms, "bytes": nbytes, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "copies": copies,
-            "stored": stored, "x": x, "weights": ws}
+            "ms_single_launch": single, "stored": stored, "x": x, "weights": ws}
 
 
 def build_products(S, rng, plan, tokens, gtype=2):
@@ -214,10 +242,12 @@ def run_c3(S, steps, warmup, rng, fused=True):
             mm.launch(S.ctx, m, 1, stream=S.stream.handle)
 
     ms = S.time_graph(body, steps, warmup)
+    single = S.time_single(body, reps=5)
     gbs = total / (ms * 1e-3) / 1e9
-    log(f"{tag}: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s aggregate, {1e3 / ms:.0f} tokens/s")
+    log(f"{tag}: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s aggregate, {1e3 / ms:.0f} tokens/s; "
+        f"launched eagerly {single * 1e3:.1f} us/step")
     return {"ms_per_step": ms, "bytes": total, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "launches": len(launches),
-            "tokens_per_s": 1e3 / ms}
+            "tokens_per_s": 1e3 / ms, "ms_single_launch": single}
 
 
 def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=None):
@@ -303,6 +333,79 @@ def cpu_baseline_c2(stored, x, rows, columns, seconds=10.0):
                       f"of {t * 1e3:.1f} ms; oracle/liborc.so on {threads} threads"}
 
 
+def cpu_table(threads_all):
+    """The CPU baseline table: the oracle's reference-order f32 product and its
+    f64 product (the reference tests' check) for C1-C5, on one thread and on
+    `threads_all`, median of the runs made. C1-C4 run in full; C5 is one layer
+    timed on 128 of its 2,048 token rows, scaled by 16 (tokens) and 16
+    (layers; the head, a GEMV, is left out); single-thread C4 and C5 are one
+    run each. Host only: no GPU call."""
+    from charlotte_amd import synthetic
+    from tests.support.oracle_lib import Oracle
+
+    oracle = Oracle()
+    rng = np.random.default_rng(0xC9)
+
+    def timed(fn, reps):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    def products(shapes, tokens):
+        out = []
+        for gtype, rows, columns, count in shapes:
+            out.append((gtype, rows, columns, synthetic.weight(rng, gtype, rows, columns),
+                        synthetic.activations(rng, tokens, columns), count))
+        return out
+
+    def run(kind, prods, threads, reps):
+        # each distinct product timed; products that repeat (layers) count `count` times
+        total = 0.0
+        for prod in prods:
+            one = [prod]
+            def fn_one(one=one):
+                gtype, rows, columns, stored, x, _ = one[0]
+                if kind == "f32":
+                    oracle.matmul_f32(gtype, stored, rows, columns, x, threads=threads)
+                else:
+                    oracle.matmul_f64(gtype, stored, rows, columns, x, threads=threads)
+            total += timed(fn_one, reps) * prod[5]
+        return total
+
+    c3_layer = [(2, 2048, 1024, 28), (2, 1024, 1024, 56), (2, 1024, 2048, 28), (2, 3072, 1024, 56), (2, 1024, 3072, 28)]
+    c5_layer = [(2, 2048, 2048, 32), (2, 512, 2048, 32), (2, 8192, 2048, 32), (2, 2048, 8192, 16)]
+    configs = [
+        ("c1", products([(2, 3072, 1024, 1)], 1), "GB/s", gemv_bytes(2, 3072, 1024), 1.0, 1),
+        ("c2", products([(14, 262144, 1152, 1)], 1), "GB/s", gemv_bytes(14, 262144, 1152), 1.0, 1),
+        ("c3", products(c3_layer + [(14, 151936, 1024, 1)], 1), "GB/s",
+         sum(gemv_bytes(g, r, c) * n for g, r, c, n in c3_layer) + gemv_bytes(14, 151936, 1024), 1.0, 1),
+        ("c4", products([(2, 8192, 2048, 1)], 512), "TFLOP/s", 2 * 512 * 8192 * 2048, 1.0, 0),
+        ("c5", products(c5_layer, 128), "TFLOP/s", 2 * 2048 * sum(r * c * n for _, r, c, n in c5_layer), 16.0, 0),
+    ]
+    rows_out = []
+    for name, prods, unit, work, scale, small in configs:
+        for kind in ("f32", "f64"):
+            for threads in (1, threads_all):
+                reps = 5 if small or threads > 1 else 1
+                t = run(kind, prods, threads, reps) * scale
+                value = work / t / (1e9 if unit == "GB/s" else 1e12)
+                rows_out.append({"config": name, "kind": kind, "threads": threads, "seconds": t, "value": value,
+                                 "unit": unit, "runs": reps,
+                                 "note": "one layer on 128 of 2048 token rows, x16 tokens x16 layers" if name == "c5"
+                                 else "in full"})
+                log(f"cpu {name} {kind} {threads} thread(s): {t:.4f} s, {value:.3f} {unit}")
+    model = ""
+    try:
+        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return {"cpu_table": rows_out, "host": {"cpus": os.cpu_count(), "threads_used": threads_all, "model": model}}
+
+
 def run_copy(S, nbytes=256 << 20, reps=5):
     """A plain device copy of known size: the yardstick the HBM counters
     (rocprofv3 FETCH_SIZE / WRITE_SIZE) are scaled by."""
@@ -336,7 +439,12 @@ def main():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--only", default="c1,c2,c3,c4,c5,c6,c7")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-table", action="store_true",
+                   help="time the CPU baseline table (C1-C5, f32 and f64, 1 and all threads) and exit")
     args = p.parse_args()
+    if args.cpu_table:
+        print(json.dumps(cpu_table(min(os.cpu_count() or 1, 16))), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this path is measured on one MI355X); got --gpus {args.gpus}",
               file=sys.stderr)

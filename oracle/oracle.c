@@ -383,33 +383,75 @@ int orc_matmul_f32(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t
 
 /* tests/gpu/matmul_test.cpp:190-211: each output in f64 over the decoded
  * weights, and its bound gamma(2K) * sum_k |w x|, gamma(n) = nu / (1 - nu),
- * u = 2^-24. */
-int orc_matmul_f64(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t columns, const float* x,
-                   uint32_t tokens, double* y, double* bound) {
-    if (columns % 32 != 0) return -1;
-    const uint64_t K = columns;
+ * u = 2^-24. Rows [r0, r1) of the product, one job of orc_matmul_f64_threads. */
+struct f64_job {
+    uint32_t type;
+    const uint8_t* blocks;
+    uint64_t rows, columns, r0, r1;
+    const float* x;
+    uint32_t tokens;
+    double *y, *bound;
+    int status;
+};
+
+static void* f64_rows(void* arg) {
+    struct f64_job* j = arg;
+    const uint64_t K = j->columns;
     const double nu = (double)(2 * K) * ldexp(1.0, -24);
     const double gamma = nu / (1 - nu);
     float* w = malloc((size_t)(K * sizeof(float)));
-    if (!w) return -2;
-    for (uint64_t o = 0; o < rows; ++o) {
-        if (orc_dequantize_range(type, blocks, o * K, K, w) != 0) {
-            free(w);
-            return -1;
+    if (!w) {
+        j->status = -2;
+        return NULL;
+    }
+    for (uint64_t o = j->r0; o < j->r1; ++o) {
+        if (orc_dequantize_range(j->type, j->blocks, o * K, K, w) != 0) {
+            j->status = -1;
+            break;
         }
-        for (uint32_t t = 0; t < tokens; ++t) {
+        for (uint32_t t = 0; t < j->tokens; ++t) {
             double sum = 0, absolute = 0;
             for (uint64_t k = 0; k < K; ++k) {
-                const double p = (double)w[k] * (double)x[(uint64_t)t * K + k];
+                const double p = (double)w[k] * (double)j->x[(uint64_t)t * K + k];
                 sum += p;
                 absolute += fabs(p);
             }
-            y[(uint64_t)t * rows + o] = sum;
-            if (bound) bound[(uint64_t)t * rows + o] = gamma * absolute;
+            j->y[(uint64_t)t * j->rows + o] = sum;
+            if (j->bound) j->bound[(uint64_t)t * j->rows + o] = gamma * absolute;
         }
     }
     free(w);
-    return 0;
+    return NULL;
+}
+
+/* The same on `threads` host threads, rows split evenly (each output is one
+ * thread's whole sum, so the values do not depend on the count). */
+int orc_matmul_f64_threads(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t columns, const float* x,
+                           uint32_t tokens, double* y, double* bound, uint32_t threads) {
+    if (columns % 32 != 0) return -1;
+    if (threads < 1) threads = 1;
+    if (threads > 256) threads = 256;
+    struct f64_job jobs[256];
+    pthread_t ids[256];
+    for (uint32_t i = 0; i < threads; ++i)
+        jobs[i] = (struct f64_job){type, blocks, rows, columns, rows * i / threads, rows * (i + 1) / threads,
+                                   x, tokens, y, bound, 0};
+    if (threads == 1) {
+        f64_rows(&jobs[0]);
+        return jobs[0].status;
+    }
+    for (uint32_t i = 0; i < threads; ++i) pthread_create(&ids[i], NULL, f64_rows, &jobs[i]);
+    int status = 0;
+    for (uint32_t i = 0; i < threads; ++i) {
+        pthread_join(ids[i], NULL);
+        if (jobs[i].status != 0) status = jobs[i].status;
+    }
+    return status;
+}
+
+int orc_matmul_f64(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t columns, const float* x,
+                   uint32_t tokens, double* y, double* bound) {
+    return orc_matmul_f64_threads(type, blocks, rows, columns, x, tokens, y, bound, 1);
 }
 
 /* ---- the reference tests' input fill -------------------------------------- */

@@ -39,6 +39,8 @@
  *                           bits differ between orders (test_oracle.py), plus
  *                           within gamma(2K) of orc_matmul_f64.
  *   orc_matmul_f64          brute force against numpy float64 dot products.
+ *   orc_matmul_f64_threads  the same rows split over threads: equal to the
+ *                           one-thread result element for element (test).
  *   orc_fill_unit           the hash of tests/gpu/support/fill.h:24-29, pinned
  *                           by its range and by recomputation in numpy.
  *   orc_activate            against math.exp/tanh within its stated bound.
@@ -93,6 +95,8 @@ int orc_matmul_f32(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t
 /* The same in f64, and each output's bound gamma(2K) * sum |w x|. */
 int orc_matmul_f64(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t columns, const float* x,
                    uint32_t tokens, double* y, double* bound);
+int orc_matmul_f64_threads(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t columns, const float* x,
+                           uint32_t tokens, double* y, double* bound, uint32_t threads);
 
 /* tests/gpu/support/fill.h:24-29: a value in [-1, 1) for index i. */
 float orc_fill_unit(uint32_t i);

@@ -57,6 +57,8 @@ class Oracle:
                                        ctypes.c_uint32, _f32p, ctypes.c_uint32]
         lib.orc_matmul_f64.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64, _f32p,
                                        ctypes.c_uint32, _f64p, _f64p]
+        lib.orc_matmul_f64_threads.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64, _f32p,
+                                               ctypes.c_uint32, _f64p, _f64p, ctypes.c_uint32]
         lib.orc_fill_unit.restype = ctypes.c_float
         lib.orc_fill_unit.argtypes = [ctypes.c_uint32]
         lib.orc_fill.argtypes = [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, _f32p]
@@ -152,13 +154,18 @@ class Oracle:
                                        _ptr(y, _f32p), threads) == 0
         return y
 
-    def matmul_f64(self, gtype, blocks, rows, columns, x):
+    def matmul_f64(self, gtype, blocks, rows, columns, x, threads=1):
         b = _bytes(blocks)
         x = np.ascontiguousarray(x, np.float32).reshape(-1, columns)
         y = np.empty((x.shape[0], rows), np.float64)
         bound = np.empty_like(y)
-        assert self.lib.orc_matmul_f64(gtype, _ptr(b, _u8p), rows, columns, _ptr(x, _f32p), x.shape[0],
-                                       _ptr(y, _f64p), _ptr(bound, _f64p)) == 0
+        if threads == 1:
+            status = self.lib.orc_matmul_f64(gtype, _ptr(b, _u8p), rows, columns, _ptr(x, _f32p), x.shape[0],
+                                             _ptr(y, _f64p), _ptr(bound, _f64p))
+        else:
+            status = self.lib.orc_matmul_f64_threads(gtype, _ptr(b, _u8p), rows, columns, _ptr(x, _f32p),
+                                                     x.shape[0], _ptr(y, _f64p), _ptr(bound, _f64p), threads)
+        assert status == 0
         return y, bound
 
     def fill(self, seed, count, amplitude=1.0):

@@ -9,6 +9,8 @@ The path is not bit-exact by design; these tests pin its error, its
 epilogues and its input scaling (tiny, huge and zero token rows).
 """
 
+import os
+
 import numpy as np
 import pytest
 
@@ -17,6 +19,7 @@ from tests.support.oracle_lib import Q4_0, Q4_1, Q6_K, Q8_0
 pytestmark = pytest.mark.gpu
 
 TOLERANCE = 1e-5
+THREADS = max(1, min(16, os.cpu_count() or 1))
 
 
 @pytest.fixture(scope="module")
@@ -26,7 +29,7 @@ def ctx():
 
     c = mm.Context(0)
     c.set_gemm_path(mm.GemmPath.SPLIT_F16_MFMA)
-    ws = hx.Buffer(mm.workspace_bytes(1024, 8192))
+    ws = hx.Buffer(mm.workspace_bytes(2048, 8192))
     c.set_workspace(ws.ptr, ws.nbytes)
     yield c
     c.close()
@@ -133,8 +136,9 @@ def test_mfma_epilogues(oracle, run):
         w.free()
 
 
-def test_mfma_c4_shape_sampled(oracle, run):
-    """C4, 512 x 8192 x 2048, sampled token rows."""
+def test_mfma_c4_shape_in_full(oracle, run):
+    """C4, 512 x 8192 x 2048: every token row within the bar of the reference
+    order (itself within gamma(2K) of f64), and 64 sampled rows against f64."""
     from charlotte_amd import synthetic
 
     rows, columns, tokens = 8192, 2048, 512
@@ -143,11 +147,57 @@ def test_mfma_c4_shape_sampled(oracle, run):
     x = synthetic.activations(rng, tokens, columns)
     w = run.weight(Q4_0, rows, columns, stored)
     got = run.write(w, x, tokens)
-    sample = np.random.default_rng(1).choice(tokens, 32, replace=False)
-    y64, _ = oracle.matmul_f64(Q4_0, stored, rows, columns, x[sample])
-    canonical = oracle.matmul_f32(Q4_0, stored, rows, columns, x[sample], threads=8)
-    _within(got[sample], y64, canonical, "C4 sampled")
+    canonical = oracle.matmul_f32(Q4_0, stored, rows, columns, x, threads=THREADS)
+    _within(got, canonical.astype(np.float64), canonical, "C4 against the reference order")
+    sample = np.sort(np.random.default_rng(1).choice(tokens, 64, replace=False))
+    y64, _ = oracle.matmul_f64(Q4_0, stored, rows, columns, x[sample], threads=THREADS)
+    _within(got[sample], y64, canonical[sample], "C4 sampled against f64")
     w.free()
+
+
+def test_mfma_c5_layer_products_at_2048_tokens(oracle, run):
+    """One Llama 3.2 1B layer at C5's 2,048 tokens on the matrix cores: QKV,
+    o, gated gate/up (SiLU) and down, 64 sampled token rows over every output
+    row against f64."""
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+
+    rng = np.random.default_rng(0xC5)
+    tokens, hidden, ffn = 2048, 2048, 8192
+    sample = np.sort(np.random.default_rng(51).choice(tokens, 64, replace=False))
+
+    def weight(rows, columns):
+        stored = synthetic.q4_0(rng, rows, columns)
+        return stored, run.weight(Q4_0, rows, columns, stored)
+
+    def check(got, stored, rows, columns, xin, what):
+        y64, _ = oracle.matmul_f64(Q4_0, stored, rows, columns, xin[sample], threads=THREADS)
+        canonical = oracle.matmul_f32(Q4_0, stored, rows, columns, xin[sample], threads=THREADS)
+        _within(got[sample], y64, canonical, what)
+        return y64, canonical
+
+    x = synthetic.activations(rng, tokens, hidden)
+    qkv = [weight(r, hidden) for r in (2048, 512, 512)]
+    got = run.product([mm.Member(w) for _, w in qkv], x, tokens, [2048, 512, 512], epilogue=mm.Epilogue.QKV)
+    for i, ((stored, w), g, r) in enumerate(zip(qkv, got, (2048, 512, 512))):
+        check(g, stored, r, hidden, x, f"QKV member {i}")
+        w.free()
+    o_stored, o = weight(hidden, hidden)
+    check(run.write(o, x, tokens), o_stored, hidden, hidden, x, "o")
+    o.free()
+    (g_stored, gate), (u_stored, up) = weight(ffn, hidden), weight(ffn, hidden)
+    got = run.product([mm.Member(gate), mm.Member(up)], x, tokens, [ffn], epilogue=mm.Epilogue.GatedActivation,
+                      activation=mm.Activation.SiLU)[0]
+    g64, _ = oracle.matmul_f64(Q4_0, g_stored, ffn, hidden, x[sample], threads=THREADS)
+    u64, _ = oracle.matmul_f64(Q4_0, u_stored, ffn, hidden, x[sample], threads=THREADS)
+    want = oracle.gated(g64.astype(np.float32), u64.astype(np.float32), activation=0)
+    _within(got[sample], want.astype(np.float64), want, "gated gate/up")
+    gate.free()
+    up.free()
+    xd = synthetic.activations(rng, tokens, ffn)
+    d_stored, down = weight(hidden, ffn)
+    check(run.write(down, xd, tokens), d_stored, hidden, ffn, xd, "down")
+    down.free()
 
 
 def test_mfma_needs_a_workspace(run):

@@ -12,6 +12,8 @@ Inputs are the reference tests' fill (fill.h:24-29, seed 7, amplitude 1) or
 seeded N(0,1).
 """
 
+import os
+
 import numpy as np
 import pytest
 
@@ -22,6 +24,7 @@ pytestmark = pytest.mark.gpu
 
 TOKENS = 64
 WIDEST = 3072
+THREADS = max(1, min(16, os.cpu_count() or 1))
 
 
 @pytest.fixture(scope="module")
@@ -236,6 +239,8 @@ def test_c2_q6_k_lm_head_262144x1152(oracle, run):
 
 
 def test_c4_q4_0_prefill_512x8192x2048(oracle, run):
+    """C4 in full: every output the oracle's bits; f64 and the argmax on 64
+    sampled token rows over every output row."""
     from charlotte_amd import synthetic
     from tests.support.gpu import bits_equal, first_difference
 
@@ -245,18 +250,67 @@ def test_c4_q4_0_prefill_512x8192x2048(oracle, run):
     x = synthetic.activations(rng, tokens, columns)
     w = run.weight(Q4_0, rows, columns, stored)
     got = run.write(w, x, tokens)
-    row_bytes = columns // 32 * 18
-    for r0 in (0, 4000, rows - 128):
-        part = stored[r0 * row_bytes : (r0 + 128) * row_bytes]
-        want = oracle.matmul_f32(Q4_0, part, 128, columns, x, threads=16)
-        assert bits_equal(got[:, r0 : r0 + 128], want), first_difference(got[:, r0 : r0 + 128], want)
-        y64, _ = oracle.matmul_f64(Q4_0, part, 128, columns, x[:64])
-        _tolerance_and_argmax(got[:64, r0 : r0 + 128], y64)
+    want = oracle.matmul_f32(Q4_0, stored, rows, columns, x, threads=THREADS)
+    assert bits_equal(got, want), first_difference(got, want)
+    sample = np.sort(np.random.default_rng(40).choice(tokens, 64, replace=False))
+    y64, _ = oracle.matmul_f64(Q4_0, stored, rows, columns, x[sample], threads=THREADS)
+    _tolerance_and_argmax(got[sample], y64)
     # decode-vs-prefill: the same bits for the same token
     for t_ in (0, 255, 511):
         alone = run.write(w, x[t_ : t_ + 1], 1)
         assert bits_equal(alone[0], got[t_])
     w.free()
+
+
+def test_c5_layer_products_at_2048_tokens(oracle, run):
+    """One Llama 3.2 1B layer at C5's step of 2,048 tokens: QKV (three members,
+    2048 + 512 + 512 rows), o (2048 x 2048), gate/up (gated, SiLU, 8192 rows
+    each) and down (2048 x 8192), each the oracle's bits on 64 sampled token
+    rows over every output row; and the Q6_K head (128,256 x 2,048) on the
+    step's last token, in full."""
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+    from tests.support.gpu import bits_equal, first_difference
+
+    rng = np.random.default_rng(5)
+    tokens, hidden, ffn = 2048, 2048, 8192
+    sample = np.sort(np.random.default_rng(50).choice(tokens, 64, replace=False))
+
+    def weight(rows, columns, gtype=Q4_0):
+        stored = synthetic.weight(rng, gtype, rows, columns)
+        return stored, run.weight(gtype, rows, columns, stored)
+
+    x = synthetic.activations(rng, tokens, hidden)
+    qkv = [weight(r, hidden) for r in (2048, 512, 512)]
+    got = run.product([mm.Member(w) for _, w in qkv], x, tokens, [2048, 512, 512], epilogue=mm.Epilogue.QKV)
+    for (stored, w), g, r in zip(qkv, got, (2048, 512, 512)):
+        want = oracle.matmul_f32(Q4_0, stored, r, hidden, x[sample], threads=THREADS)
+        assert bits_equal(g[sample], want), first_difference(g[sample], want)
+        w.free()
+    o_stored, o = weight(hidden, hidden)
+    got = run.write(o, x, tokens)
+    want = oracle.matmul_f32(Q4_0, o_stored, hidden, hidden, x[sample], threads=THREADS)
+    assert bits_equal(got[sample], want), first_difference(got[sample], want)
+    o.free()
+    (g_stored, gate), (u_stored, up) = weight(ffn, hidden), weight(ffn, hidden)
+    got = run.product([mm.Member(gate), mm.Member(up)], x, tokens, [ffn], epilogue=mm.Epilogue.GatedActivation,
+                      activation=mm.Activation.SiLU)[0]
+    want = oracle.gated(oracle.matmul_f32(Q4_0, g_stored, ffn, hidden, x[sample], threads=THREADS),
+                        oracle.matmul_f32(Q4_0, u_stored, ffn, hidden, x[sample], threads=THREADS), activation=0)
+    assert bits_equal(got[sample], want), first_difference(got[sample], want)
+    gate.free()
+    up.free()
+    xd = synthetic.activations(rng, tokens, ffn)
+    d_stored, down = weight(hidden, ffn)
+    got = run.write(down, xd, tokens)
+    want = oracle.matmul_f32(Q4_0, d_stored, hidden, ffn, xd[sample], threads=THREADS)
+    assert bits_equal(got[sample], want), first_difference(got[sample], want)
+    down.free()
+    h_stored, head = weight(128256, hidden, Q6_K)
+    got = run.write(head, x, tokens, rows=mm.Rows.LastToken)
+    want = oracle.matmul_f32(Q6_K, h_stored, 128256, hidden, x[tokens - 1 :], threads=THREADS)
+    assert bits_equal(got, want), first_difference(got, want)
+    head.free()
 
 
 # ---- errors the host turns away --------------------------------------------

@@ -266,7 +266,7 @@ def test_f32_threads_do_not_change_bits(oracle, fixture_tensors):
 
 
 def test_f64_oracle_is_a_plain_dot_product(oracle, fixture_tensors):
-    t = fixture_tensors["w_q4_1_1152"] if False else fixture_tensors["w_q4_0"]
+    t = fixture_tensors["w_q4_0"]
     x = oracle.fill(7, 2 * t.columns)
     y, bound = oracle.matmul_f64(t.type, t.data, t.rows, t.columns, x)
     w = oracle.dequantize(t.type, t.data).reshape(t.rows, t.columns).astype(np.float64)
@@ -275,6 +275,15 @@ def test_f64_oracle_is_a_plain_dot_product(oracle, fixture_tensors):
     u = 2.0**-24
     gamma = 2 * t.columns * u / (1 - 2 * t.columns * u)
     assert np.allclose(bound, gamma * (np.abs(x.reshape(2, -1)).astype(np.float64) @ np.abs(w).T), rtol=1e-12)
+
+
+@pytest.mark.parametrize("threads", [2, 3, 8])
+def test_f64_threads_split_rows_without_changing_a_value(oracle, fixture_tensors, threads):
+    t = fixture_tensors["w_q6_k"]
+    x = oracle.fill(11, 3 * t.columns)
+    one, b1 = oracle.matmul_f64(t.type, t.data, t.rows, t.columns, x)
+    many, bm = oracle.matmul_f64(t.type, t.data, t.rows, t.columns, x, threads=threads)
+    assert (one.view(np.uint64) == many.view(np.uint64)).all() and (b1.view(np.uint64) == bm.view(np.uint64)).all()
 
 
 @pytest.mark.parametrize("name", ["w_q4_0", "w_q6_k", "w_set2", "qkv_q", "ffn_gate"])
