@@ -351,28 +351,16 @@ __device__ __forceinline__ void group_product(float4_t (&tot)[R][T], const half8
 // bytes a chunk) and written into the other at the batch's end. Each wave's
 // codes for the next batch are loaded into registers alongside. So every
 // load has a whole batch of products to arrive in, and a workgroup meets at
-// one barrier a batch. 16-byte chunk k of token t sits at chunk k ^ (t & 7),
-// spreading the 16 tokens a read takes over the banks.
-#ifndef CHM_MFMA_SWIZZLE
-#define CHM_MFMA_SWIZZLE 1
-#endif
-#ifndef CHM_MFMA_PREFETCH_A
-#define CHM_MFMA_PREFETCH_A 0
-#endif
-#ifndef CHM_MFMA_W_AHEAD
-#define CHM_MFMA_W_AHEAD 1
-#endif
-#ifndef CHM_MFMA_WAVES_A_SIMD
-#define CHM_MFMA_WAVES_A_SIMD 2
-#endif
+// one barrier a batch. 16-byte chunk k of token t sits at a swizzled chunk
+// (below), spreading the 16 tokens a read takes over the banks. (Codes two
+// batches ahead, or the A operand read a group ahead, measured no better.)
+constexpr uint32_t kMfmaWavesASimd = 2;
 
 // The chunk a token's 16-byte chunk k sits at. With 64 banks (256 bytes a
 // bank row), tokens t and t ^ 1 share a row, and t and t + 8 would collide
 // under k ^ (t & 7); k ^ ((t >> 1) & 7) spreads the 16 tokens of a read over
 // all 16 chunk positions of a bank row.
-__device__ __forceinline__ uint32_t swizzle(uint32_t t, uint32_t k) {
-    return CHM_MFMA_SWIZZLE ? k ^ ((t >> 1) & 7u) : k ^ (t & 7u);
-}
+__device__ __forceinline__ uint32_t swizzle(uint32_t t, uint32_t k) { return k ^ ((t >> 1) & 7u); }
 
 template <uint32_t F, int R, int T, bool FULL>
 __global__ __launch_bounds__(256, 2) void gemm_mfma(Product a, const uint8_t* __restrict__ xp,
@@ -432,19 +420,18 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma(Product a, const uint8_t* __
     // Batch b: its input in LDS buffer b & 1, its codes in `wc`; the next
     // batch's loads go to `xr` and `wn`.
     u32x4_t xr[kBatch][XC];
-    // The codes go CHM_MFMA_W_AHEAD batches ahead (they come from HBM; the
-    // input, from L2): three buffers in turn.
-    Batch<F, R> w0, w1, w2;
+    // The codes go a batch ahead (they come from HBM; the input, from L2):
+    // two buffers in turn.
+    Batch<F, R> w0, w1;
     auto batch = [&](uint32_t b, const Batch<F, R>& wcur, Batch<F, R>& wahead) {
         __syncthreads();  // buffer b & 1 is written; buffer (b + 1) & 1 is read no more
         const bool more = b + 1 < batches;
         if (more) load_x(b + 1, xr);
-        if (b + CHM_MFMA_W_AHEAD < batches) wahead.load(rows, b + CHM_MFMA_W_AHEAD, G, q, aligned);
+        if (b + 1 < batches) wahead.load(rows, b + 1, G, q, aligned);
         Codes<F> wc[kBatch][R];
         wcur.codes(wc);
         const u32x4_t* buf = xs[b & 1u][0];
-        // A operands of group j of the batch; with CHM_MFMA_PREFETCH_A, group
-        // j + 1's are read before group j's products.
+        // A operands of group j of the batch, two buffers in turn.
         half8_t ah[2][T], al[2][T];
         auto read = [&](int j, half8_t (&xh)[T], half8_t (&xl)[T]) {
 #pragma unroll
@@ -454,33 +441,19 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma(Product a, const uint8_t* __
                 xl[t] = __builtin_bit_cast(half8_t, buf[j * BM * 8 + tok * 8 + swizzle(tok, 2 * q + 1)]);
             }
         };
-        if (CHM_MFMA_PREFETCH_A) read(0, ah[0], al[0]);
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
-            if (CHM_MFMA_PREFETCH_A) {
-                if (j + 1 < kBatch) read(j + 1, ah[(j + 1) & 1], al[(j + 1) & 1]);
-            } else {
-                read(j, ah[j & 1], al[j & 1]);
-            }
+            read(j, ah[j & 1], al[j & 1]);
             if (b * kBatch + j < G) group_product<F, R, T>(tot, ah[j & 1], al[j & 1], wc[j], q);
         }
         if (more) store((b + 1) & 1u, xr);
     };
     load_x(0, xr);
     w0.load(rows, 0, G, q, aligned);
-    if (CHM_MFMA_W_AHEAD == 2) w1.load(rows, 1 < batches ? 1 : 0, G, q, aligned);
     store(0, xr);
-    if constexpr (CHM_MFMA_W_AHEAD == 2) {
-        for (uint32_t b = 0; b < batches; b += 3) {
-            batch(b, w0, w2);
-            if (b + 1 < batches) batch(b + 1, w1, w0);
-            if (b + 2 < batches) batch(b + 2, w2, w1);
-        }
-    } else {
-        for (uint32_t b = 0; b < batches; b += 2) {
-            batch(b, w0, w1);
-            if (b + 1 < batches) batch(b + 1, w1, w0);
-        }
+    for (uint32_t b = 0; b < batches; b += 2) {
+        batch(b, w0, w1);
+        if (b + 1 < batches) batch(b + 1, w1, w0);
     }
 
     // Lane (c, q) holds tokens 4q .. 4q+3 of each token block for row c of
@@ -524,7 +497,7 @@ static void launch_format(const Product& a, const uint8_t* xp, const float* inv,
     const auto waves = [&](int r, int t) {
         return uint64_t{(a.tokens + 16u * t - 1) / (16u * t)} * ((a.rows + 16u * r - 1) / (16u * r));
     };
-    const uint64_t want = uint64_t{compute_units} * 4 * CHM_MFMA_WAVES_A_SIMD;
+    const uint64_t want = uint64_t{compute_units} * 4 * kMfmaWavesASimd;
     if constexpr (F == kQ4_0) {
         if (waves(4, 4) >= want) return go<F, 4, 4>(a, xp, inv, stream);
     }

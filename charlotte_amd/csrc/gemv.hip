@@ -31,12 +31,8 @@ hipError_t launch_gemv_stream(const Product& a, uint32_t compute_units, bool lim
 // Workgroups a CU is asked to hold at once, as launch bounds: the L = 32
 // kernel's registers allow 4 waves a SIMD at SPAN <= 2 as it stands; the L = 4
 // Q6_K kernel holds a 9-group run (65 registers) and spills past 128.
-#ifndef CHM_RANGES_MIN_BLOCKS
-#define CHM_RANGES_MIN_BLOCKS 2
-#endif
-#ifndef CHM_QUARTERS_MIN_BLOCKS
-#define CHM_QUARTERS_MIN_BLOCKS 3
-#endif
+constexpr int kRangesMinBlocks = 2;
+constexpr int kQuartersMinBlocks = 3;
 
 constexpr int kWaves = 4;     // waves a workgroup
 constexpr int kPad = 33;      // a row's 32 range sums, padded
@@ -74,7 +70,7 @@ __device__ __forceinline__ void finish_rows(const Product& a, uint32_t first, ui
 constexpr int batch_of(int span) { return span >= 3 ? 2 : span == 2 ? 4 : 8; }
 
 template <uint32_t F, int SPAN, bool XREG, bool FULL, int B>
-__global__ __launch_bounds__(256, CHM_RANGES_MIN_BLOCKS) void gemv_ranges(Product a, uint32_t steps, uint32_t tiles) {
+__global__ __launch_bounds__(256, kRangesMinBlocks) void gemv_ranges(Product a, uint32_t steps, uint32_t tiles) {
     __shared__ float partials[kWaves][kWaveRows * kPad];
     extern __shared__ float4 xs4[];  // x, staged when it is not held in registers
 
@@ -328,14 +324,11 @@ __device__ __forceinline__ uint32_t x_slot(uint32_t v) {
 
 // L = 4: lane j of a row owns ranges 8j .. 8j + 7, exactly G / 4 = SPAN
 // groups (G = 4 SPAN, G >= 32, so no range is empty). Its run's bytes are
-// contiguous. With CHM_QUARTERS_PIPELINE, a wave loads its next step's runs
-// while it decodes the current one (two run buffers, used in turn).
-#ifndef CHM_QUARTERS_PIPELINE
-#define CHM_QUARTERS_PIPELINE 0
-#endif
+// contiguous. (Loading the next step's runs during the current decode, two
+// run buffers in turn, measured slower.)
 
 template <uint32_t F, int SPAN, bool FULL>
-__global__ __launch_bounds__(256, CHM_QUARTERS_MIN_BLOCKS) void gemv_quarters(Product a, uint32_t steps, uint32_t tiles) {
+__global__ __launch_bounds__(256, kQuartersMinBlocks) void gemv_quarters(Product a, uint32_t steps, uint32_t tiles) {
     __shared__ float partials[kWaves][kWaveRows * kPad];
     extern __shared__ float4 xs4[];
 
@@ -430,21 +423,9 @@ __global__ __launch_bounds__(256, CHM_QUARTERS_MIN_BLOCKS) void gemv_quarters(Pr
             wave_sync();
         }
     };
-    if constexpr (CHM_QUARTERS_PIPELINE) {
-        Run<F, SPAN>& even = first;
-        Run<F, SPAN> odd;
-        for (uint32_t n = 0; n < total_steps; n += 2) {
-            load(odd, n + 1);
-            decode(even, n);
-            if (n + 1 >= total_steps) break;
-            load(even, n + 2);
-            decode(odd, n + 1);
-        }
-    } else {
-        for (uint32_t n = 0; n < total_steps; ++n) {
-            if (n > 0) load(first, n);
-            decode(first, n);
-        }
+    for (uint32_t n = 0; n < total_steps; ++n) {
+        if (n > 0) load(first, n);
+        decode(first, n);
     }
 }
 
