@@ -27,6 +27,8 @@ namespace chm {
 
 bool gemv_stream_takes(const Product& a, uint32_t format);
 hipError_t launch_gemv_stream(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream);
+bool gemv_stream8_takes(const Product& a, uint32_t format);
+hipError_t launch_gemv_stream8(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream);
 
 // Workgroups a CU is asked to hold at once, as launch bounds: the L = 32
 // kernel's registers allow 4 waves a SIMD at SPAN <= 2 as it stands; the L = 4
@@ -528,12 +530,15 @@ static hipError_t launch_format(const Product& a, const GemvPlan& plan, uint32_t
     return hipGetLastError();
 }
 
-bool gemv_limbs_takes(const Product& a, uint32_t format) { return gemv_stream_takes(a, format); }
+bool gemv_limbs_takes(const Product& a, uint32_t format) {
+    return gemv_stream_takes(a, format) || gemv_stream8_takes(a, format);
+}
 
-// `limbs`: the INT8_LIMBS path where it is built (the streamed kernel's
+// `limbs`: the INT8_LIMBS path where it is built (the streamed kernels'
 // shapes); every other shape decodes in the canonical order.
 hipError_t launch_gemv(const Product& a, uint32_t format, uint32_t compute_units, bool limbs, hipStream_t stream) {
     if (gemv_stream_takes(a, format)) return launch_gemv_stream(a, compute_units, limbs, stream);
+    if (gemv_stream8_takes(a, format)) return launch_gemv_stream8(a, compute_units, limbs, stream);
     GemvPlan plan;
     if (!gemv_plan(a.rows, a.groups, compute_units, &plan)) return hipErrorInvalidValue;
     switch (format) {
