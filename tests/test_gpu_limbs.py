@@ -5,7 +5,8 @@ reference-order f32 product's wherever its top two differ by more than the
 error allows (BASELINE's bar, as the matrix-core prefill's tests hold it).
 
 The path is not bit-exact by design. These tests pin its error at the shapes
-it is built for (Q6_K, K = 1,152, rows in 16s), over inputs of every scale,
+it is built for (Q6_K, K = 1,152 and 1,024 with rows in 16s, 2,048 with rows
+in 8s), over inputs of every scale,
 with outliers, zeros and non-finite values, through each epilogue it takes;
 and that every other decode still runs in the canonical order, bit for bit.
 """
@@ -172,7 +173,8 @@ def test_limbs_epilogues(oracle, run):
         w.free()
 
 
-@pytest.mark.parametrize("gtype,rows,columns", [(Q6_K, 100, K), (Q6_K, 64, 2048), (Q4_0, 3072, 1024)])
+@pytest.mark.parametrize("gtype,rows,columns",
+                         [(Q6_K, 100, K), (Q6_K, 100, 1024), (Q6_K, 60, 2048), (Q6_K, 64, 3072), (Q4_0, 3072, 1024)])
 def test_other_decodes_stay_canonical(oracle, run, gtype, rows, columns):
     """Shapes the path is not built for decode in the canonical order: the
     oracle's bits, whatever the setting."""
