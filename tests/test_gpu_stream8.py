@@ -131,3 +131,36 @@ def test_stream8_limbs_within_tolerance(oracle, limbs_run, rows, columns):
     if a != b:
         s = np.sort(y64[0])
         assert s[-1] - s[-2] <= 2 * err
+
+
+@pytest.mark.parametrize("columns", [1024, 2048])
+def test_stream8_limbs_members_epilogues_and_the_head(oracle, limbs_run, columns):
+    """The INT8_LIMBS form through QKV members, Write with clip, bias and
+    activation, and the head's last token: within the bar of the f64 totals
+    the epilogue is applied to."""
+    from charlotte_amd import matmul as mm
+
+    def within(got, want64, what):
+        err = np.abs(got.astype(np.float64) - want64).max()
+        top = np.abs(want64).max()
+        assert np.isfinite(got).all() and err <= 1e-5 * top, f"{what}: {err:.3e} vs {top:.3e}"
+
+    widths = [256, 64, 64]
+    data = [_data(r, columns, seed=90 + i + columns) for i, r in enumerate(widths)]
+    x = data[0][1]
+    ws = [limbs_run.weight(Q6_K, r, columns, d[0]) for r, d in zip(widths, data)]
+    got = limbs_run.product([mm.Member(w) for w in ws], x, 1, widths, epilogue=mm.Epilogue.QKV)
+    for i, (r, d) in enumerate(zip(widths, data)):
+        within(got[i], oracle.matmul_f64(Q6_K, d[0], r, columns, x)[0], f"member {i}")
+    clip = np.array([-1.0, 1.5, -3.0, 2.5], np.float32)
+    bias = np.linspace(-0.5, 0.5, 256, dtype=np.float32)
+    t64, _ = oracle.matmul_f64(Q6_K, data[0][0], 256, columns, oracle.clamp(x, clip[0], clip[1]))
+    got = limbs_run.product([mm.Member(ws[0])], x, 1, [256], clip=clip, bias=bias, activated=True,
+                            activation=mm.Activation.SiLU)[0]
+    want = oracle.finish(t64.astype(np.float32), clip=clip, bias=bias, activated=True, activation=0)
+    within(got, want.astype(np.float64), "Write with options")
+    xs = np.concatenate([np.random.default_rng(9).standard_normal((2, columns), dtype=np.float32), x])
+    got = limbs_run.write(ws[0], xs, 3, rows=mm.Rows.LastToken)
+    within(got, oracle.matmul_f64(Q6_K, data[0][0], 256, columns, x)[0], "last token")
+    for w in ws:
+        w.free()
