@@ -30,8 +30,8 @@
 // moves. Not the canonical bits: within 1e-5 of them.
 #include <algorithm>
 
-#include "limbs.hpp"
 #include "product.hpp"
+#include "stream.hpp"
 
 namespace chm {
 
@@ -41,23 +41,6 @@ constexpr uint32_t kStepGroups = kStepRows * 36;  // 576
 // A step's 16-byte chunks a stream: lo 576, hi 288, scales 72, d 9 (144
 // bytes: 72 super-blocks).
 constexpr uint32_t kLoChunks = kStepGroups, kHiChunks = kStepGroups / 2, kScChunks = kStepGroups / 8, kDChunks = 9;
-
-typedef __attribute__((address_space(3))) void* lds_void;
-
-// vmcnt(0) alone, in s_waitcnt's gfx9 encoding (the other counters at
-// their no-wait values).
-constexpr int kVmcnt0 = (0x7 << 4) | (0xF << 8);
-
-// Copies `chunks` 16-byte chunks from `from` to LDS `to`, 64 a wave
-// instruction (lanes past the last chunk copy nothing).
-template <uint32_t kChunks>
-__device__ __forceinline__ void copy_stream(const uint8_t* from, u32x4s_t* to, uint32_t lane) {
-#pragma unroll
-    for (uint32_t i = 0; i < (kChunks + 63) / 64; ++i) {
-        if (64 * i + 64 <= kChunks || 64 * i + lane < kChunks)
-            __builtin_amdgcn_global_load_lds(from + 16 * (64 * i + lane), (lds_void)(to + 64 * i), 16, 0, 0);
-    }
-}
 
 // A lane's share of a step, as held in registers between the stage and the
 // decode: its nine groups' lo and hi, their scale pairs, the two d's.

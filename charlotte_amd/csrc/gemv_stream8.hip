@@ -20,8 +20,8 @@
 // the row's L sums added pairwise.
 #include <algorithm>
 
-#include "limbs.hpp"
 #include "product.hpp"
+#include "stream.hpp"
 
 namespace chm {
 
@@ -30,19 +30,6 @@ namespace {
 constexpr int kWaves8 = 4;
 constexpr uint32_t kLo8 = 512, kHi8 = 256, kSc8 = 64, kD8 = 8;  // 16-byte chunks a stream a step
 constexpr uint32_t kSlice8 = 65;  // x slice stride, float4 or u32x4 (8 groups of 8, one of padding)
-
-typedef __attribute__((address_space(3))) void* lds_void8;
-
-constexpr int kVmcnt0x = (0x7 << 4) | (0xF << 8);  // s_waitcnt vmcnt(0) alone
-
-template <uint32_t kChunks>
-__device__ __forceinline__ void copy_stream8(const uint8_t* from, u32x4s_t* to, uint32_t lane) {
-#pragma unroll
-    for (uint32_t i = 0; i < (kChunks + 63) / 64; ++i) {
-        if (64 * i + 64 <= kChunks || 64 * i + lane < kChunks)
-            __builtin_amdgcn_global_load_lds(from + 16 * (64 * i + lane), (lds_void8)(to + 64 * i), 16, 0, 0);
-    }
-}
 
 // A lane's share of a step: its 8 groups' lo and hi, their scale pairs, d.
 struct StepRun8 {
@@ -79,10 +66,10 @@ __global__ __launch_bounds__(256, 2) void gemv_stream8(Product a, uint32_t steps
     auto issue = [&](uint32_t step) {
         const Piece w = piece_of(a, step * kRows);
         const uint64_t n = w.blocks, g0 = static_cast<uint64_t>(w.row) * G;  // the step's first group
-        copy_stream8<kLo8>(w.piece + 16 * g0, lo_s, lane);
-        copy_stream8<kHi8>(w.piece + 128 * n + 8 * g0, hi_s, lane);
-        copy_stream8<kSc8>(w.piece + 192 * n + 2 * g0, sc_s, lane);
-        copy_stream8<kD8>(w.piece + 208 * n + 2 * (g0 / 8), d_s, lane);
+        copy_stream<kLo8>(w.piece + 16 * g0, lo_s, lane);
+        copy_stream<kHi8>(w.piece + 128 * n + 8 * g0, hi_s, lane);
+        copy_stream<kSc8>(w.piece + 192 * n + 2 * g0, sc_s, lane);
+        copy_stream<kD8>(w.piece + 208 * n + 2 * (g0 / 8), d_s, lane);
     };
     const uint32_t lg = G * rho + 8 * j;  // the lane's first group within a step (a super-block's first)
     // The stage's reads are instructions the compiler does not look into (it
@@ -243,7 +230,7 @@ __global__ __launch_bounds__(256, 2) void gemv_stream8(Product a, uint32_t steps
     }
     if (step >= steps) return;
     while (true) {
-        __builtin_amdgcn_s_waitcnt(kVmcnt0x);
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
         __asm__ __volatile__("" ::: "memory");
         StepRun8 run;
         take(run);
