@@ -40,8 +40,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
-FP32_PEAK_TFLOPS = 157.3   # MI355X FP32 (vector and matrix); the vector figure counts packed FP32
-FP32_NONPACKED_TFLOPS = 78.6  # FP32 FMA without packed instructions, which this build does not issue
+FP32_PEAK_TFLOPS = 157.3   # MI355X FP32 (vector and matrix)
 F16_PEAK_TFLOPS = 2516.6   # MI355X FP16 dense matrix
 MALL_BYTES = 256 << 20
 METRIC = "GEMV HBM GB/s (% of 8 TB/s); prefill GEMM TFLOP/s (% peak); host-CPU baseline"
@@ -285,7 +284,7 @@ def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=No
     log(f"{name}: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s ({100 * tflops / FP32_PEAK_TFLOPS:.1f}% of FP32 peak, "
         f"{100 * tflops / F16_PEAK_TFLOPS:.1f}% of dense FP16 matrix peak)")
     return {"ms_per_step": ms, "flops": flops, "TFLOP/s": tflops, "path": path.name,
-            "frac_fp32": tflops / FP32_PEAK_TFLOPS, "frac_fp32_nonpacked": tflops / FP32_NONPACKED_TFLOPS,
+            "frac_fp32": tflops / FP32_PEAK_TFLOPS,
             "frac_f16_matrix": tflops / F16_PEAK_TFLOPS,
             "tokens_per_s": tokens / (ms * 1e-3), "launches": len(launches), "head_gemv_bytes": head_bytes}
 
