@@ -66,9 +66,8 @@ __device__ __forceinline__ void finish_rows(const Product& a, uint32_t first, ui
 // L = 32: lane r of a half-wave owns range r — at most SPAN groups, its
 // chain from zero over them, and no other range; its range sum goes to LDS.
 // Rows a batch: B steps' loads are issued before any is decoded, so a wave
-// keeps B rows' bytes in flight rather than one. A product of one step a
-// wave (fewer than 8,192 rows) takes batches of one: loading rows it will not
-// use would only hold the wave.
+// keeps B rows' bytes in flight rather than one; B never exceeds a wave's
+// steps, so every row loaded is decoded.
 constexpr int batch_of(int span) { return span >= 3 ? 2 : span == 2 ? 4 : 8; }
 
 template <uint32_t F, int SPAN, bool XREG, bool FULL, int B>
@@ -452,10 +451,24 @@ bool gemv_plan(uint32_t rows, uint32_t groups, uint32_t compute_units, GemvPlan*
     }
     const uint32_t rows_a_step = 64 / plan->lanes;
     const uint32_t max_steps = kWaveRows / rows_a_step;
-    // Steps a wave: the most, up to max_steps, that still gives every CU
-    // about 8 waves.
-    const uint32_t steps = rows / (rows_a_step * compute_units * 8);
-    plan->steps = steps < 1 ? 1 : steps > max_steps ? max_steps : steps;
+    if (plan->lanes == 4) {
+        // Steps a wave: the most, up to max_steps, that still gives every CU
+        // about 8 waves.
+        const uint32_t steps = rows / (rows_a_step * compute_units * 8);
+        plan->steps = steps < 1 ? 1 : steps > max_steps ? max_steps : steps;
+        return true;
+    }
+    // L = 32: a power of two of steps a wave, the fewest that bring the grid
+    // down to one workgroup a CU — two for products of 2^20 groups or more.
+    // A small product is bound by its workgroups' dispatch and one memory
+    // round trip, so fewer workgroups with more rows each finish sooner
+    // (Q4_0 3,072 x 1,024: 384 workgroups 5.0 us, 192 4.3 us, 96 4.8 us);
+    // a large one needs the second workgroup's loads in flight.
+    const uint64_t per_cu = static_cast<uint64_t>(rows) * groups >= (1u << 20) ? 2 : 1;
+    const uint64_t target = per_cu * compute_units * kWaves * rows_a_step;
+    uint32_t steps = 1;
+    while (steps < max_steps && steps * target < rows) steps *= 2;
+    plan->steps = steps;
     return true;
 }
 
@@ -490,10 +503,18 @@ static void go_epilogue(const Product& a, uint32_t steps, uint32_t compute_units
     const uint32_t tiles = (a.rows + rows_a_tile - 1) / rows_a_tile;
     const size_t lds = XREG ? 0 : (static_cast<size_t>(a.groups) * 32 + (L == 4 ? 16 : 0)) * sizeof(float);
     if constexpr (L == 32) {
+        // Steps are a power of two: a batch is never more than a wave's steps,
+        // so no load is issued for a row the wave does not decode.
+        constexpr int most = batch_of(SPAN);
         if (steps == 1) {
             launch_ranges<F, SPAN, XREG, FULL, 1>(a, steps, tiles, lds, compute_units, stream);
-        } else {
-            launch_ranges<F, SPAN, XREG, FULL, batch_of(SPAN)>(a, steps, tiles, lds, compute_units, stream);
+        } else if (steps == 2 || most == 2) {
+            launch_ranges<F, SPAN, XREG, FULL, 2>(a, steps, tiles, lds, compute_units, stream);
+        } else if constexpr (most >= 4) {
+            if (steps == 4 || most == 4)
+                launch_ranges<F, SPAN, XREG, FULL, 4>(a, steps, tiles, lds, compute_units, stream);
+            else
+                launch_ranges<F, SPAN, XREG, FULL, most>(a, steps, tiles, lds, compute_units, stream);
         }
     } else {
         thread_local size_t cached_lds = ~size_t{0};
