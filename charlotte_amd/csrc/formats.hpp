@@ -62,35 +62,63 @@ struct Q6_KGroup {
     float first, minus_32_first, second, minus_32_second;
 };
 
-__device__ __forceinline__ Q4_0Group load_q4_0(const uint8_t* piece, uint64_t n, uint64_t gi) {
+// A group's bytes as loaded, before any arithmetic on them (fetch_*), and
+// the group they make (group_of): a kernel may load a group well before it
+// uses it without waiting on the loads at once.
+struct Q4_0Bytes {
+    uint4 c;
+    uint32_t d;
+};
+
+__device__ __forceinline__ Q4_0Bytes fetch_q4_0(const uint8_t* piece, uint64_t n, uint64_t gi) {
+    return {*reinterpret_cast<const uint4*>(piece + 16 * gi), *reinterpret_cast<const uint16_t*>(piece + 16 * n + 2 * gi)};
+}
+
+__device__ __forceinline__ Q4_0Group group_of(const Q4_0Bytes& b) {
     Q4_0Group g;
-    const uint4 c = *reinterpret_cast<const uint4*>(piece + 16 * gi);
-    g.w[0] = c.x;
-    g.w[1] = c.y;
-    g.w[2] = c.z;
-    g.w[3] = c.w;
-    g.d = half_to_float(*reinterpret_cast<const uint16_t*>(piece + 16 * n + 2 * gi));
+    g.w[0] = b.c.x;
+    g.w[1] = b.c.y;
+    g.w[2] = b.c.z;
+    g.w[3] = b.c.w;
+    g.d = half_to_float(b.d);
     g.minus_8d = -8.0f * g.d;
     return g;
 }
 
-__device__ __forceinline__ Q6_KGroup load_q6_k(const uint8_t* piece, uint64_t n, uint64_t gi) {
+__device__ __forceinline__ Q4_0Group load_q4_0(const uint8_t* piece, uint64_t n, uint64_t gi) {
+    return group_of(fetch_q4_0(piece, n, gi));
+}
+
+struct Q6_KBytes {
+    uint4 lo;
+    uint2 hi;
+    uint32_t sc, d;
+};
+
+__device__ __forceinline__ Q6_KBytes fetch_q6_k(const uint8_t* piece, uint64_t n, uint64_t gi) {
+    return {*reinterpret_cast<const uint4*>(piece + 16 * gi), *reinterpret_cast<const uint2*>(piece + 128 * n + 8 * gi),
+            *reinterpret_cast<const uint16_t*>(piece + 192 * n + 2 * gi),
+            *reinterpret_cast<const uint16_t*>(piece + 208 * n + 2 * (gi / 8))};
+}
+
+__device__ __forceinline__ Q6_KGroup group_of(const Q6_KBytes& b) {
     Q6_KGroup g;
-    const uint4 lo = *reinterpret_cast<const uint4*>(piece + 16 * gi);
-    const uint2 hi = *reinterpret_cast<const uint2*>(piece + 128 * n + 8 * gi);
-    const uint32_t sc = *reinterpret_cast<const uint16_t*>(piece + 192 * n + 2 * gi);
-    const float d = half_to_float(*reinterpret_cast<const uint16_t*>(piece + 208 * n + 2 * (gi / 8)));
-    g.lo[0] = lo.x;
-    g.lo[1] = lo.y;
-    g.lo[2] = lo.z;
-    g.lo[3] = lo.w;
-    g.hi[0] = hi.x;
-    g.hi[1] = hi.y;
-    g.first = d * static_cast<float>(static_cast<int8_t>(sc & 0xFFu));
-    g.second = d * static_cast<float>(static_cast<int8_t>(sc >> 8));
+    const float d = half_to_float(b.d);
+    g.lo[0] = b.lo.x;
+    g.lo[1] = b.lo.y;
+    g.lo[2] = b.lo.z;
+    g.lo[3] = b.lo.w;
+    g.hi[0] = b.hi.x;
+    g.hi[1] = b.hi.y;
+    g.first = d * static_cast<float>(static_cast<int8_t>(b.sc & 0xFFu));
+    g.second = d * static_cast<float>(static_cast<int8_t>(b.sc >> 8));
     g.minus_32_first = -32.0f * g.first;
     g.minus_32_second = -32.0f * g.second;
     return g;
+}
+
+__device__ __forceinline__ Q6_KGroup load_q6_k(const uint8_t* piece, uint64_t n, uint64_t gi) {
+    return group_of(fetch_q6_k(piece, n, gi));
 }
 
 struct Q4_1Group {
@@ -103,33 +131,56 @@ struct Q8_0Group {
     float d;
 };
 
-__device__ __forceinline__ Q4_1Group load_q4_1(const uint8_t* piece, uint64_t n, uint64_t gi) {
+struct Q4_1Bytes {
+    uint4 c;
+    uint32_t dm;
+};
+
+__device__ __forceinline__ Q4_1Bytes fetch_q4_1(const uint8_t* piece, uint64_t n, uint64_t gi) {
+    return {*reinterpret_cast<const uint4*>(piece + 16 * gi), *reinterpret_cast<const uint32_t*>(piece + 16 * n + 4 * gi)};
+}
+
+__device__ __forceinline__ Q4_1Group group_of(const Q4_1Bytes& b) {
     Q4_1Group g;
-    const uint4 c = *reinterpret_cast<const uint4*>(piece + 16 * gi);
-    const uint32_t dm = *reinterpret_cast<const uint32_t*>(piece + 16 * n + 4 * gi);
-    g.w[0] = c.x;
-    g.w[1] = c.y;
-    g.w[2] = c.z;
-    g.w[3] = c.w;
-    g.d = half_to_float(dm & 0xFFFFu);
-    g.m = half_to_float(dm >> 16);
+    g.w[0] = b.c.x;
+    g.w[1] = b.c.y;
+    g.w[2] = b.c.z;
+    g.w[3] = b.c.w;
+    g.d = half_to_float(b.dm & 0xFFFFu);
+    g.m = half_to_float(b.dm >> 16);
+    return g;
+}
+
+__device__ __forceinline__ Q4_1Group load_q4_1(const uint8_t* piece, uint64_t n, uint64_t gi) {
+    return group_of(fetch_q4_1(piece, n, gi));
+}
+
+struct Q8_0Bytes {
+    uint4 a, b;
+    uint32_t d;
+};
+
+__device__ __forceinline__ Q8_0Bytes fetch_q8_0(const uint8_t* piece, uint64_t n, uint64_t gi) {
+    const uint4* c = reinterpret_cast<const uint4*>(piece + 32 * gi);
+    return {c[0], c[1], *reinterpret_cast<const uint16_t*>(piece + 32 * n + 2 * gi)};
+}
+
+__device__ __forceinline__ Q8_0Group group_of(const Q8_0Bytes& b) {
+    Q8_0Group g;
+    g.w[0] = b.a.x;
+    g.w[1] = b.a.y;
+    g.w[2] = b.a.z;
+    g.w[3] = b.a.w;
+    g.w[4] = b.b.x;
+    g.w[5] = b.b.y;
+    g.w[6] = b.b.z;
+    g.w[7] = b.b.w;
+    g.d = half_to_float(b.d);
     return g;
 }
 
 __device__ __forceinline__ Q8_0Group load_q8_0(const uint8_t* piece, uint64_t n, uint64_t gi) {
-    Q8_0Group g;
-    const uint4* c = reinterpret_cast<const uint4*>(piece + 32 * gi);
-    const uint4 a = c[0], b = c[1];
-    g.w[0] = a.x;
-    g.w[1] = a.y;
-    g.w[2] = a.z;
-    g.w[3] = a.w;
-    g.w[4] = b.x;
-    g.w[5] = b.y;
-    g.w[6] = b.z;
-    g.w[7] = b.w;
-    g.d = half_to_float(*reinterpret_cast<const uint16_t*>(piece + 32 * n + 2 * gi));
-    return g;
+    return group_of(fetch_q8_0(piece, n, gi));
 }
 
 // Weight l (0..31) of a group, exact.
@@ -206,32 +257,6 @@ __device__ __forceinline__ void unpack(const uint8_t* piece, uint64_t n, uint64_
         const Q6_KGroup g = load_q6_k(piece, n, gi);
 #pragma unroll
         for (int l = 0; l < 32; ++l) out[l] = weight(g, l);
-    }
-}
-
-// Weights 16 h .. 16 h + 15 (h = 0, 1) of group gi, exact: what one of a
-// group's two staging lanes decodes in the prefill tile.
-template <uint32_t F>
-__device__ __forceinline__ void unpack_half(const uint8_t* piece, uint64_t n, uint64_t gi, uint32_t h, float* w) {
-    if constexpr (F == kQ4_0) {
-        const Q4_0Group q = load_q4_0(piece, n, gi);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) w[j] = weight(q, 16 * h + j);
-    } else if constexpr (F == kQ4_1) {
-        const Q4_1Group q = load_q4_1(piece, n, gi);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) w[j] = weight(q, 16 * h + j);
-    } else if constexpr (F == kQ8_0) {
-        const uint4 c = *reinterpret_cast<const uint4*>(piece + 32 * gi + 16 * h);
-        const float d = half_to_float(*reinterpret_cast<const uint16_t*>(piece + 32 * n + 2 * gi));
-        const uint32_t words[4] = {c.x, c.y, c.z, c.w};
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-            w[j] = static_cast<float>(static_cast<int32_t>(static_cast<int8_t>((words[j >> 2] >> (8 * (j & 3))) & 0xFFu))) * d;
-    } else {
-        const Q6_KGroup q = load_q6_k(piece, n, gi);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) w[j] = weight(q, 16 * h + j);
     }
 }
 

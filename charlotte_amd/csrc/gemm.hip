@@ -28,6 +28,15 @@ __device__ __forceinline__ uint64_t range_sum_at(const Product& a, uint32_t r, u
     return (static_cast<uint64_t>(r) * a.tokens + token) * a.rows + p;
 }
 
+// A group's bytes as loaded; group_of() makes the group weight() decodes.
+template <uint32_t F>
+__device__ __forceinline__ auto fetch_group(const uint8_t* piece, uint64_t n, uint64_t gi) {
+    if constexpr (F == kQ4_0) return fetch_q4_0(piece, n, gi);
+    else if constexpr (F == kQ4_1) return fetch_q4_1(piece, n, gi);
+    else if constexpr (F == kQ8_0) return fetch_q8_0(piece, n, gi);
+    else return fetch_q6_k(piece, n, gi);
+}
+
 // SPLIT: `chunks` workgroups a tile, chunk c taking ranges [32c / chunks,
 // 32(c + 1) / chunks) and writing their sums to `range_sums`; else one a
 // tile, writing the outputs.
@@ -75,40 +84,39 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
     const uint32_t g_begin = range_lo(r_begin, G), g_end = range_lo(r_end, G);
     while (next_r < r_end && range_lo(next_r, G) <= g_begin) ++next_r;
 
+    // Group g + 1's stored bytes and inputs are loaded into registers before
+    // group g's products run, so their round trip overlaps the arithmetic;
+    // they are decoded and staged after the next barrier.
+    decltype(fetch_group<F>(nullptr, 0, 0)) staged{};
+    float4 xnext[XPer / 4];
+    auto fetch = [&](uint32_t g) {
+        if (slive) staged = fetch_group<F>(spiece.piece, spiece.blocks, static_cast<uint64_t>(spiece.row) * G + g);
+        if (xlive) {
+            const float4* src = reinterpret_cast<const float4*>(xsrc + g * 32);
+#pragma unroll
+            for (int v = 0; v < XPer / 4; ++v) xnext[v] = src[v];
+        }
+    };
+    if (g_begin < g_end) fetch(g_begin);
+
     for (uint32_t g = g_begin; g < g_end; ++g) {
         __syncthreads();  // the last group's tiles are read
         {
-            float w[16];
-            if (slive) {
-                const uint64_t gi = static_cast<uint64_t>(spiece.row) * G + g;
-                unpack_half<F>(spiece.piece, spiece.blocks, gi, shalf, w);
-            } else {
+            const auto grp = group_of(staged);
 #pragma unroll
-                for (int j = 0; j < 16; ++j) w[j] = 0.0f;
-            }
-#pragma unroll
-            for (int j = 0; j < 16; ++j) wflat[(16 * shalf + j) * kRowsATile + srow] = w[j];
+            for (int j = 0; j < 16; ++j)
+                wflat[(16 * shalf + j) * kRowsATile + srow] = slive ? weight(grp, 16 * shalf + j) : 0.0f;
         }
-        {
-            float xv[XPer];
-            if (xlive) {
-                const float4* src = reinterpret_cast<const float4*>(xsrc + g * 32);
 #pragma unroll
-                for (int v = 0; v < XPer / 4; ++v) {
-                    const float4 q = clamp_input(a, src[v]);
-                    xv[4 * v] = q.x;
-                    xv[4 * v + 1] = q.y;
-                    xv[4 * v + 2] = q.z;
-                    xv[4 * v + 3] = q.w;
-                }
-            } else {
-#pragma unroll
-                for (int v = 0; v < XPer; ++v) xv[v] = 0.0f;
-            }
-#pragma unroll
-            for (int v = 0; v < XPer; ++v) xflat[(xpart * XPer + v) * BM + xtok] = xv[v];
+        for (int v = 0; v < XPer / 4; ++v) {
+            const float4 q = xlive ? clamp_input(a, xnext[v]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            xflat[(xpart * XPer + 4 * v) * BM + xtok] = q.x;
+            xflat[(xpart * XPer + 4 * v + 1) * BM + xtok] = q.y;
+            xflat[(xpart * XPer + 4 * v + 2) * BM + xtok] = q.z;
+            xflat[(xpart * XPer + 4 * v + 3) * BM + xtok] = q.w;
         }
         __syncthreads();
+        if (g + 1 < g_end) fetch(g + 1);
 #pragma unroll 4
         for (int k = 0; k < 32; ++k) {
             const float4 wa = Ws[k][tx], wb = Ws[k][16 + tx];
