@@ -49,8 +49,8 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
     auto token_at = [&](uint32_t ty, int i) -> uint32_t {
         return TM == 2 ? 2 * ty + i : 4 * ty + (i & 3) + 64 * (i >> 2);
     };
-    __shared__ float4 Ws[32][kRowsATile / 4];
-    __shared__ float4 Xs[32][BM / 4];
+    __shared__ float4 Ws[2][32][kRowsATile / 4];
+    __shared__ float4 Xs[2][32][BM / 4];
     const uint32_t t = threadIdx.x, tx = t & 15u, ty = t >> 4;
     const uint32_t tile_t = blockIdx.x % token_tiles, tile_r = (blockIdx.x / token_tiles) % row_tiles;
     const uint32_t chunk = blockIdx.x / (token_tiles * row_tiles);
@@ -68,8 +68,6 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
     const uint32_t xtok = t % BM, xpart = t / BM;
     const bool xlive = m0 + xtok < a.tokens;
     const float* xsrc = a.x + static_cast<uint64_t>(m0 + xtok) * K + xpart * XPer;
-    float* wflat = reinterpret_cast<float*>(Ws);
-    float* xflat = reinterpret_cast<float*>(Xs);
 
     float s[TM][8], tot[TM][8];
 #pragma unroll
@@ -84,9 +82,10 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
     const uint32_t g_begin = range_lo(r_begin, G), g_end = range_lo(r_end, G);
     while (next_r < r_end && range_lo(next_r, G) <= g_begin) ++next_r;
 
-    // Group g + 1's stored bytes and inputs are loaded into registers before
-    // group g's products run, so their round trip overlaps the arithmetic;
-    // they are decoded and staged after the next barrier.
+    // Two tiles in LDS: group g's products read one while group g + 1 is
+    // staged into the other, one barrier a group. Group g + 2's stored bytes
+    // and inputs are loaded into registers behind that barrier, so their round
+    // trip overlaps group g + 1's arithmetic.
     decltype(fetch_group<F>(nullptr, 0, 0)) staged{};
     float4 xnext[XPer / 4];
     auto fetch = [&](uint32_t g) {
@@ -97,16 +96,13 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
             for (int v = 0; v < XPer / 4; ++v) xnext[v] = src[v];
         }
     };
-    if (g_begin < g_end) fetch(g_begin);
-
-    for (uint32_t g = g_begin; g < g_end; ++g) {
-        __syncthreads();  // the last group's tiles are read
-        {
-            const auto grp = group_of(staged);
+    auto stage = [&](int b) {
+        float* wflat = reinterpret_cast<float*>(Ws[b]);
+        float* xflat = reinterpret_cast<float*>(Xs[b]);
+        const auto grp = group_of(staged);
 #pragma unroll
-            for (int j = 0; j < 16; ++j)
-                wflat[(16 * shalf + j) * kRowsATile + srow] = slive ? weight(grp, 16 * shalf + j) : 0.0f;
-        }
+        for (int j = 0; j < 16; ++j)
+            wflat[(16 * shalf + j) * kRowsATile + srow] = slive ? weight(grp, 16 * shalf + j) : 0.0f;
 #pragma unroll
         for (int v = 0; v < XPer / 4; ++v) {
             const float4 q = xlive ? clamp_input(a, xnext[v]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -115,26 +111,34 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
             xflat[(xpart * XPer + 4 * v + 2) * BM + xtok] = q.z;
             xflat[(xpart * XPer + 4 * v + 3) * BM + xtok] = q.w;
         }
-        __syncthreads();
-        if (g + 1 < g_end) fetch(g + 1);
+    };
+    if (g_begin < g_end) {
+        fetch(g_begin);
+        stage(0);
+    }
+    __syncthreads();
+    if (g_begin + 1 < g_end) fetch(g_begin + 1);
+
+    for (uint32_t g = g_begin; g < g_end; ++g) {
+        const int b = (g - g_begin) & 1;
 #pragma unroll 4
         for (int k = 0; k < 32; ++k) {
-            const float4 wa = Ws[k][tx], wb = Ws[k][16 + tx];
+            const float4 wa = Ws[b][k][tx], wb = Ws[b][k][16 + tx];
             const float w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
             float x[TM];
             if constexpr (TM == 2) {
-                const float2 xa = reinterpret_cast<const float2*>(Xs[k])[ty];
+                const float2 xa = reinterpret_cast<const float2*>(Xs[b][k])[ty];
                 x[0] = xa.x;
                 x[1] = xa.y;
             } else {
-                const float4 xa = Xs[k][ty];
+                const float4 xa = Xs[b][k][ty];
                 x[0] = xa.x;
                 x[1] = xa.y;
                 x[2] = xa.z;
                 x[3] = xa.w;
             }
             if constexpr (TM == 8) {
-                const float4 xb = Xs[k][16 + ty];
+                const float4 xb = Xs[b][k][16 + ty];
                 x[4] = xb.x;
                 x[5] = xb.y;
                 x[6] = xb.z;
@@ -168,6 +172,11 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
             }
             while (next_r < r_end && range_lo(next_r, G) <= g + 1) ++next_r;
         }
+        // Group g + 1 into the other tile, last read by group g - 1's products
+        // before the previous barrier.
+        if (g + 1 < g_end) stage(b ^ 1);
+        __syncthreads();
+        if (g + 2 < g_end) fetch(g + 2);
     }
     if constexpr (SPLIT) return;
 
