@@ -201,9 +201,15 @@ __global__ __launch_bounds__(256) void combine_ranges(Product a, const float* ra
     const uint64_t id = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (id >= static_cast<uint64_t>(a.tokens) * a.rows) return;
     const uint32_t token = static_cast<uint32_t>(id / a.rows), p = static_cast<uint32_t>(id % a.rows);
+    // All 32 loads issued before the first add — every range's slot lies in
+    // the buffer, written or not — then the non-empty ranges added in order.
+    float sums[32];
+#pragma unroll
+    for (uint32_t r = 0; r < 32; ++r) sums[r] = range_sums[range_sum_at(a, r, token, p)];
     float total = 0.0f;
+#pragma unroll
     for (uint32_t r = 0; r < 32; ++r)
-        if (range_lo(r, a.groups) < range_lo(r + 1, a.groups)) total = total + range_sums[range_sum_at(a, r, token, p)];
+        if (range_lo(r, a.groups) < range_lo(r + 1, a.groups)) total = total + sums[r];
     emit<true>(a, p, token, token, total, 0.0f);
 }
 
