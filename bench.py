@@ -246,8 +246,46 @@ def run_c3(S, steps, warmup, rng, fused=True):
     gbs = total / (ms * 1e-3) / 1e9
     log(f"{tag}: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s aggregate, {1e3 / ms:.0f} tokens/s; "
         f"launched eagerly {single * 1e3:.1f} us/step")
-    return {"ms_per_step": ms, "bytes": total, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "launches": len(launches),
-            "tokens_per_s": 1e3 / ms, "ms_single_launch": single}
+    out = {"ms_per_step": ms, "bytes": total, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "launches": len(launches),
+           "tokens_per_s": 1e3 / ms, "ms_single_launch": single}
+    if fused:
+        out.update(decode_matches_prefill(S, launches, xs, rng))
+    return out
+
+
+def decode_matches_prefill(S, launches, xs, rng, tokens=4):
+    """The step's token decoded alone (the outputs the timed launches wrote) against the same token
+    prefilled as the last of `tokens`: every product, bit for bit (the consistency the reference tracks,
+    tests/gpu/matmul_test.cpp:257-267)."""
+    from charlotte_amd import synthetic
+
+    mm = S.mm
+    S.stream.sync()
+    prefill_x = {}
+    for c, b in xs.items():
+        rows = np.concatenate([synthetic.activations(rng, tokens - 1, c), b.read(np.float32).reshape(1, c)])
+        prefill_x[c] = S.buffer(rows)
+    compared = differing = 0
+    for m in launches:
+        columns = m.members[0].weight.columns
+        if m.epilogue == mm.Epilogue.QKV:
+            widths = [mem.weight.rows for mem in m.members]
+        else:
+            widths = [m.members[0].weight.rows]
+        outs = [S.buffer(nbytes=4 * w * tokens) for w in widths]
+        p = mm.MatmulLaunch(m.members, prefill_x[columns].ptr, [o.ptr for o in outs], epilogue=m.epilogue,
+                            activation=m.activation)
+        mm.launch(S.ctx, p, tokens, stream=S.stream.handle)
+        S.stream.sync()
+        for ptr, o, w in zip(m.outputs, outs, widths):
+            decoded = np.empty(w, np.float32)
+            S.hx.check(S.hx.lib.chx_d2h(decoded.ctypes.data, ptr, 4 * w), "d2h")
+            last = o.read(np.uint32).reshape(tokens, w)[-1]
+            compared += w
+            differing += int((decoded.view(np.uint32) != last).sum())
+    log(f"decode vs prefill (token {tokens} of {tokens}): {compared} outputs of {len(launches)} products, "
+        f"{differing} differ")
+    return {"decode_prefill_outputs_compared": compared, "decode_prefill_bits_equal": differing == 0}
 
 
 def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=None):
