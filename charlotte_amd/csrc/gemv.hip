@@ -12,8 +12,9 @@
 // lane exactly 9 groups — 8 ranges, 144 contiguous code bytes.
 //
 // x: lane j's slice never changes, so with SPAN <= 3 groups it is loaded into
-// registers once; otherwise the workgroup stages all of x in LDS once and
-// lanes read it there (lanes of one j read the same words: a broadcast).
+// registers once; otherwise the workgroup stages all of x in LDS once,
+// interleaved by range so a half-wave's lanes read consecutive words (L = 32;
+// the two half-waves read the same words: a broadcast).
 // Each step loads all of its groups' bytes before decoding any, so a wave
 // has a step's weights in flight at once.
 // Range sums meet in LDS, 33 floats a row (padded against bank conflicts);
@@ -124,18 +125,20 @@ __global__ __launch_bounds__(256, kRangesMinBlocks) void gemv_ranges(Product a, 
             for (int k = 0; k < SPAN * 32; ++k) xr[k] = clamp_to(xr[k], lo, hi);
         }
     } else {
-        // At most SPAN float4 a thread (G <= 32 SPAN): every load issued
-        // (clamped inside x) before any is stored, so they go out together
-        // behind the first batch's.
+        // Staged range-interleaved: float4 v of group g0(r) + i of range r at
+        // xs4[256 i + 32 v + r], so the 32 lanes of a half-wave, one a range,
+        // read 32 consecutive float4 (range-major, they would all fall in the
+        // same banks). Thread t stages range t % 32, float4 t / 32 of each of
+        // its range's groups; every load is issued before any is stored.
         const float4* src = reinterpret_cast<const float4*>(x);
+        const uint32_t sr = threadIdx.x & 31u, sv = threadIdx.x >> 5;
+        const uint32_t s0 = range_lo(sr, G), s1 = range_lo(sr + 1, G);
         float4 xv[SPAN];
 #pragma unroll
-        for (int k = 0; k < SPAN; ++k) xv[k] = src[min(threadIdx.x + 256 * k, G * 8 - 1)];
+        for (int k = 0; k < SPAN; ++k) xv[k] = src[min(s0 + k, G - 1) * 8 + sv];
 #pragma unroll
-        for (int k = 0; k < SPAN; ++k) {
-            const uint32_t v = threadIdx.x + 256 * k;
-            if (v < G * 8) xs4[v] = clamp_input(a, xv[k]);
-        }
+        for (int k = 0; k < SPAN; ++k)
+            xs4[256 * k + threadIdx.x] = s0 + k < s1 ? clamp_input(a, xv[k]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         __syncthreads();
     }
 #pragma unroll
@@ -164,10 +167,10 @@ __global__ __launch_bounds__(256, kRangesMinBlocks) void gemv_ranges(Product a, 
                                 s = raw[b][i].chain(xr + 32 * i, s);
                             } else {
                                 float xg[32];
-                                const float4* src = xs4 + 8 * (g0 + i);
+                                const float4* src = xs4 + 256 * i + r;
 #pragma unroll
                                 for (int v = 0; v < 8; ++v) {
-                                    const float4 q = src[v];
+                                    const float4 q = src[32 * v];
                                     xg[4 * v] = q.x;
                                     xg[4 * v + 1] = q.y;
                                     xg[4 * v + 2] = q.z;
@@ -501,7 +504,11 @@ template <uint32_t F, int L, int SPAN, bool XREG, bool FULL>
 static void go_epilogue(const Product& a, uint32_t steps, uint32_t compute_units, hipStream_t stream) {
     const uint32_t rows_a_tile = kWaves * steps * (64 / L);
     const uint32_t tiles = (a.rows + rows_a_tile - 1) / rows_a_tile;
-    const size_t lds = XREG ? 0 : (static_cast<size_t>(a.groups) * 32 + (L == 4 ? 16 : 0)) * sizeof(float);
+    // x staged: L = 32, SPAN float4 a thread (range-interleaved); L = 4, x in
+    // order with a pad.
+    const size_t lds = XREG ? 0
+                       : L == 32 ? static_cast<size_t>(SPAN) * 256 * sizeof(float4)
+                                 : (static_cast<size_t>(a.groups) * 32 + 16) * sizeof(float);
     if constexpr (L == 32) {
         // Steps are a power of two: a batch is never more than a wave's steps,
         // so no load is issued for a row the wave does not decode.
