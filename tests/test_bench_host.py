@@ -1,0 +1,44 @@
+"""bench.py's host side, without a GPU: the algorithmic bytes its rooflines
+divide by (the figures the measurement plan fixes for C1-C3), the CPU
+baseline's fields on a small sample, and its refusal of more than one GPU.
+"""
+
+import os
+import subprocess
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+import bench  # noqa: E402
+
+
+def test_gemv_bytes_are_the_algorithmic_figures():
+    # stored weight bytes + 4 K (x) + 4 N (y)
+    assert bench.gemv_bytes(2, 3072, 1024) == 1_785_856  # C1
+    assert bench.gemv_bytes(14, 262144, 1152) == 248_779_264  # C2
+    # C3 unfused: 28 layers of seven Q4_0 products and the Q6_K head, 197 launches
+    layer = [(2048, 1024), (1024, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (3072, 1024), (1024, 3072)]
+    total = 28 * sum(bench.gemv_bytes(2, r, c) for r, c in layer) + bench.gemv_bytes(14, 151936, 1024)
+    assert total == 378_487_296
+
+
+def test_cpu_baseline_reports_its_fields_on_a_sample():
+    from charlotte_amd import synthetic
+
+    rng = np.random.default_rng(1)
+    rows, columns = 256, 1152
+    stored = synthetic.q6_k(rng, rows, columns)
+    x = synthetic.activations(rng, 1, columns)
+    r = bench.cpu_baseline_c2(stored, x, rows, columns, seconds=0.05)
+    assert set(r) == {"value", "unit", "cores", "kind", "sample"}
+    assert r["unit"] == "GB/s" and r["kind"] == "port" and r["cores"] >= 1 and r["value"] > 0
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode != 0
+    assert "one GPU" in r.stderr
