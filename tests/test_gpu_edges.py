@@ -1,0 +1,96 @@
+"""Extreme values through every canonical decode kernel and the prefill tile,
+against the oracle: weights whose block scales take the reference tests' edge
+values (+-0, the smallest and largest subnormal, +-65504; Q6_K sub-block
+scales -128 and 127), and inputs holding +inf, NaN, +-1e28, subnormals and -0,
+one kind of special a token, and a token whose inputs are all subnormal
+(reading them as zero would change its bits). Finite outputs must be the oracle's bits and
+NaN outputs NaN (a NaN's payload is not part of the order of addition).
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+from tests.support import blocks as B
+from tests.support.oracle_lib import Q4_0, Q6_K
+
+pytestmark = pytest.mark.gpu
+
+THREADS = max(1, min(16, os.cpu_count() or 1))
+BLOCK_BYTES = {Q4_0: 18, Q6_K: 210}
+D_OFFSET = {Q4_0: 0, Q6_K: 208}  # where a block's fp16 d lies
+WEIGHTS_A_BLOCK = {Q4_0: 32, Q6_K: 256}
+
+
+@pytest.fixture(scope="module")
+def run():
+    from charlotte_amd import matmul as mm
+    from tests.support.gpu import Runner
+
+    c = mm.Context(0)
+    c.set_gemm_path(mm.GemmPath.CANONICAL)
+    yield Runner(c)
+    c.close()
+
+
+def _edge_weight(gtype, rows, columns):
+    """The format's edge blocks, and every fifth block's d set to one of the
+    edge scales in turn."""
+    count = rows * columns // WEIGHTS_A_BLOCK[gtype]
+    stored = bytearray(B.q4_0_edge_blocks(count) if gtype == Q4_0 else B.q6_k_edge_blocks(count))
+    size, at = BLOCK_BYTES[gtype], D_OFFSET[gtype]
+    for b in range(0, count, 5):
+        d = B.EDGE_SCALES[(b // 5) % len(B.EDGE_SCALES)]
+        stored[size * b + at : size * b + at + 2] = int(d).to_bytes(2, "little")
+    return bytes(stored)
+
+
+def _special_inputs(columns, seed):
+    """Five tokens: huge (1e28, so most products stay finite against the
+    largest weights), subnormal and -0 values; one +inf (inf or NaN where its
+    weight is 0); one NaN; plain N(0, 1); N(0, 1) x 1e-39, every input
+    subnormal."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((5, columns), dtype=np.float32)
+    x[4] = (x[4].astype(np.float64) * 1e-39).astype(np.float32)
+    x[0, 3], x[0, 40], x[0, 41], x[0, columns - 1] = 1e28, 1e-40, -1e-42, -0.0
+    x[0, 77::97] = np.float32(-1e28)
+    x[0, 13::61] = np.float32(3e-39)
+    x[1, columns // 2] = np.inf
+    x[2, 5] = np.nan
+    return x
+
+
+def _check(got, want, what):
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    nan_w, nan_g = np.isnan(want), np.isnan(got)
+    assert (nan_w == nan_g).all(), f"{what}: NaN at {np.argwhere(nan_w != nan_g)[:4].tolist()}"
+    gb, wb = got[~nan_w].view(np.uint32), want[~nan_w].view(np.uint32)
+    bad = np.flatnonzero(gb != wb)
+    assert bad.size == 0, f"{what}: {bad.size} differ; first got {got[~nan_w][bad[0]]!r} want {want[~nan_w][bad[0]]!r}"
+
+
+# (format, rows, K): the ranges kernel with x in registers and staged in LDS,
+# the L = 4 kernel (rows not whole 16-row steps), the streamed K = 1,152 and
+# K = 1,024 / 2,048 kernels.
+CASES = [(Q4_0, 256, 1024), (Q4_0, 96, 4096), (Q6_K, 70, 1152), (Q6_K, 64, 1152), (Q6_K, 64, 1024),
+         (Q6_K, 48, 2048)]
+
+
+@pytest.mark.parametrize("gtype,rows,columns", CASES)
+def test_edges_decoded_and_prefilled(oracle, run, gtype, rows, columns):
+    stored = _edge_weight(gtype, rows, columns)
+    x = _special_inputs(columns, seed=rows + columns)
+    w = run.weight(gtype, rows, columns, stored)
+    try:
+        want = oracle.matmul_f32(gtype, stored, rows, columns, x, threads=THREADS)
+        assert np.isfinite(want[0]).mean() > 0.5 and np.isfinite(want[3]).mean() > 0.5 and np.isnan(want[2]).all()
+        for t in range(5):
+            got = run.write(w, x[t : t + 1], 1)
+            _check(got[0], want[t], f"decode token {t}")
+        got = run.write(w, x, 5)
+        _check(got, want, "prefill")
+    finally:
+        w.free()
