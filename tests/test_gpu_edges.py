@@ -34,11 +34,12 @@ def run():
     c.close()
 
 
-def _edge_weight(gtype, rows, columns):
-    """The format's edge blocks, and every fifth block's d set to one of the
-    edge scales in turn."""
+def _edge_weight(gtype, rows, columns, seed=None):
+    """The format's edge blocks (their codes and later scales from the LCG at
+    `seed`), and every fifth block's d set to one of the edge scales in turn."""
     count = rows * columns // WEIGHTS_A_BLOCK[gtype]
-    stored = bytearray(B.q4_0_edge_blocks(count) if gtype == Q4_0 else B.q6_k_edge_blocks(count))
+    make = B.q4_0_edge_blocks if gtype == Q4_0 else B.q6_k_edge_blocks
+    stored = bytearray(make(count) if seed is None else make(count, seed=seed))
     size, at = BLOCK_BYTES[gtype], D_OFFSET[gtype]
     for b in range(0, count, 5):
         d = B.EDGE_SCALES[(b // 5) % len(B.EDGE_SCALES)]
@@ -94,3 +95,38 @@ def test_edges_decoded_and_prefilled(oracle, run, gtype, rows, columns):
         _check(got, want, "prefill")
     finally:
         w.free()
+
+
+@pytest.mark.parametrize("columns", [1024, 1152])
+def test_edges_through_the_epilogues(oracle, run, columns):
+    """The same weights and inputs through GatedActivation (SiLU) and Write
+    with bias and GELU-tanh: the activations of huge, infinite and NaN
+    totals, decoded and prefilled."""
+    from charlotte_amd import matmul as mm
+
+    gtype, rows = (Q4_0, 128) if columns == 1024 else (Q6_K, 64)
+    stored = [_edge_weight(gtype, rows, columns), _edge_weight(gtype, rows, columns, seed=0x68E31DA4)]
+    x = _special_inputs(columns, seed=7 * columns)
+    ws = [run.weight(gtype, rows, columns, s) for s in stored]
+    try:
+        gate = oracle.matmul_f32(gtype, stored[0], rows, columns, x, threads=THREADS)
+        up = oracle.matmul_f32(gtype, stored[1], rows, columns, x, threads=THREADS)
+        want_gated = oracle.gated(gate, up, activation=0)
+        bias = np.linspace(-3.0, 3.0, rows, dtype=np.float32)
+        want_write = oracle.finish(gate, bias=bias, activated=True, activation=1)
+        for t in (0, 1, 3, 4):
+            got = run.product([mm.Member(ws[0]), mm.Member(ws[1])], x[t : t + 1], 1, [rows],
+                              epilogue=mm.Epilogue.GatedActivation, activation=mm.Activation.SiLU)[0]
+            _check(got[0], want_gated[t], f"gated decode token {t}")
+            got = run.product([mm.Member(ws[0])], x[t : t + 1], 1, [rows], bias=bias, activated=True,
+                              activation=mm.Activation.GeluTanh)[0]
+            _check(got[0], want_write[t], f"write decode token {t}")
+        got = run.product([mm.Member(ws[0]), mm.Member(ws[1])], x, 5, [rows], epilogue=mm.Epilogue.GatedActivation,
+                          activation=mm.Activation.SiLU)[0]
+        _check(got, want_gated, "gated prefill")
+        got = run.product([mm.Member(ws[0])], x, 5, [rows], bias=bias, activated=True,
+                          activation=mm.Activation.GeluTanh)[0]
+        _check(got, want_write, "write prefill")
+    finally:
+        for w in ws:
+            w.free()
