@@ -100,6 +100,24 @@ def test_mfma_input_scaling(oracle, run, scale):
     w.free()
 
 
+@pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
+def test_mfma_non_finite_input_poisons_its_token_only(oracle, run, bad):
+    """A token holding a non-finite input: every output of that token NaN
+    (its exact products are +-inf or NaN; the split of an infinite input is
+    inf + NaN); the other tokens keep the tolerance."""
+    rows, columns, tokens = 256, 1024, 20
+    stored, x = _data(Q4_0, rows, columns, tokens, seed=11)
+    x[6, 500] = bad
+    w = run.weight(Q4_0, rows, columns, stored)
+    got = run.write(w, x, tokens)
+    w.free()
+    assert np.isnan(got[6]).all()
+    keep = [t for t in range(tokens) if t != 6]
+    y64, _ = oracle.matmul_f64(Q4_0, stored, rows, columns, x[keep])
+    canonical = oracle.matmul_f32(Q4_0, stored, rows, columns, x[keep])
+    _within(got[keep], y64, canonical, f"tokens beside the {bad!r} one")
+
+
 def test_mfma_epilogues(oracle, run):
     from charlotte_amd import matmul as mm
 
