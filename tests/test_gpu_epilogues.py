@@ -115,11 +115,14 @@ def test_gated_wide_tiles(oracle, run):
 # ---- GatedByInput (matmul.wgsl:347-364, 575-590) -----------------------------
 
 
-@pytest.mark.parametrize("gtype,columns", [(Q4_0, 2048), (Q6_K, 1152)])
-def test_gated_by_input(oracle, run, gtype, columns):
+# 300 rows: the ranges and L = 4 decodes; 304 (whole 16-row steps): the
+# LDS-streamed Q6_K decodes at K = 1,152, 1,024 and 2,048.
+@pytest.mark.parametrize("gtype,columns,rows", [(Q4_0, 2048, 300), (Q6_K, 1152, 300), (Q6_K, 1152, 304),
+                                                (Q6_K, 1024, 304), (Q6_K, 2048, 304)])
+def test_gated_by_input(oracle, run, gtype, columns, rows):
     from charlotte_amd import matmul as mm
 
-    rows, tokens, stride, column = 300, 40, 337, 17
+    tokens, stride, column = 40, 337, 17
     stored, x = _data(gtype, rows, columns, tokens, seed=21)
     w = run.weight(gtype, rows, columns, stored)
     u = np.random.default_rng(22).standard_normal((tokens, stride), dtype=np.float32)
