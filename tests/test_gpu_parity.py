@@ -218,6 +218,35 @@ def test_c1_q4_0_decode_3072x1024(oracle, run):
     w.free()
 
 
+def test_c2_in_two_pieces_is_the_whole_weights_bits(run):
+    """C2's head as two pieces (the 128 MiB binding splits it, plan.cpp:294-306),
+    one launch a piece writing its rows of the one output (matmul.cpp:283-291):
+    the pieces' rows are not whole 16-row steps, so they take the L = 4
+    decode, and must give the streamed whole weight's bits."""
+    from charlotte_amd import harness as hx
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+    from tests.support.gpu import bits_equal, first_difference
+
+    rng = np.random.default_rng(12)
+    rows, columns = 262144, 1152
+    stored = synthetic.q6_k(rng, rows, columns)
+    x = synthetic.activations(rng, 1, columns)
+    whole = run.weight(Q6_K, rows, columns, stored)
+    want = run.write(whole, x, 1)
+    whole.free()
+    parts = [(0, 142030), (142030, rows - 142030)]  # even rows: whole super-blocks
+    pieces = [run.weight(Q6_K, n, columns, stored[f * 945 : (f + n) * 945]) for f, n in parts]
+    xb, yb = hx.Buffer.of(x), hx.Buffer(rows * 4)
+    for (f, n), p in zip(parts, pieces):
+        mm.launch(run.ctx, mm.MatmulLaunch([mm.Member(p, output_row=f)], xb.ptr, [yb.ptr], out_width=rows), 1)
+    hx.sync()
+    got = yb.read(np.float32).reshape(1, rows)
+    for b in [xb, yb, *pieces]:
+        b.free()
+    assert bits_equal(got, want), first_difference(got, want)
+
+
 def test_c2_q6_k_lm_head_262144x1152(oracle, run):
     from charlotte_amd import synthetic
     from tests.support.gpu import bits_equal, first_difference
