@@ -17,6 +17,7 @@
 #include "gather.hpp"
 #include "gguf.hpp"
 #include "layout.hpp"
+#include "plan.hpp"
 #include "product.hpp"
 
 struct charlotte_hip_matmul_context {
@@ -60,14 +61,13 @@ Status hip_fail(charlotte_hip_matmul_context* ctx, hipError_t e, const char* wha
                 std::string(what) + ": " + hipGetErrorString(e));
 }
 
-// Formats a weight may hold; the products read all but F32, a gather's table.
+// The formats a weight may hold: the reference's format table
+// (capability.cpp:57-65). The products and the gather read them all.
 bool known(uint32_t type) {
-    return type == CHARLOTTE_HIP_MATMUL_F32 || type == CHARLOTTE_HIP_MATMUL_Q4_0 || type == CHARLOTTE_HIP_MATMUL_Q4_1 ||
+    return type == CHARLOTTE_HIP_MATMUL_F32 || type == CHARLOTTE_HIP_MATMUL_F16 || type == CHARLOTTE_HIP_MATMUL_BF16 ||
+           type == CHARLOTTE_HIP_MATMUL_Q4_0 || type == CHARLOTTE_HIP_MATMUL_Q4_1 ||
            type == CHARLOTTE_HIP_MATMUL_Q8_0 || type == CHARLOTTE_HIP_MATMUL_Q6_K;
 }
-bool product_reads(uint32_t type) { return known(type) && type != CHARLOTTE_HIP_MATMUL_F32; }
-// The matrix-core prefill's formats: every product format.
-bool mfma_reads(uint32_t type) { return product_reads(type); }
 
 // The shape checks of a weight: rows of whole 32-weight groups
 // (matmul.h:668-671, format.h:138-160) in a tensor of whole blocks.
@@ -77,17 +77,175 @@ Status check_shape(charlotte_hip_matmul_context* ctx, uint32_t type, uint64_t ro
     if (columns % 32 != 0)
         return fail(ctx, CHARLOTTE_HIP_MATMUL_SHAPE_NOT_GROUPS,
                     "weight: " + std::to_string(columns) + " columns are not whole 32-weight groups");
-    if ((rows * columns) % chm::block_weights_host(type) != 0)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_SHAPE_NOT_GROUPS, "weight: not a whole number of blocks");
+    // Bounded first, so rows x columns (below 2^61) cannot wrap.
     if (rows > 0xFFFFFFFFull || columns / 32 > 0xFFFFFFull)
         return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "weight: too many rows or columns");
+    if ((rows * columns) % chm::block_weights_host(type) != 0)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_SHAPE_NOT_GROUPS, "weight: not a whole number of blocks");
     return CHARLOTTE_HIP_MATMUL_OK;
 }
 
 // kernels_matmul split geometry (matmul.cpp:26-37, 233-250; plan.h:113).
 constexpr uint32_t kTileOutputs = 64, kTileTokens = 32, kPrefillBlock = 512;
-// Under AUTO, steps of fewer tokens stay on the VALU tile.
-constexpr uint32_t kMfmaLeast = 16;
+
+uint32_t split_tokens_of(uint32_t epilogue, uint64_t rows, uint64_t columns, charlotte_hip_matmul_split_gate gate) {
+    if (epilogue == CHARLOTTE_HIP_MATMUL_GATED_ACTIVATION || gate.denominator == 0 || rows == 0) return 1;
+    const uint64_t groups = columns / 32;
+    const uint64_t out_tiles = (rows + kTileOutputs - 1) / kTileOutputs;
+    const uint64_t by_ratio = groups * gate.numerator / (uint64_t{gate.denominator} * out_tiles);
+    const uint64_t by_cap = gate.max_workgroups / out_tiles;
+    const uint64_t token_tiles = std::min(by_ratio, by_cap);
+    if (token_tiles == 0) return 1;
+    return static_cast<uint32_t>(std::min<uint64_t>(token_tiles * kTileTokens, kPrefillBlock));
+}
+
+// What a launch is planned for beyond its descriptor.
+struct Target {
+    uint32_t compute_units;
+    uint32_t gemm_path, gemv_path;
+    uint64_t workspace_bytes;
+};
+
+// A failed check: its status and its message.
+struct Verdict {
+    Status status = CHARLOTTE_HIP_MATMUL_OK;
+    std::string message;
+    bool ok() const { return status == CHARLOTTE_HIP_MATMUL_OK; }
+};
+
+Verdict refuse(Status s, std::string message) { return {s, std::move(message)}; }
+
+// A launch's checks and the product its kernels receive, on the host alone:
+// the reference's preconditions (matmul.h:661-671) and this library's. Every
+// sum is taken in 64 bits and every value narrowed to a kernel's 32 is
+// checked first, so no descriptor can wrap past a check into an access
+// outside a weight or an output. `ctx` is the launching context, or null for
+// a plan, which also takes shape-only weights.
+Verdict describe(const charlotte_hip_matmul_desc* desc, uint32_t tokens, const charlotte_hip_matmul_context* ctx,
+                 chm::Product* out, uint32_t* format) {
+    const auto bad = [](std::string m) { return refuse(CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: " + m); };
+    if (!desc) return bad("no descriptor");
+    if (tokens == 0) return bad("a step of no tokens");
+    const charlotte_hip_matmul_desc& d = *desc;
+    if (d.member_count < 1 || d.member_count > 3) return bad("member_count " + std::to_string(d.member_count));
+    if (d.epilogue > CHARLOTTE_HIP_MATMUL_GATED_BY_INPUT) return bad("epilogue " + std::to_string(d.epilogue));
+    if (d.rows > CHARLOTTE_HIP_MATMUL_LAST_TOKEN) return bad("rows " + std::to_string(d.rows));
+    if (d.activation > CHARLOTTE_HIP_MATMUL_SIGMOID) return bad("activation " + std::to_string(d.activation));
+    const uint32_t divisor = d.row_divisor ? d.row_divisor : 1;
+    // program.cpp:382-387: a divided launch is never over the last token.
+    if (divisor != 1 && d.rows == CHARLOTTE_HIP_MATMUL_LAST_TOKEN) return bad("a row divisor over the last token");
+    const bool gated = d.epilogue == CHARLOTTE_HIP_MATMUL_GATED_ACTIVATION;
+    const bool by_input = d.epilogue == CHARLOTTE_HIP_MATMUL_GATED_BY_INPUT;
+    // The options are a Write's; a gated product may be clipped (matmul.h:229-255, 623-629).
+    if ((d.bias || d.activated) && d.epilogue != CHARLOTTE_HIP_MATMUL_WRITE)
+        return bad("bias and activated are a Write's options");
+    if (d.clip && d.epilogue != CHARLOTTE_HIP_MATMUL_WRITE && !gated)
+        return bad("clip is a Write's or a gated product's option");
+    if (gated && d.member_count != 2) return bad("a gated product takes two members, gate and up");
+    if (gated && d.members[0].rows != d.members[1].rows) return bad("gate and up rows differ");
+    if (by_input && !d.gate_input) return bad("GatedByInput without its input");
+    if (!d.input) return bad("no input");
+    if (reinterpret_cast<uintptr_t>(d.input) % 16 != 0) return bad("input not 16-byte aligned");
+    if (d.out_width > 0xFFFFFFFFull) return bad("out_width past 2^32");
+
+    chm::Product a{};
+    const charlotte_hip_matmul_weight* head = d.members[0].weight;
+    if (!head) return bad("member 0 has no weight");
+    if (!known(head->type))
+        return refuse(CHARLOTTE_HIP_MATMUL_UNSUPPORTED_TYPE, "launch: GGUF type " + std::to_string(head->type));
+    uint64_t rows = 0;
+    for (uint32_t i = 0; i < d.member_count; ++i) {
+        const charlotte_hip_matmul_member& m = d.members[i];
+        const std::string who = "member " + std::to_string(i);
+        if (!m.weight) return bad(who + " has no weight");
+        if (ctx && m.weight->ctx != ctx) return bad(who + " of another context");
+        if (ctx && !m.weight->piece) return bad(who + " is a shape-only weight");
+        if (m.weight->type != head->type || m.weight->columns != head->columns)
+            return bad("members differ in format or width");
+        if (m.rows == 0 || m.row_offset > m.weight->rows || m.rows > m.weight->rows - m.row_offset)
+            return bad(who + " rows past its weight");
+        if (m.output_row > 0xFFFFFFFFull) return bad(who + " output_row past 2^32");
+        float* o = d.epilogue == CHARLOTTE_HIP_MATMUL_QKV ? d.outputs[i] : d.outputs[0];
+        if (!o) return bad(who + " has no output");
+        // Weights hold at most 2^32 - 1 rows (check_shape), so each value
+        // below fits 32 bits; `rows` is at most three of them.
+        a.m[i] = chm::Member{m.weight->piece,
+                             m.weight->blocks,
+                             static_cast<uint32_t>(m.row_offset),
+                             static_cast<uint32_t>(m.rows),
+                             static_cast<uint32_t>(std::min<uint64_t>(rows, 0xFFFFFFFFull)),
+                             static_cast<uint32_t>(m.output_row),
+                             static_cast<uint32_t>(d.out_width),
+                             0,
+                             o};
+        rows += m.rows;
+    }
+    if (rows > 0x7FFFFFFFull) return bad("too many rows");
+    // A gated product writes its gate's rows a token; the rest, out_width
+    // (0: the product's rows) with each member at its output_row.
+    const uint64_t width = gated ? d.members[0].rows : rows;
+    for (uint32_t i = 0; i < d.member_count; ++i) {
+        if (a.m[i].out_width == 0) a.m[i].out_width = static_cast<uint32_t>(width);
+        if (gated && a.m[i].out_width < width) return bad("out_width below the gate's rows");
+        if ((d.epilogue == CHARLOTTE_HIP_MATMUL_WRITE || by_input) &&
+            uint64_t{a.m[i].out_row} + a.m[i].rows > a.m[i].out_width)
+            return bad("output rows past out_width");
+    }
+    a.x = d.input;
+    a.members = d.member_count;
+    a.rows = static_cast<uint32_t>(rows);
+    a.groups = static_cast<uint32_t>(head->columns / 32);
+    a.epilogue = d.epilogue;
+    a.activation = d.activation;
+    a.last_token = d.rows == CHARLOTTE_HIP_MATMUL_LAST_TOKEN;
+    a.tokens = tokens / divisor;  // the launch's rows (matmul.wgsl:87-91)
+    a.gate_stride = d.gate_input_stride;
+    a.gate_column = d.gate_input_column;
+    a.gate_input = d.gate_input;
+    a.clip = d.clip;
+    a.bias = d.bias;
+    a.activated = d.activated ? 1u : 0u;
+    *out = a;
+    *format = head->type;
+    return {};
+}
+
+// The kernel a described product runs on `t`, and its shape: decode for one
+// token or the head's last; else the VALU tile, split along K when the gate
+// allows the step and its range sums fit `range_sums_bytes` (a product with
+// options, or gated, never splits: matmul.cpp:166-172, 233-241), or the
+// matrix cores when the target asks for them.
+Verdict plan_product(const chm::Product& a, uint32_t format, const Target& t, charlotte_hip_matmul_split_gate gate,
+                     uint64_t range_sums_bytes, chm::Plan* plan) {
+    *plan = chm::Plan{};
+    if (a.tokens == 0) return {};  // a divided step of fewer tokens than the divisor: nothing runs
+    if (a.tokens == 1 || a.last_token) {
+        if (!chm::plan_gemv(a, format, t.compute_units, t.gemv_path == CHARLOTTE_HIP_MATMUL_GEMV_INT8_LIMBS, plan))
+            return refuse(CHARLOTTE_HIP_MATMUL_UNSUPPORTED, "launch: no decode kernel takes the product");
+        return {};
+    }
+    if (t.gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_SPLIT_F16_MFMA) {
+        if (!chm::mfma_reads(format))
+            return refuse(CHARLOTTE_HIP_MATMUL_UNSUPPORTED,
+                          "launch: the matrix-core prefill reads Q4_0, Q4_1, Q8_0 and Q6_K, not GGUF type " +
+                              std::to_string(format));
+        const uint64_t need = chm::mfma_workspace_bytes(a.tokens, a.groups);
+        if (t.workspace_bytes < need)
+            return refuse(CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT,
+                          "launch: the matrix-core path needs a workspace of " + std::to_string(need) + " bytes");
+        chm::plan_gemm_mfma(a, format, t.compute_units, plan);
+        return {};
+    }
+    bool split = false;
+    const bool options = a.clip || a.bias || a.activated;
+    if (!options && a.epilogue != chm::kGated && range_sums_bytes && gate.denominator) {
+        const uint64_t fits = range_sums_bytes / 4 / (uint64_t{a.rows} * 32);
+        const uint64_t most = std::min<uint64_t>(split_tokens_of(a.epilogue, a.rows, uint64_t{a.groups} * 32, gate), fits);
+        split = a.tokens <= most;
+    }
+    chm::plan_gemm_canonical(a, t.compute_units, split, plan);
+    return {};
+}
 
 }  // namespace
 
@@ -233,6 +391,19 @@ charlotte_hip_matmul_status charlotte_hip_matmul_weight_wrap(charlotte_hip_matmu
     return ok(ctx);
 }
 
+charlotte_hip_matmul_status charlotte_hip_matmul_weight_shape(uint32_t gguf_type, uint64_t rows, uint64_t columns,
+                                                              charlotte_hip_matmul_weight** out) {
+    if (!out) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    *out = nullptr;
+    if (Status s = check_shape(nullptr, gguf_type, rows, columns); s != CHARLOTTE_HIP_MATMUL_OK) return s;
+    auto* w = new (std::nothrow) charlotte_hip_matmul_weight;
+    if (!w) return CHARLOTTE_HIP_MATMUL_OUT_OF_MEMORY;
+    const uint64_t blocks = rows * columns / chm::block_weights_host(gguf_type);
+    *w = {nullptr, gguf_type, rows, columns, blocks, chm::layout_bytes(gguf_type, blocks), nullptr, false};
+    *out = w;
+    return CHARLOTTE_HIP_MATMUL_OK;
+}
+
 charlotte_hip_matmul_status charlotte_hip_matmul_weight_free(charlotte_hip_matmul_weight* weight) {
     if (!weight) return CHARLOTTE_HIP_MATMUL_OK;
     Status s = CHARLOTTE_HIP_MATMUL_OK;
@@ -250,20 +421,53 @@ const void* charlotte_hip_matmul_weight_device(const charlotte_hip_matmul_weight
 
 uint32_t charlotte_hip_matmul_split_tokens(uint32_t epilogue, uint64_t rows, uint64_t columns,
                                            charlotte_hip_matmul_split_gate gate) {
-    if (epilogue == CHARLOTTE_HIP_MATMUL_GATED_ACTIVATION || gate.denominator == 0 || rows == 0) return 1;
-    const uint64_t groups = columns / 32;
-    const uint64_t out_tiles = (rows + kTileOutputs - 1) / kTileOutputs;
-    const uint64_t by_ratio = groups * gate.numerator / (uint64_t{gate.denominator} * out_tiles);
-    const uint64_t by_cap = gate.max_workgroups / out_tiles;
-    const uint64_t token_tiles = std::min(by_ratio, by_cap);
-    if (token_tiles == 0) return 1;
-    return static_cast<uint32_t>(std::min<uint64_t>(token_tiles * kTileTokens, kPrefillBlock));
+    return split_tokens_of(epilogue, rows, columns, gate);
 }
 
 uint64_t charlotte_hip_matmul_range_sum_floats(uint32_t epilogue, uint64_t rows, uint64_t columns,
                                                charlotte_hip_matmul_split_gate gate) {
-    const uint32_t split = charlotte_hip_matmul_split_tokens(epilogue, rows, columns, gate);
+    const uint32_t split = split_tokens_of(epilogue, rows, columns, gate);
     return split < 2 ? 0 : uint64_t{split} * rows * 32;
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_plan_launch(const charlotte_hip_matmul_desc* desc,
+                                                             const charlotte_hip_matmul_target* target,
+                                                             charlotte_hip_matmul_split_gate gate,
+                                                             uint64_t range_sums_bytes, uint32_t tokens,
+                                                             charlotte_hip_matmul_plan* out, char* message,
+                                                             uint64_t message_bytes) {
+    if (message && message_bytes) message[0] = 0;
+    if (!target || !out || target->compute_units == 0) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    *out = charlotte_hip_matmul_plan{};
+    chm::Product a{};
+    uint32_t format = 0;
+    Verdict v = describe(desc, tokens, nullptr, &a, &format);
+    chm::Plan plan;
+    if (v.ok())
+        v = plan_product(a, format, Target{target->compute_units, target->gemm_path, target->gemv_path,
+                                           target->workspace_bytes},
+                         gate, range_sums_bytes, &plan);
+    if (!v.ok()) {
+        if (message && message_bytes) {
+            const size_t n = std::min<uint64_t>(v.message.size(), message_bytes - 1);
+            std::memcpy(message, v.message.data(), n);
+            message[n] = 0;
+        }
+        return v.status;
+    }
+    out->kernel = plan.kernel;
+    out->launches = plan.launches;
+    out->canonical = plan.canonical ? 1u : 0u;
+    out->rows = a.last_token ? 1u : a.tokens;
+    out->lanes_a_row = plan.lanes;
+    out->groups_a_lane = plan.span;
+    out->steps_a_wave = plan.steps;
+    out->tile_tokens = plan.tile_tokens;
+    out->tile_rows = plan.tile_rows;
+    out->chunks = plan.chunks;
+    out->tiles = plan.tiles;
+    out->workgroups = plan.workgroups;
+    return CHARLOTTE_HIP_MATMUL_OK;
 }
 
 charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_context* ctx,
@@ -271,123 +475,25 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
                                                         charlotte_hip_matmul_split_gate gate, void* range_sums,
                                                         uint64_t range_sums_bytes, uint32_t tokens, void* stream) {
     if (!ctx) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
-    if (!desc) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: no descriptor");
-    if (tokens == 0) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: a step of no tokens");
-    const charlotte_hip_matmul_desc& d = *desc;
-    if (d.member_count < 1 || d.member_count > 3)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member_count " + std::to_string(d.member_count));
-    if (d.epilogue > CHARLOTTE_HIP_MATMUL_GATED_BY_INPUT)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: epilogue " + std::to_string(d.epilogue));
-    if (d.rows > CHARLOTTE_HIP_MATMUL_LAST_TOKEN)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: rows " + std::to_string(d.rows));
-    if (d.activation > CHARLOTTE_HIP_MATMUL_SIGMOID)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: activation " + std::to_string(d.activation));
-    const bool gated = d.epilogue == CHARLOTTE_HIP_MATMUL_GATED_ACTIVATION;
-    const bool by_input = d.epilogue == CHARLOTTE_HIP_MATMUL_GATED_BY_INPUT;
-    // The options are a Write's; a gated product may be clipped (matmul.h:229-255, 623-629).
-    if ((d.bias || d.activated) && d.epilogue != CHARLOTTE_HIP_MATMUL_WRITE)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: bias and activated are a Write's options");
-    if (d.clip && d.epilogue != CHARLOTTE_HIP_MATMUL_WRITE && !gated)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: clip is a Write's or a gated product's option");
-    if (gated && d.member_count != 2)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: a gated product takes two members, gate and up");
-    if (gated && d.members[0].rows != d.members[1].rows)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: gate and up rows differ");
-    if (by_input && !d.gate_input)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: GatedByInput without its input");
-    if (!d.input) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: no input");
-    if (reinterpret_cast<uintptr_t>(d.input) % 16 != 0)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: input not 16-byte aligned");
-
     chm::Product a{};
-    const charlotte_hip_matmul_weight* head = d.members[0].weight;
-    if (!head) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member 0 has no weight");
-    if (!product_reads(head->type))
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_UNSUPPORTED_TYPE,
-                    "launch: GGUF type " + std::to_string(head->type) + " (the products read Q4_0, Q4_1, Q8_0, Q6_K)");
-    uint64_t rows = 0;
-    for (uint32_t i = 0; i < d.member_count; ++i) {
-        const charlotte_hip_matmul_member& m = d.members[i];
-        if (!m.weight) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member " + std::to_string(i) + " has no weight");
-        if (m.weight->ctx != ctx) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member " + std::to_string(i) + " of another context");
-        if (m.weight->type != head->type || m.weight->columns != head->columns)
-            return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: members differ in format or width");
-        if (m.rows == 0 || m.row_offset + m.rows > m.weight->rows)
-            return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member " + std::to_string(i) + " rows past its weight");
-        float* out = d.epilogue == CHARLOTTE_HIP_MATMUL_QKV ? d.outputs[i] : d.outputs[0];
-        if (!out) return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: member " + std::to_string(i) + " has no output");
-        a.m[i] = chm::Member{m.weight->piece,
-                             m.weight->blocks,
-                             static_cast<uint32_t>(m.row_offset),
-                             static_cast<uint32_t>(m.rows),
-                             static_cast<uint32_t>(rows),
-                             static_cast<uint32_t>(m.output_row),
-                             static_cast<uint32_t>(d.out_width),
-                             0,
-                             out};
-        rows += m.rows;
-    }
-    if (rows > 0x7FFFFFFFull || d.out_width > 0xFFFFFFFFull)
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: too many rows");
-    // A gated product writes its gate's rows a token; the rest, out_width
-    // (0: the product's rows) with each member at its output_row.
-    const uint64_t width = gated ? d.members[0].rows : rows;
-    for (uint32_t i = 0; i < d.member_count; ++i) {
-        if (a.m[i].out_width == 0) a.m[i].out_width = static_cast<uint32_t>(width);
-        if (gated && a.m[i].out_width < width)
-            return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: out_width below the gate's rows");
-        if ((d.epilogue == CHARLOTTE_HIP_MATMUL_WRITE || by_input) && a.m[i].out_row + a.m[i].rows > a.m[i].out_width)
-            return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: output rows past out_width");
-    }
-    a.x = d.input;
-    a.members = d.member_count;
-    a.rows = static_cast<uint32_t>(rows);
-    a.groups = static_cast<uint32_t>(head->columns / 32);
-    a.epilogue = d.epilogue;
-    a.activation = d.activation;
-    a.last_token = d.rows == CHARLOTTE_HIP_MATMUL_LAST_TOKEN;
-    a.tokens = tokens;
-    a.gate_stride = d.gate_input_stride;
-    a.gate_column = d.gate_input_column;
-    a.gate_input = d.gate_input;
-    a.clip = d.clip;
-    a.bias = d.bias;
-    a.activated = d.activated ? 1u : 0u;
-
+    uint32_t format = 0;
+    Verdict v = describe(desc, tokens, ctx, &a, &format);
+    chm::Plan plan;
+    const Target target{ctx->compute_units, ctx->gemm_path, ctx->gemv_path,
+                        ctx->workspace ? ctx->workspace_bytes : 0};
+    if (v.ok()) v = plan_product(a, format, target, gate, range_sums ? range_sums_bytes : 0, &plan);
+    if (!v.ok()) return fail(ctx, v.status, v.message);
+    if (plan.kernel == chm::kNoKernel) return ok(ctx);
+    if (plan.kernel == chm::kGemmSplit && reinterpret_cast<uintptr_t>(range_sums) % 4 != 0)
+        return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: range_sums not 4-byte aligned");
     if (hipError_t e = hipSetDevice(ctx->device); e != hipSuccess) return hip_fail(ctx, e, "launch: hipSetDevice");
     auto* s = static_cast<hipStream_t>(stream);
     hipError_t e;
-    const bool decode = tokens == 1 || a.last_token;
-    if (decode && !chm::gemv_supports(a.groups))
-        return fail(ctx, CHARLOTTE_HIP_MATMUL_UNSUPPORTED,
-                    "launch: decode of K = " + std::to_string(head->columns) + " (built for K up to 8,192)");
-    if (decode) {
-        e = chm::launch_gemv(a, head->type, ctx->compute_units, ctx->gemv_path == CHARLOTTE_HIP_MATMUL_GEMV_INT8_LIMBS, s);
-    } else {
-        // The split form takes the steps the gate allows whose range sums fit
-        // the buffer; a product with options, or gated, never splits
-        // (matmul.cpp:166-172, 233-241).
-        uint64_t split = 1;
-        const bool options = d.clip || d.bias || d.activated;
-        if (!options && !gated && range_sums && range_sums_bytes && gate.denominator) {
-            if (reinterpret_cast<uintptr_t>(range_sums) % 4 != 0)
-                return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: range_sums not 4-byte aligned");
-            const uint64_t fits = range_sums_bytes / 4 / (rows * 32);
-            split = std::min<uint64_t>(charlotte_hip_matmul_split_tokens(d.epilogue, rows, head->columns, gate), fits);
-        }
-        float* sums = tokens <= split ? static_cast<float*>(range_sums) : nullptr;
-        // The matrix cores: when asked, or under AUTO for a step the split
-        // form does not take, given a workspace that holds the step.
-        const uint64_t need = chm::mfma_workspace_bytes(tokens, a.groups);
-        const bool room = ctx->workspace && ctx->workspace_bytes >= need;
-        const bool mfma = ctx->gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_SPLIT_F16_MFMA ||
-                          (ctx->gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_AUTO && !sums && room && tokens >= kMfmaLeast &&
-                           mfma_reads(head->type));
-        if (mfma && !room)
-            return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT,
-                        "launch: the matrix-core path needs a workspace of " + std::to_string(need) + " bytes");
-        e = mfma ? chm::launch_gemm_mfma(a, head->type, ctx->compute_units, ctx->workspace, s)
-                 : chm::launch_gemm_canonical(a, head->type, ctx->compute_units, sums, s);
+    switch (plan.kernel) {
+        case chm::kGemmMfma: e = chm::launch_gemm_mfma(a, format, plan, ctx->workspace, s); break;
+        case chm::kGemmTiled: e = chm::launch_gemm_canonical(a, format, plan, nullptr, s); break;
+        case chm::kGemmSplit: e = chm::launch_gemm_canonical(a, format, plan, static_cast<float*>(range_sums), s); break;
+        default: e = chm::launch_gemv(a, format, plan, ctx->compute_units, s); break;
     }
     if (e != hipSuccess) return hip_fail(ctx, e, "launch");
     return ok(ctx);

@@ -119,9 +119,88 @@ __device__ __forceinline__ float chain_q8_0(const uint32_t w[8], uint32_t d_bits
     return s;
 }
 
+// An F32 group: its 32 floats, the chain over them.
+__device__ __forceinline__ float chain_f32(const uint32_t w[32], const float* x, float s) {
+#pragma unroll
+    for (int l = 0; l < 32; ++l) s = __builtin_fmaf(__uint_as_float(w[l]), x[l], s);
+    return s;
+}
+
+// An F16 group: 16 dwords, two halves each, the lower first. Each half is
+// converted exactly inside the multiply-add (v_fma_mix_f32 takes a binary16
+// operand as its f32 value): one instruction a weight.
+__device__ __forceinline__ float chain_f16(const uint32_t w[16], const float* x, float s) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const half2_t h = __builtin_bit_cast(half2_t, w[i]);
+        s = __builtin_fmaf(static_cast<float>(h.x), x[2 * i], s);
+        s = __builtin_fmaf(static_cast<float>(h.y), x[2 * i + 1], s);
+    }
+    return s;
+}
+
+// A BF16 group: 16 dwords, two values each, the lower first; a value is its
+// 16 bits at the top of an f32 (a shift or a mask), exact.
+__device__ __forceinline__ float chain_bf16(const uint32_t w[16], const float* x, float s) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        s = __builtin_fmaf(bf16_low(w[i]), x[2 * i], s);
+        s = __builtin_fmaf(bf16_high(w[i]), x[2 * i + 1], s);
+    }
+    return s;
+}
+
 // A group's raw bytes as a kernel holds them between load and use.
 template <uint32_t F>
 struct Raw;
+
+template <>
+struct Raw<kF32> {
+    uint32_t w[32];
+    __device__ __forceinline__ void load(const uint8_t* piece, uint64_t, uint64_t gi) {
+        const uint4* c = reinterpret_cast<const uint4*>(piece + 128 * gi);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            const uint4 q = c[v];
+            w[4 * v] = q.x;
+            w[4 * v + 1] = q.y;
+            w[4 * v + 2] = q.z;
+            w[4 * v + 3] = q.w;
+        }
+    }
+    __device__ __forceinline__ float chain(const float* x, float s) const { return chain_f32(w, x, s); }
+};
+
+// F16 and BF16: 64 bytes a group.
+template <uint32_t F>
+struct RawHalves {
+    uint32_t w[16];
+    __device__ __forceinline__ void load(const uint8_t* piece, uint64_t, uint64_t gi) {
+        const uint4* c = reinterpret_cast<const uint4*>(piece + 64 * gi);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint4 q = c[v];
+            w[4 * v] = q.x;
+            w[4 * v + 1] = q.y;
+            w[4 * v + 2] = q.z;
+            w[4 * v + 3] = q.w;
+        }
+    }
+    __device__ __forceinline__ float chain(const float* x, float s) const {
+        return F == kF16 ? chain_f16(w, x, s) : chain_bf16(w, x, s);
+    }
+};
+
+template <>
+struct Raw<kF16> : RawHalves<kF16> {};
+template <>
+struct Raw<kBF16> : RawHalves<kBF16> {};
+
+// Dwords a group holds in registers between load and use.
+template <uint32_t F>
+constexpr int raw_dwords() {
+    return F == kF32 ? 32 : F == kF16 || F == kBF16 ? 16 : F == kQ8_0 ? 9 : F == kQ6_K ? 8 : 5;
+}
 
 template <>
 struct Raw<kQ4_0> {

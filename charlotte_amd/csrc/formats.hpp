@@ -16,7 +16,11 @@
 //         d, m    [16n, 20n)    fp16 d then fp16 m, one dword a block
 //   Q8_0  codes   [0, 32n)      32 int8 a block, weight j at byte j
 //         scales  [32n, 34n)    fp16 d a block
-//   F32   floats  [0, 4n)       a "block" is one weight (the gather's tables)
+//   F32   floats  [0, 4n)       a "block" is one weight
+//   F16   halves  [0, 2n)       a "block" is one binary16 weight
+//   BF16  values  [0, 2n)       a "block" is one bfloat16 weight: an f32's top half
+// F32, F16 and BF16 group gi is values 32gi .. 32gi + 31 (f32.wgsl, f16.wgsl,
+// bf16.wgsl); each decodes to its exact f32 with no arithmetic to round.
 // Groups are counted flat over the piece — group gi is row gi / G's group
 // gi % G — so a Q6_K row need not be whole super-blocks (q6_k.wgsl:13-42).
 //
@@ -34,21 +38,34 @@
 
 namespace chm {
 
-enum Format : uint32_t { kF32 = 0, kQ4_0 = 2, kQ4_1 = 3, kQ8_0 = 8, kQ6_K = 14 };
+enum Format : uint32_t { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ4_1 = 3, kQ8_0 = 8, kQ6_K = 14, kBF16 = 30 };
 
 // Bytes a stored block, and weights a block (src/core/gguf/types.h:65-101).
 constexpr uint32_t block_bytes(uint32_t f) {
-    return f == kF32 ? 4u : f == kQ4_0 ? 18u : f == kQ4_1 ? 20u : f == kQ8_0 ? 34u : f == kQ6_K ? 210u : 0u;
+    return f == kF32 ? 4u
+           : f == kF16 || f == kBF16 ? 2u
+           : f == kQ4_0 ? 18u
+           : f == kQ4_1 ? 20u
+           : f == kQ8_0 ? 34u
+           : f == kQ6_K ? 210u
+                        : 0u;
 }
 constexpr uint32_t block_weights(uint32_t f) {
-    return f == kF32 ? 1u : f == kQ4_0 || f == kQ4_1 || f == kQ8_0 ? 32u : f == kQ6_K ? 256u : 0u;
+    return f == kF32 || f == kF16 || f == kBF16 ? 1u : f == kQ4_0 || f == kQ4_1 || f == kQ8_0 ? 32u : f == kQ6_K ? 256u : 0u;
 }
+// The unquantized formats: a group is its 32 values as stored, 128 or 64 bytes.
+constexpr bool plain_values(uint32_t f) { return f == kF32 || f == kF16 || f == kBF16; }
 
 // binary16 bits -> binary32, exact for every finite input, subnormals
 // included (the f16 denormal mode is left at its IEEE default).
 __device__ __forceinline__ float half_to_float(uint32_t bits) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
 }
+
+// bfloat16 -> binary32: the value's 16 bits are the top of the f32 (the low
+// half of a dword shifted up, the high half masked), exact.
+__device__ __forceinline__ float bf16_low(uint32_t word) { return __uint_as_float(word << 16); }
+__device__ __forceinline__ float bf16_high(uint32_t word) { return __uint_as_float(word & 0xFFFF0000u); }
 
 // The 16 code bytes and scale of Q4_0 group gi, and the group's data of Q6_K.
 struct Q4_0Group {
@@ -183,6 +200,34 @@ __device__ __forceinline__ Q8_0Group load_q8_0(const uint8_t* piece, uint64_t n,
     return group_of(fetch_q8_0(piece, n, gi));
 }
 
+// Half h of an unquantized group — values 16h .. 16h + 15 — as the prefill
+// tile stages it: F32 four float4s, F16 and BF16 two dwords' worth of uint4.
+template <uint32_t F>
+struct ValuesHalf {
+    uint4 v[F == kF32 ? 4 : 2];
+};
+
+template <uint32_t F>
+__device__ __forceinline__ ValuesHalf<F> fetch_values_half(const uint8_t* piece, uint64_t gi, uint32_t h) {
+    constexpr uint32_t group_bytes = F == kF32 ? 128u : 64u;
+    const uint4* at = reinterpret_cast<const uint4*>(piece + group_bytes * gi + group_bytes / 2 * h);
+    ValuesHalf<F> out;
+#pragma unroll
+    for (int i = 0; i < (F == kF32 ? 4 : 2); ++i) out.v[i] = at[i];
+    return out;
+}
+
+// Value j (0..15) of a fetched half, exact.
+template <uint32_t F>
+__device__ __forceinline__ float value(const ValuesHalf<F>& h, int j) {
+    const uint4 q = h.v[F == kF32 ? j >> 2 : j >> 3];
+    const int word = F == kF32 ? j & 3 : (j >> 1) & 3;
+    const uint32_t w = word == 0 ? q.x : word == 1 ? q.y : word == 2 ? q.z : q.w;
+    if constexpr (F == kF32) return __uint_as_float(w);
+    else if constexpr (F == kF16) return half_to_float((j & 1) ? w >> 16 : w & 0xFFFFu);
+    else return (j & 1) ? bf16_high(w) : bf16_low(w);
+}
+
 // Weight l (0..31) of a group, exact.
 __device__ __forceinline__ float weight(const Q4_0Group& g, int l) {
     const uint32_t q = (g.w[(l & 15) >> 2] >> (8 * (l & 3) + 4 * (l >> 4))) & 0xFu;
@@ -252,6 +297,18 @@ __device__ __forceinline__ void unpack(const uint8_t* piece, uint64_t n, uint64_
             out[4 * v + 1] = q.y;
             out[4 * v + 2] = q.z;
             out[4 * v + 3] = q.w;
+        }
+    } else if constexpr (F == kF16 || F == kBF16) {
+        const uint4* h = reinterpret_cast<const uint4*>(piece + 64 * gi);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint4 q = h[v];
+            const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                out[8 * v + 2 * i] = F == kF16 ? half_to_float(w[i] & 0xFFFFu) : bf16_low(w[i]);
+                out[8 * v + 2 * i + 1] = F == kF16 ? half_to_float(w[i] >> 16) : bf16_high(w[i]);
+            }
         }
     } else {
         const Q6_KGroup g = load_q6_k(piece, n, gi);

@@ -26,6 +26,13 @@ template <uint32_t F>
 __device__ __forceinline__ float4 unpack4(const uint8_t* piece, uint64_t n, uint64_t gi, uint32_t v) {
     if constexpr (F == kF32) {
         return *reinterpret_cast<const float4*>(piece + 128 * gi + 16 * v);
+    } else if constexpr (F == kF16 || F == kBF16) {
+        const uint2 h = *reinterpret_cast<const uint2*>(piece + 64 * gi + 8 * v);
+        if constexpr (F == kF16)
+            return {half_to_float(h.x & 0xFFFFu), half_to_float(h.x >> 16), half_to_float(h.y & 0xFFFFu),
+                    half_to_float(h.y >> 16)};
+        else
+            return {bf16_low(h.x), bf16_high(h.x), bf16_low(h.y), bf16_high(h.y)};
     } else if constexpr (F == kQ8_0) {
         const uint32_t c = *reinterpret_cast<const uint32_t*>(piece + 32 * gi + 4 * v);
         const float d = half_to_float(*reinterpret_cast<const uint16_t*>(piece + 32 * n + 2 * gi));
@@ -111,6 +118,8 @@ hipError_t launch_gather(const Gather& g, uint32_t format, hipStream_t stream) {
     const dim3 grid = grid_of(g);
     switch (format) {
         case kF32: hipLaunchKernelGGL(gather_rows<kF32>, grid, dim3(256), 0, stream, g); break;
+        case kF16: hipLaunchKernelGGL(gather_rows<kF16>, grid, dim3(256), 0, stream, g); break;
+        case kBF16: hipLaunchKernelGGL(gather_rows<kBF16>, grid, dim3(256), 0, stream, g); break;
         case kQ4_0: hipLaunchKernelGGL(gather_rows<kQ4_0>, grid, dim3(256), 0, stream, g); break;
         case kQ4_1: hipLaunchKernelGGL(gather_rows<kQ4_1>, grid, dim3(256), 0, stream, g); break;
         case kQ8_0: hipLaunchKernelGGL(gather_rows<kQ8_0>, grid, dim3(256), 0, stream, g); break;

@@ -17,6 +17,7 @@
 // ranges only, each range sum written to `range_sums` range first,
 // [32][tokens][rows]; the combine adds a row's 32 sums in order from zero.
 // Range sums are the same bits either way, so split and tiled outputs agree.
+#include "plan.hpp"
 #include "product.hpp"
 
 namespace chm {
@@ -29,11 +30,14 @@ __device__ __forceinline__ uint64_t range_sum_at(const Product& a, uint32_t r, u
 }
 
 // A group's bytes as loaded; group_of() makes the group weight() decodes.
+// The unquantized formats load only the half (`half`, 16 values) the lane
+// stages: their values are their bytes, 64 or 32 of them a half.
 template <uint32_t F>
-__device__ __forceinline__ auto fetch_group(const uint8_t* piece, uint64_t n, uint64_t gi) {
+__device__ __forceinline__ auto fetch_group(const uint8_t* piece, uint64_t n, uint64_t gi, uint32_t half) {
     if constexpr (F == kQ4_0) return fetch_q4_0(piece, n, gi);
     else if constexpr (F == kQ4_1) return fetch_q4_1(piece, n, gi);
     else if constexpr (F == kQ8_0) return fetch_q8_0(piece, n, gi);
+    else if constexpr (plain_values(F)) return fetch_values_half<F>(piece, gi, half);
     else return fetch_q6_k(piece, n, gi);
 }
 
@@ -86,10 +90,11 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
     // staged into the other, one barrier a group. Group g + 2's stored bytes
     // and inputs are loaded into registers behind that barrier, so their round
     // trip overlaps group g + 1's arithmetic.
-    decltype(fetch_group<F>(nullptr, 0, 0)) staged{};
+    decltype(fetch_group<F>(nullptr, 0, 0, 0)) staged{};
     float4 xnext[XPer / 4];
     auto fetch = [&](uint32_t g) {
-        if (slive) staged = fetch_group<F>(spiece.piece, spiece.blocks, static_cast<uint64_t>(spiece.row) * G + g);
+        if (slive)
+            staged = fetch_group<F>(spiece.piece, spiece.blocks, static_cast<uint64_t>(spiece.row) * G + g, shalf);
         if (xlive) {
             const float4* src = reinterpret_cast<const float4*>(xsrc + g * 32);
 #pragma unroll
@@ -99,10 +104,28 @@ __global__ __launch_bounds__(256) void gemm_canonical(Product a, uint32_t token_
     auto stage = [&](int b) {
         float* wflat = reinterpret_cast<float*>(Ws[b]);
         float* xflat = reinterpret_cast<float*>(Xs[b]);
-        const auto grp = group_of(staged);
+        if constexpr (plain_values(F)) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
-            wflat[(16 * shalf + j) * kRowsATile + srow] = slive ? weight(grp, 16 * shalf + j) : 0.0f;
+            for (int j = 0; j < 16; ++j)
+                wflat[(16 * shalf + j) * kRowsATile + srow] = slive ? value<F>(staged, j) : 0.0f;
+        } else if constexpr (F == kQ8_0) {
+            // The lane's half of the codes chosen by a select, so every index
+            // below is a constant (an index by shalf would go through scratch).
+            const auto grp = group_of(staged);
+            uint32_t hw[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) hw[k] = shalf ? grp.w[4 + k] : grp.w[k];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int32_t q = static_cast<int8_t>((hw[j >> 2] >> (8 * (j & 3))) & 0xFFu);
+                wflat[(16 * shalf + j) * kRowsATile + srow] = slive ? static_cast<float>(q) * grp.d : 0.0f;
+            }
+        } else {
+            const auto grp = group_of(staged);
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                wflat[(16 * shalf + j) * kRowsATile + srow] = slive ? weight(grp, 16 * shalf + j) : 0.0f;
+        }
 #pragma unroll
         for (int v = 0; v < XPer / 4; ++v) {
             const float4 q = xlive ? clamp_input(a, xnext[v]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -214,58 +237,69 @@ __global__ __launch_bounds__(256) void combine_ranges(Product a, const float* ra
 }
 
 template <uint32_t F, int BM>
-static void go(const Product& a, uint32_t token_tiles, uint32_t row_tiles, uint32_t chunks, float* range_sums,
-               hipStream_t stream) {
-    const dim3 grid(token_tiles * row_tiles * chunks);
+static void go(const Product& a, const Plan& plan, float* range_sums, hipStream_t stream) {
+    const dim3 grid(plan.token_tiles * plan.row_tiles * plan.chunks);
     if (range_sums)
-        hipLaunchKernelGGL((gemm_canonical<F, BM, true, false>), grid, dim3(256), 0, stream, a, token_tiles, row_tiles,
-                           chunks, range_sums);
+        hipLaunchKernelGGL((gemm_canonical<F, BM, true, false>), grid, dim3(256), 0, stream, a, plan.token_tiles,
+                           plan.row_tiles, plan.chunks, range_sums);
     else if (plain_epilogue(a))
-        hipLaunchKernelGGL((gemm_canonical<F, BM, false, false>), grid, dim3(256), 0, stream, a, token_tiles, row_tiles,
-                           1u, nullptr);
+        hipLaunchKernelGGL((gemm_canonical<F, BM, false, false>), grid, dim3(256), 0, stream, a, plan.token_tiles,
+                           plan.row_tiles, 1u, nullptr);
     else
-        hipLaunchKernelGGL((gemm_canonical<F, BM, false, true>), grid, dim3(256), 0, stream, a, token_tiles, row_tiles,
-                           1u, nullptr);
+        hipLaunchKernelGGL((gemm_canonical<F, BM, false, true>), grid, dim3(256), 0, stream, a, plan.token_tiles,
+                           plan.row_tiles, 1u, nullptr);
 }
 
-// The tiled form; with `range_sums` (room for 32 x tokens x rows floats), the
-// split form and its combine, the ranges cut into as few chunks as still give
-// every CU two workgroups.
-hipError_t launch_gemm_canonical(const Product& a, uint32_t format, uint32_t compute_units, float* range_sums,
-                                 hipStream_t stream) {
+template <uint32_t F>
+static void go_format(const Product& a, const Plan& plan, float* range_sums, hipStream_t stream) {
+    if (plan.tile_tokens == 128)
+        go<F, 128>(a, plan, range_sums, stream);
+    else if (plan.tile_tokens == 32)
+        go<F, 32>(a, plan, range_sums, stream);
+    else
+        go<F, 64>(a, plan, range_sums, stream);
+}
+
+// The tile: 128 tokens where that still gives every CU two workgroups, 32
+// for a short step (no lanes on absent tokens), else 64. Split along K, the
+// ranges cut into as few chunks as still give every CU two workgroups.
+void plan_gemm_canonical(const Product& a, uint32_t compute_units, bool split, Plan* plan) {
+    *plan = Plan{};
     const uint32_t row_tiles = (a.rows + kRowsATile - 1) / kRowsATile;
-    const bool wide = ((a.tokens + 127) / 128) * row_tiles >= 2 * compute_units;
-    const bool narrow = a.tokens <= 32;  // a short step: no lanes on absent tokens
+    const bool wide = static_cast<uint64_t>((a.tokens + 127) / 128) * row_tiles >= 2ull * compute_units;
+    const bool narrow = a.tokens <= 32;
     const uint32_t bm = wide ? 128 : narrow ? 32 : 64;
     const uint32_t token_tiles = (a.tokens + bm - 1) / bm;
     uint32_t chunks = 1;
-    if (range_sums) {
+    if (split) {
         chunks = 2;
-        while (chunks < 32 && token_tiles * row_tiles * chunks < 2 * compute_units) chunks *= 2;
+        while (chunks < 32 && static_cast<uint64_t>(token_tiles) * row_tiles * chunks < 2ull * compute_units)
+            chunks *= 2;
     }
+    plan->kernel = split ? kGemmSplit : kGemmTiled;
+    plan->launches = split ? 2 : 1;
+    plan->tile_tokens = bm;
+    plan->tile_rows = kRowsATile;
+    plan->token_tiles = token_tiles;
+    plan->row_tiles = row_tiles;
+    plan->chunks = chunks;
+    plan->tiles = static_cast<uint64_t>(token_tiles) * row_tiles;
+    plan->workgroups = plan->tiles * chunks;
+}
+
+// The tiled form; with `range_sums` (room for 32 x tokens x rows floats), the
+// split form and its combine.
+hipError_t launch_gemm_canonical(const Product& a, uint32_t format, const Plan& plan, float* range_sums,
+                                 hipStream_t stream) {
     switch (format) {
-        case kQ4_0:
-            wide ? go<kQ4_0, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-                 : narrow ? go<kQ4_0, 32>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-                          : go<kQ4_0, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
-            break;
-        case kQ4_1:
-            wide ? go<kQ4_1, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-                 : narrow ? go<kQ4_1, 32>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-                          : go<kQ4_1, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
-            break;
-        case kQ8_0:
-            wide ? go<kQ8_0, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-                 : narrow ? go<kQ8_0, 32>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-                          : go<kQ8_0, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
-            break;
-        case kQ6_K:
-            wide ? go<kQ6_K, 128>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-                 : narrow ? go<kQ6_K, 32>(a, token_tiles, row_tiles, chunks, range_sums, stream)
-                          : go<kQ6_K, 64>(a, token_tiles, row_tiles, chunks, range_sums, stream);
-            break;
-        default:
-            return hipErrorInvalidValue;
+        case kQ4_0: go_format<kQ4_0>(a, plan, range_sums, stream); break;
+        case kQ4_1: go_format<kQ4_1>(a, plan, range_sums, stream); break;
+        case kQ8_0: go_format<kQ8_0>(a, plan, range_sums, stream); break;
+        case kQ6_K: go_format<kQ6_K>(a, plan, range_sums, stream); break;
+        case kF32: go_format<kF32>(a, plan, range_sums, stream); break;
+        case kF16: go_format<kF16>(a, plan, range_sums, stream); break;
+        case kBF16: go_format<kBF16>(a, plan, range_sums, stream); break;
+        default: return hipErrorInvalidValue;
     }
     if (range_sums) {
         const uint64_t outputs = static_cast<uint64_t>(a.tokens) * a.rows;

@@ -32,6 +32,7 @@
 #include <type_traits>
 
 #include "decode.hpp"
+#include "plan.hpp"
 #include "product.hpp"
 
 namespace chm {
@@ -478,48 +479,72 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma(Product a, const uint8_t* __
 }
 
 template <uint32_t F, int R, int T>
-static void go(const Product& a, const uint8_t* xp, const float* inv, hipStream_t stream) {
-    const uint32_t token_tiles = (a.tokens + T * 16 - 1) / (T * 16);
-    const uint32_t row_tiles = (a.rows + 64 * R - 1) / (64 * R);
+static void go(const Product& a, const Plan& plan, const uint8_t* xp, const float* inv, hipStream_t stream) {
     const uint32_t m = static_cast<uint32_t>(mfma_padded_tokens(a.tokens));
-    const dim3 grid(token_tiles * row_tiles);
+    const dim3 grid(plan.token_tiles * plan.row_tiles);
     if (plain_epilogue(a))
-        hipLaunchKernelGGL((gemm_mfma<F, R, T, false>), grid, dim3(256), 0, stream, a, xp, inv, token_tiles, m);
+        hipLaunchKernelGGL((gemm_mfma<F, R, T, false>), grid, dim3(256), 0, stream, a, xp, inv, plan.token_tiles, m);
     else
-        hipLaunchKernelGGL((gemm_mfma<F, R, T, true>), grid, dim3(256), 0, stream, a, xp, inv, token_tiles, m);
+        hipLaunchKernelGGL((gemm_mfma<F, R, T, true>), grid, dim3(256), 0, stream, a, xp, inv, plan.token_tiles, m);
 }
 
-// The widest wave tile that still gives every SIMD two waves, else the
-// smallest. Q6_K's 4 x 4 tile would not fit two waves' registers.
 template <uint32_t F>
-static void launch_format(const Product& a, const uint8_t* xp, const float* inv, uint32_t compute_units,
-                          hipStream_t stream) {
+static hipError_t launch_format(const Product& a, const Plan& plan, const uint8_t* xp, const float* inv,
+                                hipStream_t stream) {
+    if constexpr (F == kQ4_0) {
+        if (plan.wave_rows == 4 && plan.wave_tokens == 4) return go<F, 4, 4>(a, plan, xp, inv, stream), hipSuccess;
+    }
+    if (plan.wave_rows == 2 && plan.wave_tokens == 4) return go<F, 2, 4>(a, plan, xp, inv, stream), hipSuccess;
+    if (plan.wave_rows == 2 && plan.wave_tokens == 2) return go<F, 2, 2>(a, plan, xp, inv, stream), hipSuccess;
+    return hipErrorInvalidValue;
+}
+
+bool mfma_reads(uint32_t format) {
+    return format == kQ4_0 || format == kQ4_1 || format == kQ8_0 || format == kQ6_K;
+}
+
+// The widest wave tile (16-row blocks x 16-token blocks) that still gives
+// every SIMD two waves, else the smallest. Q6_K's 4 x 4 tile would not fit
+// two waves' registers.
+void plan_gemm_mfma(const Product& a, uint32_t format, uint32_t compute_units, Plan* plan) {
+    *plan = Plan{};
     const auto waves = [&](int r, int t) {
         return uint64_t{(a.tokens + 16u * t - 1) / (16u * t)} * ((a.rows + 16u * r - 1) / (16u * r));
     };
     const uint64_t want = uint64_t{compute_units} * 4 * kMfmaWavesASimd;
-    if constexpr (F == kQ4_0) {
-        if (waves(4, 4) >= want) return go<F, 4, 4>(a, xp, inv, stream);
-    }
-    if (waves(2, 4) >= want)
-        go<F, 2, 4>(a, xp, inv, stream);
-    else
-        go<F, 2, 2>(a, xp, inv, stream);
+    int r = 2, t = 2;
+    if (format == kQ4_0 && waves(4, 4) >= want)
+        r = 4, t = 4;
+    else if (waves(2, 4) >= want)
+        r = 2, t = 4;
+    plan->kernel = kGemmMfma;
+    plan->launches = 2;  // prepare_x, then the product
+    plan->canonical = false;
+    plan->wave_rows = r;
+    plan->wave_tokens = t;
+    plan->tile_tokens = 16 * t;
+    plan->tile_rows = 64 * r;
+    plan->token_tiles = (a.tokens + 16 * t - 1) / (16 * t);
+    plan->row_tiles = (a.rows + 64 * r - 1) / (64 * r);
+    plan->tiles = static_cast<uint64_t>(plan->token_tiles) * plan->row_tiles;
+    plan->workgroups = plan->tiles;
 }
 
-hipError_t launch_gemm_mfma(const Product& a, uint32_t format, uint32_t compute_units, void* workspace,
+hipError_t launch_gemm_mfma(const Product& a, uint32_t format, const Plan& plan, void* workspace,
                             hipStream_t stream) {
     const uint64_t m = mfma_padded_tokens(a.tokens);
     uint8_t* xp = static_cast<uint8_t*>(workspace);
     float* inv = reinterpret_cast<float*>(xp + m * a.groups * 128);
     hipLaunchKernelGGL(prepare_x, dim3(static_cast<uint32_t>(m)), dim3(256), 0, stream, a, xp, inv);
+    hipError_t e;
     switch (format) {
-        case kQ4_0: launch_format<kQ4_0>(a, xp, inv, compute_units, stream); break;
-        case kQ4_1: launch_format<kQ4_1>(a, xp, inv, compute_units, stream); break;
-        case kQ8_0: launch_format<kQ8_0>(a, xp, inv, compute_units, stream); break;
-        case kQ6_K: launch_format<kQ6_K>(a, xp, inv, compute_units, stream); break;
+        case kQ4_0: e = launch_format<kQ4_0>(a, plan, xp, inv, stream); break;
+        case kQ4_1: e = launch_format<kQ4_1>(a, plan, xp, inv, stream); break;
+        case kQ8_0: e = launch_format<kQ8_0>(a, plan, xp, inv, stream); break;
+        case kQ6_K: e = launch_format<kQ6_K>(a, plan, xp, inv, stream); break;
         default: return hipErrorInvalidValue;
     }
+    if (e != hipSuccess) return e;
     return hipGetLastError();
 }
 

@@ -22,14 +22,10 @@
 #include <algorithm>
 
 #include "decode.hpp"
+#include "plan.hpp"
 #include "product.hpp"
 
 namespace chm {
-
-bool gemv_stream_takes(const Product& a, uint32_t format);
-hipError_t launch_gemv_stream(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream);
-bool gemv_stream8_takes(const Product& a, uint32_t format);
-hipError_t launch_gemv_stream8(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream);
 
 // Workgroups a CU is asked to hold at once, as launch bounds: the L = 32
 // kernel's registers allow 4 waves a SIMD at SPAN <= 2 as it stands; the L = 4
@@ -41,6 +37,7 @@ constexpr int kWaves = 4;     // waves a workgroup
 constexpr int kPad = 33;      // a row's 32 range sums, padded
 constexpr int kWaveRows = 64; // rows a wave covers at most (steps * 64 / L)
 constexpr uint32_t kMaxStagedK = 8192;
+constexpr int kChunkGroups = 8;  // past kMaxStagedK: groups a range x is staged for at a time
 
 // The range sums a wave writes to LDS are read back by lanes of the same wave
 // only. A wave's LDS operations execute in order, so ordering the compiler's
@@ -68,8 +65,14 @@ __device__ __forceinline__ void finish_rows(const Product& a, uint32_t first, ui
 // chain from zero over them, and no other range; its range sum goes to LDS.
 // Rows a batch: B steps' loads are issued before any is decoded, so a wave
 // keeps B rows' bytes in flight rather than one; B never exceeds a wave's
-// steps, so every row loaded is decoded.
-constexpr int batch_of(int span) { return span >= 3 ? 2 : span == 2 ? 4 : 8; }
+// steps, so every row loaded is decoded. The unquantized formats hold 16 or
+// 32 dwords a group, so fewer rows a batch keep the registers in bounds.
+template <uint32_t F>
+constexpr int batch_of(int span) {
+    if constexpr (F == kF32) return span >= 2 ? 1 : 2;
+    if constexpr (F == kF16 || F == kBF16) return span >= 3 ? 1 : span == 2 ? 2 : 4;
+    return span >= 3 ? 2 : span == 2 ? 4 : 8;
+}
 
 template <uint32_t F, int SPAN, bool XREG, bool FULL, int B>
 __global__ __launch_bounds__(256, kRangesMinBlocks) void gemv_ranges(Product a, uint32_t steps, uint32_t tiles) {
@@ -433,51 +436,95 @@ __global__ __launch_bounds__(256, kQuartersMinBlocks) void gemv_quarters(Product
     }
 }
 
-// How a product's GEMV runs: lanes a row, the most groups a lane holds,
-// whether x's slice is held in registers, and the steps a wave takes.
-struct GemvPlan {
-    int lanes, span;
-    bool xreg;
-    uint32_t steps;
-};
-
-// K = 1,152 (G = 36) takes 4 lanes a row, 9 groups each; every other K of
-// whole 32-groups up to 8,192 takes the reference's 32, x in registers while
-// a lane's slice is at most 3 groups. Returns false for K past 8,192.
-bool gemv_plan(uint32_t rows, uint32_t groups, uint32_t compute_units, GemvPlan* plan) {
-    if (groups == 0 || groups * 32 > kMaxStagedK) return false;
-    if (groups == 36) {
-        *plan = {4, 9, false, 1};
-    } else {
-        const int span = static_cast<int>((groups + 31) / 32);
-        *plan = {32, span, span <= 3, 1};
-    }
-    const uint32_t rows_a_step = 64 / plan->lanes;
-    const uint32_t max_steps = kWaveRows / rows_a_step;
-    if (plan->lanes == 4) {
-        // Steps a wave: the most, up to max_steps, that still gives every CU
-        // about 8 waves.
-        const uint32_t steps = rows / (rows_a_step * compute_units * 8);
-        plan->steps = steps < 1 ? 1 : steps > max_steps ? max_steps : steps;
-        return true;
-    }
-    // L = 32: a power of two of steps a wave, the fewest that bring the grid
-    // down to one workgroup a CU — two for products of 2^20 groups or more.
-    // A small product is bound by its workgroups' dispatch and one memory
-    // round trip, so fewer workgroups with more rows each finish sooner
-    // (Q4_0 3,072 x 1,024: 384 workgroups 5.0 us, 192 4.3 us, 96 4.8 us);
-    // a large one needs the second workgroup's loads in flight.
-    const uint64_t per_cu = static_cast<uint64_t>(rows) * groups >= (1u << 20) ? 2 : 1;
-    const uint64_t target = per_cu * compute_units * kWaves * rows_a_step;
-    uint32_t steps = 1;
-    while (steps < max_steps && steps * target < rows) steps *= 2;
-    plan->steps = steps;
-    return true;
+// Past K = 8,192 (a range holds more than 8 groups): x is staged in LDS 8
+// groups a range at a time (32 KB, range-interleaved as gemv_ranges stages
+// it), and every row of the tile continues its chain over each chunk before
+// the next is staged. Lane r of a half-wave owns range r of its row; a wave
+// takes STEPS steps of two rows, so a lane holds STEPS chains across the
+// chunks. A chunk's groups are loaded NB at a time for every step before any
+// is decoded. Range sums meet in LDS and add in order, as in gemv_ranges.
+template <uint32_t F>
+constexpr int chunk_batch() {
+    return F == kF32 ? 1 : F == kF16 || F == kBF16 ? 2 : 4;
 }
 
-bool gemv_supports(uint32_t groups) {
-    GemvPlan plan;
-    return gemv_plan(1, groups, 1, &plan);
+template <uint32_t F, bool FULL, int STEPS>
+__global__ __launch_bounds__(256, 2) void gemv_chunked(Product a, uint32_t tiles) {
+    __shared__ float partials[kWaves][kWaveRows * kPad];
+    __shared__ float4 xs4[kChunkGroups * 256];
+    constexpr int NB = chunk_batch<F>();
+
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t half = lane >> 5, r = lane & 31u;
+    const uint32_t G = a.groups;
+    const uint32_t g0 = range_lo(r, G), g1 = range_lo(r + 1, G);
+    const uint32_t span = (G + 31) / 32;  // the most groups a range holds
+    const uint32_t token = a.last_token ? a.tokens - 1 : 0;
+    const float4* x4 = reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(token) * G * 32);
+    // Staging role: range sr, float4 sv of each of its groups.
+    const uint32_t sr = threadIdx.x & 31u, sv = threadIdx.x >> 5;
+    const uint32_t s0 = range_lo(sr, G), s1 = range_lo(sr + 1, G);
+    float* mine = partials[wave];
+
+    for (uint32_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+        const uint32_t wave_first = (tile * kWaves + wave) * STEPS * 2;
+        Piece rows[STEPS];
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) rows[st] = piece_of(a, min(wave_first + 2 * st + half, a.rows - 1));
+        float s[STEPS];
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) s[st] = 0.0f;
+        for (uint32_t i0 = 0; i0 < span; i0 += kChunkGroups) {
+            __syncthreads();  // every lane is done with the previous chunk
+            float4 xv[kChunkGroups];
+#pragma unroll
+            for (int k = 0; k < kChunkGroups; ++k) xv[k] = x4[min(s0 + i0 + k, G - 1) * 8 + sv];
+#pragma unroll
+            for (int k = 0; k < kChunkGroups; ++k)
+                xs4[256 * k + threadIdx.x] =
+                    s0 + i0 + k < s1 ? clamp_input(a, xv[k]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            __syncthreads();
+#pragma unroll
+            for (int k0 = 0; k0 < kChunkGroups; k0 += NB) {
+                Raw<F> raw[STEPS][NB];
+#pragma unroll
+                for (int st = 0; st < STEPS; ++st) {
+                    const uint64_t row0 = static_cast<uint64_t>(rows[st].row) * G;
+#pragma unroll
+                    for (int k = 0; k < NB; ++k)
+                        raw[st][k].load(rows[st].piece, rows[st].blocks, row0 + min(g0 + i0 + k0 + k, G - 1));
+                }
+#pragma unroll
+                for (int k = 0; k < NB; ++k) {
+                    if (g0 + i0 + k0 + k < g1) {
+                        float xg[32];
+                        const float4* src = xs4 + 256 * (k0 + k) + r;
+#pragma unroll
+                        for (int v = 0; v < 8; ++v) {
+                            const float4 q = src[32 * v];
+                            xg[4 * v] = q.x;
+                            xg[4 * v + 1] = q.y;
+                            xg[4 * v + 2] = q.z;
+                            xg[4 * v + 3] = q.w;
+                        }
+#pragma unroll
+                        for (int st = 0; st < STEPS; ++st) s[st] = raw[st][k].chain(xg, s[st]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) mine[(2 * st + half) * kPad + r] = s[st];  // an empty range's is zero
+        wave_sync();
+        float total = 0.0f;
+        if (lane < STEPS * 2 && wave_first + lane < a.rows) {
+            const float* sums = mine + lane * kPad;
+#pragma unroll
+            for (int q = 0; q < 32; ++q) total = total + sums[q];
+        }
+        finish_rows<FULL>(a, wave_first, STEPS * 2, total);
+        wave_sync();  // the sums are read before the next tile writes them
+    }
 }
 
 // Workgroups of `kernel` a CU holds at once with `lds` bytes of dynamic LDS.
@@ -501,27 +548,28 @@ static void launch_ranges(const Product& a, uint32_t steps, uint32_t tiles, size
 // A grid of at most the workgroups the GPU holds at once, each looping over
 // tiles, so no tail round runs part-empty.
 template <uint32_t F, int L, int SPAN, bool XREG, bool FULL>
-static void go_epilogue(const Product& a, uint32_t steps, uint32_t compute_units, hipStream_t stream) {
-    const uint32_t rows_a_tile = kWaves * steps * (64 / L);
-    const uint32_t tiles = (a.rows + rows_a_tile - 1) / rows_a_tile;
+static void go_epilogue(const Product& a, uint32_t steps, uint32_t tiles, uint32_t compute_units, hipStream_t stream) {
     // x staged: L = 32, SPAN float4 a thread (range-interleaved); L = 4, x in
     // order with a pad.
     const size_t lds = XREG ? 0
                        : L == 32 ? static_cast<size_t>(SPAN) * 256 * sizeof(float4)
                                  : (static_cast<size_t>(a.groups) * 32 + 16) * sizeof(float);
     if constexpr (L == 32) {
-        // Steps are a power of two: a batch is never more than a wave's steps,
-        // so no load is issued for a row the wave does not decode.
-        constexpr int most = batch_of(SPAN);
-        if (steps == 1) {
+        // Steps are a power of two, and so is the batch: the batch is the
+        // smaller, so no load is issued for a row the wave does not decode.
+        constexpr uint32_t most = batch_of<F>(SPAN);
+        const uint32_t b = std::min(steps, most);
+        if (b == 1) {
             launch_ranges<F, SPAN, XREG, FULL, 1>(a, steps, tiles, lds, compute_units, stream);
-        } else if (steps == 2 || most == 2) {
-            launch_ranges<F, SPAN, XREG, FULL, 2>(a, steps, tiles, lds, compute_units, stream);
-        } else if constexpr (most >= 4) {
-            if (steps == 4 || most == 4)
-                launch_ranges<F, SPAN, XREG, FULL, 4>(a, steps, tiles, lds, compute_units, stream);
-            else
-                launch_ranges<F, SPAN, XREG, FULL, most>(a, steps, tiles, lds, compute_units, stream);
+        } else if constexpr (most >= 2) {
+            if (b == 2) {
+                launch_ranges<F, SPAN, XREG, FULL, 2>(a, steps, tiles, lds, compute_units, stream);
+            } else if constexpr (most >= 4) {
+                if (b == 4)
+                    launch_ranges<F, SPAN, XREG, FULL, 4>(a, steps, tiles, lds, compute_units, stream);
+                else if constexpr (most >= 8)
+                    launch_ranges<F, SPAN, XREG, FULL, 8>(a, steps, tiles, lds, compute_units, stream);
+            }
         }
     } else {
         thread_local size_t cached_lds = ~size_t{0};
@@ -533,47 +581,158 @@ static void go_epilogue(const Product& a, uint32_t steps, uint32_t compute_units
 }
 
 template <uint32_t F, int L, int SPAN, bool XREG>
-static void go(const Product& a, uint32_t steps, uint32_t compute_units, hipStream_t stream) {
+static void go(const Product& a, uint32_t steps, uint32_t tiles, uint32_t compute_units, hipStream_t stream) {
     if (plain_epilogue(a))
-        go_epilogue<F, L, SPAN, XREG, false>(a, steps, compute_units, stream);
+        go_epilogue<F, L, SPAN, XREG, false>(a, steps, tiles, compute_units, stream);
     else
-        go_epilogue<F, L, SPAN, XREG, true>(a, steps, compute_units, stream);
+        go_epilogue<F, L, SPAN, XREG, true>(a, steps, tiles, compute_units, stream);
+}
+
+template <uint32_t F, int STEPS>
+static void go_chunked(const Product& a, uint32_t tiles, uint32_t compute_units, hipStream_t stream) {
+    const bool plain = plain_epilogue(a);
+    auto kernel = plain ? gemv_chunked<F, false, STEPS> : gemv_chunked<F, true, STEPS>;
+    thread_local uint32_t per_cu[2] = {0, 0};
+    if (per_cu[plain] == 0) per_cu[plain] = resident(kernel, 0);
+    const dim3 grid(std::min(tiles, per_cu[plain] * compute_units));
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, a, tiles);
 }
 
 template <uint32_t F>
-static hipError_t launch_format(const Product& a, const GemvPlan& plan, uint32_t cus, hipStream_t stream) {
-    if (plan.lanes == 4) {
-        go<F, 4, 9, false>(a, plan.steps, cus, stream);
-    } else {
-        switch (plan.span) {
-            case 1: go<F, 32, 1, true>(a, plan.steps, cus, stream); break;
-            case 2: go<F, 32, 2, true>(a, plan.steps, cus, stream); break;
-            case 3: go<F, 32, 3, true>(a, plan.steps, cus, stream); break;
-            case 4: go<F, 32, 4, false>(a, plan.steps, cus, stream); break;
-            case 5: case 6: go<F, 32, 6, false>(a, plan.steps, cus, stream); break;
-            case 7: case 8: go<F, 32, 8, false>(a, plan.steps, cus, stream); break;
+static hipError_t launch_format(const Product& a, const Plan& plan, uint32_t cus, hipStream_t stream) {
+    const uint32_t tiles = static_cast<uint32_t>(plan.tiles);
+    if (plan.kernel == kGemvChunked) {
+        switch (plan.steps) {
+            case 1: go_chunked<F, 1>(a, tiles, cus, stream); break;
+            case 2: go_chunked<F, 2>(a, tiles, cus, stream); break;
+            case 4: go_chunked<F, 4>(a, tiles, cus, stream); break;
             default: return hipErrorInvalidValue;
         }
+        return hipGetLastError();
+    }
+    if (plan.kernel == kGemvQuarters) {
+        if constexpr (!plain_values(F)) {
+            go<F, 4, 9, false>(a, plan.steps, tiles, cus, stream);
+            return hipGetLastError();
+        }
+        return hipErrorInvalidValue;
+    }
+    switch (plan.span) {
+        case 1: go<F, 32, 1, true>(a, plan.steps, tiles, cus, stream); break;
+        case 2: go<F, 32, 2, true>(a, plan.steps, tiles, cus, stream); break;
+        case 3:
+            if constexpr (F != kF32) go<F, 32, 3, true>(a, plan.steps, tiles, cus, stream);
+            else return hipErrorInvalidValue;
+            break;
+        default:
+            // x staged in LDS: the quantized formats only (the others take
+            // the chunked kernel past three groups a lane).
+            if constexpr (!plain_values(F)) {
+                if (plan.span == 4) go<F, 32, 4, false>(a, plan.steps, tiles, cus, stream);
+                else if (plan.span == 6) go<F, 32, 6, false>(a, plan.steps, tiles, cus, stream);
+                else if (plan.span == 8) go<F, 32, 8, false>(a, plan.steps, tiles, cus, stream);
+                else return hipErrorInvalidValue;
+            } else {
+                return hipErrorInvalidValue;
+            }
     }
     return hipGetLastError();
 }
 
-bool gemv_limbs_takes(const Product& a, uint32_t format) {
-    return gemv_stream_takes(a, format) || gemv_stream8_takes(a, format);
+// The decode's kernel and shape:
+//   - Q6_K at K = 1,152, 1,024 or 2,048 in whole steps: the LDS-streamed
+//     kernels (the INT8_LIMBS form there when asked);
+//   - quantized K = 1,152 otherwise: 4 lanes a row, 9 groups each;
+//   - other K up to 8,192: the reference's 32 lanes a row, x in registers
+//     while a lane's slice is at most 3 groups, else staged whole in LDS
+//     (a lane's 4, 6 or 8 groups: 5 and 7 take the next size's kernel);
+//   - past 8,192, F16 and BF16 past 3,072 and F32 past 2,048 (their groups
+//     are 64 or 128 bytes, too many registers for a lane's whole slice): x
+//     staged a chunk of 8 groups a range at a time.
+bool plan_gemv(const Product& a, uint32_t format, uint32_t compute_units, bool limbs, Plan* plan) {
+    *plan = Plan{};
+    plan->launches = 1;
+    plan->tile_tokens = 1;
+    const uint32_t G = a.groups;
+    if (G == 0 || a.rows == 0 || compute_units == 0) return false;
+    if (gemv_stream_takes(a, format) || gemv_stream8_takes(a, format)) {
+        const bool stream = G == 36;
+        const uint32_t step_rows = stream ? 16 : 64 / (G / 8);
+        plan->kernel = stream ? kGemvStream : kGemvStream8;
+        plan->limbs = limbs;
+        plan->canonical = !limbs;
+        plan->lanes = stream ? 4 : G / 8;
+        plan->span = stream ? 9 : 8;
+        plan->steps = 1;
+        plan->tile_rows = step_rows;
+        plan->tiles = a.rows / step_rows;
+        plan->workgroups = std::min<uint64_t>(2ull * compute_units, (plan->tiles + 3) / 4);
+        return true;
+    }
+    if (G * 32 > kMaxStagedK || (format == kF32 && G > 64) || (plain_values(format) && G > 96)) {
+        plan->kernel = kGemvChunked;
+        plan->lanes = 32;
+        plan->span = (G + 31) / 32;
+        // Steps a wave: the fewest (1, 2 or 4) that bring the grid down to
+        // two workgroups a CU.
+        uint32_t steps = 1;
+        while (steps < 4 && static_cast<uint64_t>(steps) * kWaves * 2 * 2 * compute_units < a.rows) steps *= 2;
+        plan->steps = steps;
+        plan->tile_rows = kWaves * 2 * steps;
+        plan->tiles = (a.rows + plan->tile_rows - 1) / plan->tile_rows;
+        plan->workgroups = std::min<uint64_t>(plan->tiles, 2ull * compute_units);
+        return true;
+    }
+    if (G == 36 && !plain_values(format)) {
+        plan->kernel = kGemvQuarters;
+        plan->lanes = 4;
+        plan->span = 9;
+    } else {
+        const uint32_t span = (G + 31) / 32;
+        plan->kernel = kGemvRanges;
+        plan->lanes = 32;
+        plan->span = span <= 4 ? span : span <= 6 ? 6 : 8;
+        plan->xreg = span <= 3;
+    }
+    const uint32_t rows_a_step = 64 / plan->lanes;
+    const uint32_t max_steps = kWaveRows / rows_a_step;
+    if (plan->lanes == 4) {
+        // Steps a wave: the most, up to max_steps, that still gives every CU
+        // about 8 waves.
+        const uint32_t steps = a.rows / (rows_a_step * compute_units * 8);
+        plan->steps = steps < 1 ? 1 : steps > max_steps ? max_steps : steps;
+    } else {
+        // L = 32: a power of two of steps a wave, the fewest that bring the
+        // grid down to one workgroup a CU — two for products of 2^20 groups
+        // or more. A small product is bound by its workgroups' dispatch and
+        // one memory round trip, so fewer workgroups with more rows each
+        // finish sooner (Q4_0 3,072 x 1,024: 384 workgroups 5.0 us, 192
+        // 4.3 us, 96 4.8 us); a large one needs the second workgroup's loads
+        // in flight.
+        const uint64_t per_cu = static_cast<uint64_t>(a.rows) * G >= (1u << 20) ? 2 : 1;
+        const uint64_t target = per_cu * compute_units * kWaves * rows_a_step;
+        uint32_t steps = 1;
+        while (steps < max_steps && steps * target < a.rows) steps *= 2;
+        plan->steps = steps;
+    }
+    plan->tile_rows = kWaves * plan->steps * rows_a_step;
+    plan->tiles = (a.rows + plan->tile_rows - 1) / plan->tile_rows;
+    plan->workgroups = plan->tiles;  // at most; the launch caps it at what the GPU holds
+    return true;
 }
 
-// `limbs`: the INT8_LIMBS path where it is built (the streamed kernels'
-// shapes); every other shape decodes in the canonical order.
-hipError_t launch_gemv(const Product& a, uint32_t format, uint32_t compute_units, bool limbs, hipStream_t stream) {
-    if (gemv_stream_takes(a, format)) return launch_gemv_stream(a, compute_units, limbs, stream);
-    if (gemv_stream8_takes(a, format)) return launch_gemv_stream8(a, compute_units, limbs, stream);
-    GemvPlan plan;
-    if (!gemv_plan(a.rows, a.groups, compute_units, &plan)) return hipErrorInvalidValue;
+hipError_t launch_gemv(const Product& a, uint32_t format, const Plan& plan, uint32_t compute_units,
+                       hipStream_t stream) {
+    if (plan.kernel == kGemvStream) return launch_gemv_stream(a, compute_units, plan.limbs, stream);
+    if (plan.kernel == kGemvStream8) return launch_gemv_stream8(a, compute_units, plan.limbs, stream);
     switch (format) {
         case kQ4_0: return launch_format<kQ4_0>(a, plan, compute_units, stream);
         case kQ4_1: return launch_format<kQ4_1>(a, plan, compute_units, stream);
         case kQ8_0: return launch_format<kQ8_0>(a, plan, compute_units, stream);
         case kQ6_K: return launch_format<kQ6_K>(a, plan, compute_units, stream);
+        case kF32: return launch_format<kF32>(a, plan, compute_units, stream);
+        case kF16: return launch_format<kF16>(a, plan, compute_units, stream);
+        case kBF16: return launch_format<kBF16>(a, plan, compute_units, stream);
         default: return hipErrorInvalidValue;
     }
 }

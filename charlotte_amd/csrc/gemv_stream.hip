@@ -30,6 +30,7 @@
 // moves. Not the canonical bits: within 1e-5 of them.
 #include <algorithm>
 
+#include "plan.hpp"
 #include "product.hpp"
 #include "stream.hpp"
 

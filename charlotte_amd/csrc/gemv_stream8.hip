@@ -20,6 +20,7 @@
 // the row's L sums added pairwise.
 #include <algorithm>
 
+#include "plan.hpp"
 #include "product.hpp"
 #include "stream.hpp"
 

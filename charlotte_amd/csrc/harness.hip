@@ -111,6 +111,12 @@ int chx_unpack(uint32_t type, const void* piece, uint64_t blocks_in_piece, uint6
         case chm::kF32:
             hipLaunchKernelGGL((unpack_kernel<chm::kF32>), grid, dim3(64), 0, stream, p, blocks_in_piece, groups, out);
             break;
+        case chm::kF16:
+            hipLaunchKernelGGL((unpack_kernel<chm::kF16>), grid, dim3(64), 0, stream, p, blocks_in_piece, groups, out);
+            break;
+        case chm::kBF16:
+            hipLaunchKernelGGL((unpack_kernel<chm::kBF16>), grid, dim3(64), 0, stream, p, blocks_in_piece, groups, out);
+            break;
         case chm::kQ4_0:
             hipLaunchKernelGGL((unpack_kernel<chm::kQ4_0>), grid, dim3(64), 0, stream, p, blocks_in_piece, groups, out);
             break;

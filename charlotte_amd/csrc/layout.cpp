@@ -4,7 +4,8 @@
 //
 // Q4_0: a piece is every block's 16 code bytes, then every block's fp16
 // scale; Q4_1 its 16 code bytes, then its d and m, a dword a block; Q8_0 its
-// 32 code bytes, then its fp16 scale; F32 the floats as stored. Q6_K: each super-block repacked so a 32-weight group's bits lie
+// 32 code bytes, then its fp16 scale; F32, F16 and BF16 the values as
+// stored (device_layout.h:118-120). Q6_K: each super-block repacked so a 32-weight group's bits lie
 // together — its low nibbles in 16 bytes (byte j: weight j's nibble, then
 // weight j + 16's), its high pairs in 8 (byte m: weights m, m + 8, m + 16,
 // m + 24 at bits 0, 2, 4, 6) — the piece being every block's lo, then hi, then
@@ -111,8 +112,8 @@ bool lay_out(uint32_t format, const uint8_t* stored, uint64_t blocks, uint8_t* d
         over_threads(blocks, [&](uint64_t b0, uint64_t b1) { split_range(stored, b0, b1, blocks, head, codes, device); });
         return true;
     }
-    if (format == 0) {
-        std::memcpy(device, stored, 4 * blocks);
+    if (format == 0 || format == 1 || format == 30) {
+        std::memcpy(device, stored, stored_bytes);
         return true;
     }
     if (format == 14) {

@@ -1,0 +1,69 @@
+// How a product runs — which kernel, its tile, its grid — chosen on the host
+// from the product's shape and the device's compute units alone, so a caller
+// can ask without a device (charlotte_hip_matmul_plan_launch) and a launch
+// runs exactly what its plan says. The role of the reference's pure launcher,
+// kernels::matmul_launches (src/core/kernels/matmul/matmul.h:661-673,
+// src/core/kernels/interface.h:29-34).
+#pragma once
+
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+namespace chm {
+
+struct Product;
+
+// Values are the C ABI's charlotte_hip_matmul_kernel.
+enum Kernel : uint32_t {
+    kNoKernel = 0,
+    kGemvRanges = 1,    // decode, 32 lanes a row, lane r range r (the reference's mapping)
+    kGemvQuarters = 2,  // decode, 4 lanes a row, 9 groups each (K = 1,152)
+    kGemvStream = 3,    // decode, LDS-streamed Q6_K, K = 1,152
+    kGemvStream8 = 4,   // decode, LDS-streamed Q6_K, K = 1,024 and 2,048
+    kGemvChunked = 5,   // decode past K = 8,192: x staged a chunk of groups at a time
+    kGemmTiled = 16,    // prefill, the VALU tile
+    kGemmSplit = 17,    // prefill split along K, then the ordered combine
+    kGemmMfma = 18,     // prefill on the matrix cores, x split into two f16 parts
+};
+
+struct Plan {
+    uint32_t kernel = kNoKernel;
+    uint32_t launches = 0;     // kernel launches the product issues
+    bool canonical = true;     // the reference's order of addition: bit-exact, batch-invariant
+    bool limbs = false;        // decode: the INT8_LIMBS form
+    bool xreg = false;         // decode (L = 32): x's slice held in registers
+    uint32_t lanes = 0;        // decode: lanes a row
+    uint32_t span = 0;         // decode: the most groups a lane holds
+    uint32_t steps = 0;        // decode: steps a wave
+    uint32_t tile_tokens = 0;  // prefill: tokens a workgroup's tile (decode: 1)
+    uint32_t tile_rows = 0;    // product rows a workgroup's tile
+    uint32_t token_tiles = 0, row_tiles = 0;
+    uint32_t chunks = 1;       // the split along K: workgroups a tile
+    uint32_t wave_rows = 0, wave_tokens = 0;  // matrix cores: 16-row and 16-token blocks a wave
+    uint64_t tiles = 0;        // the main kernel's tiles; persistent decode grids loop over them
+    uint64_t workgroups = 0;   // the main kernel's grid (persistent decode grids: at most this)
+};
+
+// Decode. False when the shape has no decode kernel.
+bool plan_gemv(const Product& a, uint32_t format, uint32_t compute_units, bool limbs, Plan* plan);
+hipError_t launch_gemv(const Product& a, uint32_t format, const Plan& plan, uint32_t compute_units,
+                       hipStream_t stream);
+bool gemv_stream_takes(const Product& a, uint32_t format);
+bool gemv_stream8_takes(const Product& a, uint32_t format);
+hipError_t launch_gemv_stream(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream);
+hipError_t launch_gemv_stream8(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream);
+
+// Prefill on the VALU tile; `split` for the split along K.
+void plan_gemm_canonical(const Product& a, uint32_t compute_units, bool split, Plan* plan);
+hipError_t launch_gemm_canonical(const Product& a, uint32_t format, const Plan& plan, float* range_sums,
+                                 hipStream_t stream);
+
+// Prefill on the matrix cores.
+bool mfma_reads(uint32_t format);
+uint64_t mfma_workspace_bytes(uint32_t tokens, uint32_t groups);
+void plan_gemm_mfma(const Product& a, uint32_t format, uint32_t compute_units, Plan* plan);
+hipError_t launch_gemm_mfma(const Product& a, uint32_t format, const Plan& plan, void* workspace,
+                            hipStream_t stream);
+
+}  // namespace chm

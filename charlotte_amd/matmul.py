@@ -38,16 +38,20 @@ class Status(enum.IntEnum):
 
 
 class TensorType(enum.IntEnum):
+    """The reference's format table (src/core/capability/capability.cpp:57-65)."""
+
     F32 = 0
+    F16 = 1
     Q4_0 = 2
     Q4_1 = 3
     Q8_0 = 8
     Q6_K = 14
+    BF16 = 30
 
 
 # Weights a block of each type (src/core/gguf/types.h:65-101).
-BLOCK_WEIGHTS = {TensorType.F32: 1, TensorType.Q4_0: 32, TensorType.Q4_1: 32, TensorType.Q8_0: 32,
-                 TensorType.Q6_K: 256}
+BLOCK_WEIGHTS = {TensorType.F32: 1, TensorType.F16: 1, TensorType.BF16: 1, TensorType.Q4_0: 32, TensorType.Q4_1: 32,
+                 TensorType.Q8_0: 32, TensorType.Q6_K: 256}
 
 
 class Epilogue(enum.IntEnum):
@@ -69,9 +73,26 @@ class Rows(enum.IntEnum):
 
 
 class GemmPath(enum.IntEnum):
+    """The prefill kernel: AUTO (the default) and CANONICAL run the bit-exact VALU
+    tile; SPLIT_F16_MFMA, only when asked for, the matrix cores within 1e-5."""
+
     AUTO = 0
     CANONICAL = 1
     SPLIT_F16_MFMA = 2
+
+
+class Kernel(enum.IntEnum):
+    """charlotte_hip_matmul_kernel: the kernel a launch's plan runs."""
+
+    NONE = 0
+    GEMV_RANGES = 1
+    GEMV_QUARTERS = 2
+    GEMV_STREAM = 3
+    GEMV_STREAM8 = 4
+    GEMV_CHUNKED = 5
+    GEMM_TILED = 16
+    GEMM_SPLIT = 17
+    GEMM_MFMA = 18
 
 
 class GemvPath(enum.IntEnum):
@@ -135,7 +156,20 @@ class _Desc(ctypes.Structure):
         ("clip", ctypes.c_void_p),
         ("bias", ctypes.c_void_p),
         ("activated", ctypes.c_uint32),
+        ("row_divisor", ctypes.c_uint32),
     ]
+
+
+class _Target(ctypes.Structure):
+    _fields_ = [("compute_units", ctypes.c_uint32), ("gemm_path", ctypes.c_uint32), ("gemv_path", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32), ("workspace_bytes", ctypes.c_uint64)]
+
+
+class _Plan(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_uint32), ("launches", ctypes.c_uint32), ("canonical", ctypes.c_uint32),
+                ("rows", ctypes.c_uint32), ("lanes_a_row", ctypes.c_uint32), ("groups_a_lane", ctypes.c_uint32),
+                ("steps_a_wave", ctypes.c_uint32), ("tile_tokens", ctypes.c_uint32), ("tile_rows", ctypes.c_uint32),
+                ("chunks", ctypes.c_uint32), ("tiles", ctypes.c_uint64), ("workgroups", ctypes.c_uint64)]
 
 
 class _GatherDesc(ctypes.Structure):
@@ -184,11 +218,18 @@ SIGNATURES = {
         _c.c_int,
         [_c.c_void_p, _c.c_uint32, _c.c_uint64, _c.c_uint64, _c.c_void_p, _c.c_uint64, _c.POINTER(_c.c_void_p)],
     ),
+    "charlotte_hip_matmul_weight_shape": (
+        _c.c_int, [_c.c_uint32, _c.c_uint64, _c.c_uint64, _c.POINTER(_c.c_void_p)]),
     "charlotte_hip_matmul_weight_free": (_c.c_int, [_c.c_void_p]),
     "charlotte_hip_matmul_weight_device": (_c.c_void_p, [_c.c_void_p]),
     "charlotte_hip_matmul_launch": (
         _c.c_int,
         [_c.c_void_p, _c.POINTER(_Desc), _Gate, _c.c_void_p, _c.c_uint64, _c.c_uint32, _c.c_void_p],
+    ),
+    "charlotte_hip_matmul_plan_launch": (
+        _c.c_int,
+        [_c.POINTER(_Desc), _c.POINTER(_Target), _Gate, _c.c_uint64, _c.c_uint32, _c.POINTER(_Plan), _c.c_char_p,
+         _c.c_uint64],
     ),
     "charlotte_hip_matmul_split_tokens": (_c.c_uint32, [_c.c_uint32, _c.c_uint64, _c.c_uint64, _Gate]),
     "charlotte_hip_matmul_range_sum_floats": (_c.c_uint64, [_c.c_uint32, _c.c_uint64, _c.c_uint64, _Gate]),
@@ -324,6 +365,17 @@ class Weight:
                                                            nbytes, ctypes.byref(h)))
         self.ctx, self.type, self.rows, self.columns, self.handle = ctx, TensorType(gguf_type), rows, columns, h
 
+    @classmethod
+    def shape(cls, gguf_type, rows, columns):
+        """A shape-only weight (no device memory), for plans: charlotte_hip_matmul_weight_shape."""
+        h = ctypes.c_void_p()
+        s = lib.charlotte_hip_matmul_weight_shape(int(gguf_type), rows, columns, ctypes.byref(h))
+        if s != 0:
+            raise MatmulError(s, f"weight shape {gguf_type} {rows}x{columns}")
+        w = cls.__new__(cls)
+        w.ctx, w.type, w.rows, w.columns, w.handle = None, TensorType(gguf_type), rows, columns, h
+        return w
+
     @property
     def device(self):
         return lib.charlotte_hip_matmul_weight_device(self.handle)
@@ -359,6 +411,7 @@ class MatmulLaunch:
     clip: int = 0
     bias: int = 0
     activated: bool = False
+    row_divisor: int = 1
     _desc: Optional[_Desc] = field(default=None, repr=False)
 
     def desc(self):
@@ -374,6 +427,7 @@ class MatmulLaunch:
         d.out_width = self.out_width
         d.gate_input, d.gate_input_stride, d.gate_input_column = self.gate_input, self.gate_input_stride, self.gate_input_column
         d.clip, d.bias, d.activated = self.clip, self.bias, int(self.activated)
+        d.row_divisor = self.row_divisor
         return d
 
 
@@ -384,6 +438,50 @@ def launch(ctx: Context, m: MatmulLaunch, tokens: int, gate: SplitGate = kNever,
         m._desc = m.desc()
     ctx.check(lib.charlotte_hip_matmul_launch(ctx.handle, ctypes.byref(m._desc), _gate(gate), range_sums,
                                               range_sums_bytes, tokens, stream))
+
+
+@dataclass(frozen=True)
+class Target:
+    """What a plan is made for: charlotte_hip_matmul_target."""
+
+    compute_units: int = 256
+    gemm_path: GemmPath = GemmPath.AUTO
+    gemv_path: GemvPath = GemvPath.CANONICAL
+    workspace_bytes: int = 0
+
+
+@dataclass(frozen=True)
+class Plan:
+    """charlotte_hip_matmul_plan: the kernel a launch runs and its shape."""
+
+    kernel: Kernel
+    launches: int
+    canonical: bool
+    rows: int
+    lanes_a_row: int
+    groups_a_lane: int
+    steps_a_wave: int
+    tile_tokens: int
+    tile_rows: int
+    chunks: int
+    tiles: int
+    workgroups: int
+
+
+def plan_launch(m: MatmulLaunch, tokens: int, target: Target = Target(), gate: SplitGate = kNever,
+                range_sums_bytes=0) -> Plan:
+    """The plan charlotte_hip_matmul_launch would follow, without a device (the
+    reference's pure kernels::matmul_launches, matmul.h:661-673). Raises
+    MatmulError with the launch's status and message where the launch would fail."""
+    t = _Target(target.compute_units, int(target.gemm_path), int(target.gemv_path), 0, target.workspace_bytes)
+    p = _Plan()
+    msg = ctypes.create_string_buffer(512)
+    s = lib.charlotte_hip_matmul_plan_launch(ctypes.byref(m.desc()), ctypes.byref(t), _gate(gate), range_sums_bytes,
+                                             tokens, ctypes.byref(p), msg, len(msg))
+    if s != 0:
+        raise MatmulError(s, msg.value.decode())
+    return Plan(Kernel(p.kernel), p.launches, bool(p.canonical), p.rows, p.lanes_a_row, p.groups_a_lane,
+                p.steps_a_wave, p.tile_tokens, p.tile_rows, p.chunks, p.tiles, p.workgroups)
 
 
 # ---- the embedding gather (src/core/kernels/gather/gather.h:126-145) ------------

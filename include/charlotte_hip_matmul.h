@@ -4,11 +4,11 @@
  *
  *   y[t][o] = sum_k W[o][k] * x[t][k]
  *
- * W stays in its GGUF format (Q4_0, Q4_1, Q8_0, or Q6_K repacked) in device
- * memory and is decoded in the kernels' load path; x and y are f32. One token
- * runs the decode form (a matrix-vector product bound by HBM), more tokens the
- * prefill form (a tiled matrix product). The embedding gather decodes table
- * rows through the same formats (and F32).
+ * W stays in its GGUF format (Q4_0, Q4_1, Q8_0, Q6_K repacked, or F32, F16,
+ * BF16 as stored) in device memory and is decoded in the kernels' load path;
+ * x and y are f32. One token runs the decode form (a matrix-vector product
+ * bound by HBM), more tokens the prefill form (a tiled matrix product). The
+ * embedding gather decodes table rows through the same formats.
  *
  * What each part replaces in the reference (paths relative to its root):
  *   charlotte_hip_matmul_desc       kernels::MatmulLaunch  src/core/kernels/matmul/matmul.h:602-632
@@ -18,6 +18,9 @@
  *   charlotte_hip_matmul_split_gate kernels::SplitGate     matmul.h:634-646
  *   charlotte_hip_matmul_launch     kernels::matmul_launches + Program::run
  *                                                          matmul.h:661-673, src/core/kernels/program.h:271-318
+ *   charlotte_hip_matmul_plan_launch kernels::matmul_launches alone: the launch's plan, pure, no
+ *                                   device               matmul.h:661-673, src/core/kernels/interface.h:29-34
+ *   charlotte_hip_matmul_desc.row_divisor  kernels::Launch::row_divisor  interface.h:270-279, 292
  *   charlotte_hip_matmul_split_tokens / _range_sum_floats  matmul.h:648-659, matmul.cpp:233-250
  *   charlotte_hip_matmul_weight_*   residency::WeightView/WeightPiece + PieceWriter
  *                                                          src/core/residency/weight_view.h:28-53,
@@ -42,7 +45,7 @@
  *
  * Order of addition (determinism, batch invariance): every path but the
  * matrix-core prefill and the INT8_LIMBS decode (both opt-in, within
- * tolerance; below) adds each output's products in the reference's one
+ * tolerance, never chosen by default; below) adds each output's products in the reference's one
  * order, fixed by K alone (matmul.h:34-50): a row's G = K / 32 groups cut into
  * 32 ranges, range r groups floor(rG/32) .. floor((r+1)G/32), each range an
  * fma chain from zero in k order, the 32 range sums added in order to a total
@@ -75,14 +78,18 @@ typedef enum {
     CHARLOTTE_HIP_MATMUL_IO_ERROR = 9           /* a file that cannot be opened or mapped */
 } charlotte_hip_matmul_status;
 
-/* GGUF tensor types the kernels read (src/core/gguf/types.h:39-47). The
- * products read the four quantized formats; F32 is a gather's table only. */
+/* GGUF tensor types the kernels read (src/core/gguf/types.h:39-47): the
+ * reference's format table, every row (src/core/capability/capability.cpp:57-65).
+ * The products and the gather read all seven; the matrix-core prefill the
+ * four quantized ones. */
 enum {
     CHARLOTTE_HIP_MATMUL_F32 = 0,
+    CHARLOTTE_HIP_MATMUL_F16 = 1,
     CHARLOTTE_HIP_MATMUL_Q4_0 = 2,
     CHARLOTTE_HIP_MATMUL_Q4_1 = 3,
     CHARLOTTE_HIP_MATMUL_Q8_0 = 8,
-    CHARLOTTE_HIP_MATMUL_Q6_K = 14
+    CHARLOTTE_HIP_MATMUL_Q6_K = 14,
+    CHARLOTTE_HIP_MATMUL_BF16 = 30
 };
 
 /* kernels::Epilogue (matmul.h:594-599). */
@@ -107,11 +114,14 @@ typedef enum {
 } charlotte_hip_matmul_rows;
 
 /* Which prefill kernel runs (no counterpart: the reference has one, on WebGPU's
- * shader cores). CANONICAL is the VALU tile in the order above, bit-exact and
- * batch-invariant; SPLIT_F16_MFMA runs the products on the matrix cores with
- * x split into two f16 parts, within the tolerance max|err| / max|y| <= 1e-5
- * but not bit-exact; AUTO takes the matrix cores where a shape is built for
- * them and the context has a workspace that holds the step (below). */
+ * shader cores). AUTO, the default, and CANONICAL run the VALU tile in the
+ * order above (split along K where the gate and the caller's range sums
+ * allow), bit-exact and batch-invariant: a drop-in caller keeps the
+ * reference's decode = prefill guarantee whatever workspace it sets.
+ * SPLIT_F16_MFMA, only when asked for, runs the products on the matrix cores
+ * with x split into two f16 parts, within the tolerance max|err| / max|y| <=
+ * 1e-5 but not bit-exact and not batch-invariant with decode; it needs a
+ * workspace (below) and reads the quantized formats only. */
 typedef enum {
     CHARLOTTE_HIP_MATMUL_GEMM_AUTO = 0,
     CHARLOTTE_HIP_MATMUL_GEMM_CANONICAL = 1,
@@ -154,8 +164,8 @@ charlotte_hip_matmul_status charlotte_hip_matmul_set_gemv_path(charlotte_hip_mat
  * binary16 parts, 4 bytes a weight column a token plus a scale a token,
  * tokens rounded up to 64. The caller allocates it and owns it; launches on
  * the context use it until it is set again (NULL, 0 unsets it), so steps that
- * use it must be ordered on one stream. AUTO takes the matrix cores only for
- * a step it holds. */
+ * use it must be ordered on one stream. Only SPLIT_F16_MFMA uses it; a step
+ * it does not hold is refused with INVALID_ARGUMENT. */
 charlotte_hip_matmul_status charlotte_hip_matmul_set_workspace(charlotte_hip_matmul_context* ctx, void* device,
                                                                uint64_t bytes);
 /* Bytes the workspace needs for a step of `tokens` tokens of K = `columns`;
@@ -197,6 +207,10 @@ charlotte_hip_matmul_status charlotte_hip_matmul_weight_wrap(charlotte_hip_matmu
                                                              uint32_t gguf_type, uint64_t rows, uint64_t columns,
                                                              const void* device_piece, uint64_t bytes,
                                                              charlotte_hip_matmul_weight** out);
+/* A weight of a shape and format with no device memory: a residency::WeightView
+ * before upload (weight_view.h:28-53), for plans only. A launch refuses it. */
+charlotte_hip_matmul_status charlotte_hip_matmul_weight_shape(uint32_t gguf_type, uint64_t rows, uint64_t columns,
+                                                              charlotte_hip_matmul_weight** out);
 charlotte_hip_matmul_status charlotte_hip_matmul_weight_free(charlotte_hip_matmul_weight* weight);
 /* The weight's piece on the device (its first stream's first byte). */
 const void* charlotte_hip_matmul_weight_device(const charlotte_hip_matmul_weight* weight);
@@ -239,6 +253,13 @@ typedef struct {
     const float* clip;
     const float* bias;
     uint32_t activated;
+    /* kernels::Launch::row_divisor (interface.h:270-279): the launch's rows
+     * are the step's tokens over this, rounded down (matmul.wgsl:87-91) — a
+     * vision encoder's projection after pooling, its patches over k². 0 and
+     * 1 both mean every token (a zero-initialised descriptor is undivided).
+     * Not with LAST_TOKEN (program.cpp:382-387). A step of fewer tokens than
+     * the divisor launches nothing. */
+    uint32_t row_divisor;
 } charlotte_hip_matmul_desc;
 
 /* kernels::SplitGate: the tiled prefill splits along K when its workgroups W
@@ -256,6 +277,60 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
                                                         const charlotte_hip_matmul_desc* desc,
                                                         charlotte_hip_matmul_split_gate gate, void* range_sums,
                                                         uint64_t range_sums_bytes, uint32_t tokens, void* stream);
+
+/* ---- the launch's plan, without a device ------------------------------------ */
+
+/* Which kernel a launch runs (plan.kernel). */
+typedef enum {
+    CHARLOTTE_HIP_MATMUL_KERNEL_NONE = 0,          /* nothing runs: a divided step of fewer tokens than the divisor */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMV_RANGES = 1,   /* decode, 32 lanes a row, lane r range r (matmul.wgsl:207-243) */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMV_QUARTERS = 2, /* decode, 4 lanes a row of 9 groups each (K = 1,152) */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMV_STREAM = 3,   /* decode, Q6_K at K = 1,152 streamed through LDS */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMV_STREAM8 = 4,  /* decode, Q6_K at K = 1,024 or 2,048 streamed through LDS */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMV_CHUNKED = 5,  /* decode past K = 8,192: x staged a chunk at a time */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_TILED = 16,   /* prefill, the VALU tile */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_SPLIT = 17,   /* prefill split along K, then the ordered combine */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_MFMA = 18     /* prefill on the matrix cores (x split into two f16 parts) */
+} charlotte_hip_matmul_kernel;
+
+/* What a plan is made for: the device's compute units (256 on MI355X) and
+ * the settings a context would hold. */
+typedef struct {
+    uint32_t compute_units;
+    uint32_t gemm_path;         /* charlotte_hip_matmul_gemm_path */
+    uint32_t gemv_path;         /* charlotte_hip_matmul_gemv_path */
+    uint32_t reserved;          /* 0 */
+    uint64_t workspace_bytes;   /* the matrix-core workspace set, 0 for none */
+} charlotte_hip_matmul_target;
+
+typedef struct {
+    uint32_t kernel;            /* charlotte_hip_matmul_kernel */
+    uint32_t launches;          /* kernel launches: 0, 1, or 2 (split + combine; matrix cores: x's split + product) */
+    uint32_t canonical;         /* nonzero: the reference's order of addition — bit-exact, batch-invariant */
+    uint32_t rows;              /* input and output rows of the launch: tokens / row_divisor, or 1 (LAST_TOKEN, decode) */
+    uint32_t lanes_a_row;       /* decode: lanes a product row */
+    uint32_t groups_a_lane;     /* decode: the most 32-weight groups a lane holds (the kernel's) */
+    uint32_t steps_a_wave;      /* decode: row steps a wave takes a tile */
+    uint32_t tile_tokens;       /* prefill: tokens a workgroup's tile (decode: 1) */
+    uint32_t tile_rows;         /* product rows a workgroup's tile */
+    uint32_t chunks;            /* the split along K: workgroups a tile (else 1) */
+    uint64_t tiles;             /* tiles of the main kernel */
+    uint64_t workgroups;        /* its grid; the persistent decode kernels run at most this, each looping over tiles */
+} charlotte_hip_matmul_plan;
+
+/* The plan charlotte_hip_matmul_launch would follow for `desc` over a step of
+ * `tokens`, with `range_sums_bytes` of range sums, on `target` — and the
+ * status it would return for the descriptor, before any device work: the
+ * same checks, in the same order. Pure: no device, no allocation; the
+ * members' weights may be shape-only (charlotte_hip_matmul_weight_shape) or
+ * uploaded. A failure writes its message into `message` (up to
+ * `message_bytes`, NUL-terminated) when given. */
+charlotte_hip_matmul_status charlotte_hip_matmul_plan_launch(const charlotte_hip_matmul_desc* desc,
+                                                             const charlotte_hip_matmul_target* target,
+                                                             charlotte_hip_matmul_split_gate gate,
+                                                             uint64_t range_sums_bytes, uint32_t tokens,
+                                                             charlotte_hip_matmul_plan* out, char* message,
+                                                             uint64_t message_bytes);
 
 /* matmul.h:648-659: the most tokens a step may hold for the product to split,
  * a whole number of 32-token tiles up to 512, or 1 when it never splits; and

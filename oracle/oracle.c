@@ -41,6 +41,17 @@ float orc_fp16_to_fp32(uint16_t h) {
 
 static uint16_t le16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
+/* bfloat16 -> binary32: the 16 bits are the top half of an f32, so the value
+ * is exact, sign of zero and subnormals as stored (ggml_bf16_to_fp32, as
+ * src/core/formats/bf16/bf16.h:16-25 and tests/gpu/unpack_bf16_test.cpp:21
+ * state it). */
+float orc_bf16_to_fp32(uint16_t h) {
+    const uint32_t bits = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
 /* ---- dequantization (file order) ---------------------------------------- */
 
 /* ggml's dequantize_row_q4_0 as tests/support/q4_0_reference.h:25-53 mirrors
@@ -126,6 +137,8 @@ void orc_dequantize_q8_0(const uint8_t* blocks, uint64_t nblocks, float* out) {
 static int block_shape(uint32_t type, uint64_t* elements, uint64_t* bytes) {
     switch (type) {
         case ORC_F32: *elements = 1; *bytes = 4; return 0;
+        case ORC_F16: *elements = 1; *bytes = 2; return 0;
+        case ORC_BF16: *elements = 1; *bytes = 2; return 0;
         case ORC_Q4_0: *elements = 32; *bytes = 18; return 0;
         case ORC_Q4_1: *elements = 32; *bytes = 20; return 0;
         case ORC_Q8_0: *elements = 32; *bytes = 34; return 0;
@@ -145,6 +158,14 @@ int orc_dequantize_range(uint32_t type, const uint8_t* blocks, uint64_t first, u
     const uint64_t n = b1 - b0 + 1;
     switch (type) {
         case ORC_F32: memcpy(tmp, at, (size_t)(n * 4)); break;
+        /* F16: quant::fp16_to_fp32 of each half (tests/gpu/unpack_f16_test.cpp:39);
+         * BF16: its top-half shift (unpack_bf16_test.cpp:21). */
+        case ORC_F16:
+            for (uint64_t i = 0; i < n; ++i) tmp[i] = orc_fp16_to_fp32(le16(at + 2 * i));
+            break;
+        case ORC_BF16:
+            for (uint64_t i = 0; i < n; ++i) tmp[i] = orc_bf16_to_fp32(le16(at + 2 * i));
+            break;
         case ORC_Q4_0: orc_dequantize_q4_0(at, n, tmp); break;
         /* tests/gpu/matmul_test.cpp:153 decodes Q4_1 by its rounded answer */
         case ORC_Q4_1: orc_dequantize_q4_1(at, n, tmp, NULL); break;
@@ -237,6 +258,11 @@ int orc_lay_out(uint32_t type, const uint8_t* blocks, uint64_t nblocks, uint8_t*
         memcpy(device, blocks, (size_t)(4 * nblocks));
         return 0;
     }
+    if (type == ORC_F16 || type == ORC_BF16) {
+        /* kF16 = kBF16 = {{0, 2}}: the values as stored (device_layout.h:119-120). */
+        memcpy(device, blocks, (size_t)(2 * nblocks));
+        return 0;
+    }
     return -1;
 }
 
@@ -292,6 +318,14 @@ int orc_unpack_group(uint32_t type, const uint8_t* device, uint64_t n, uint64_t 
     if (type == ORC_F32) {
         /* src/core/formats/f32/f32.wgsl:5-13: floats 32g .. 32g + 31. */
         memcpy(out, device + 128 * group, 128);
+        return 0;
+    }
+    if (type == ORC_F16 || type == ORC_BF16) {
+        /* src/core/formats/f16/f16.wgsl:6-13, bf16/bf16.wgsl:8-18: values
+         * 32g .. 32g + 31, two a word, the lower half first. */
+        const uint8_t* at = device + 64 * group;
+        for (int j = 0; j < 32; ++j)
+            out[j] = type == ORC_F16 ? orc_fp16_to_fp32(le16(at + 2 * j)) : orc_bf16_to_fp32(le16(at + 2 * j));
         return 0;
     }
     return -1;
@@ -355,7 +389,8 @@ static void* f32_rows(void* arg) {
 
 int orc_matmul_f32(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t columns, const float* x,
                    uint32_t tokens, float* y, uint32_t threads) {
-    if (columns % 32 != 0 || (type != ORC_Q4_0 && type != ORC_Q6_K && type != ORC_Q4_1 && type != ORC_Q8_0)) return -1;
+    uint64_t per_block, block_bytes;
+    if (columns % 32 != 0 || block_shape(type, &per_block, &block_bytes) != 0) return -1;
     if (threads < 1) threads = 1;
     if (threads > 256) threads = 256;
     struct f32_job jobs[256];

@@ -11,6 +11,14 @@
  *   orc_fp16_to_fp32        known answers of tests/quant_q4_0_test.cpp:41-65;
  *                           all 65,536 inputs against numpy's float16 and
  *                           against oracle/_ref (the reference's own code).
+ *   orc_bf16_to_fp32        every one of the 65,536 inputs against numpy's
+ *                           uint32 shift and against the edge list of
+ *                           tests/gpu/unpack_bf16_test.cpp:29-40.
+ *   orc_dequantize_range    F16 and BF16 over the edge-and-LCG values of
+ *   (F16, BF16)             tests/gpu/unpack_f16_test.cpp:24-35 and
+ *                           unpack_bf16_test.cpp:29-40 against numpy's
+ *                           float16 conversion and uint32 shift; F16 also
+ *                           against oracle/_ref's fp16_to_fp32.
  *   orc_dequantize_q4_0     known answers of tests/quant_q4_0_test.cpp:87-145;
  *                           closed form; oracle/_ref on the edge-scale blocks
  *                           of tests/gpu/unpack_q4_0_test.cpp:24-37.
@@ -62,9 +70,10 @@ extern "C" {
 #endif
 
 /* GGUF tensor types (src/core/gguf/types.h:41-43). */
-enum { ORC_F32 = 0, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q8_0 = 8, ORC_Q6_K = 14 };
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q8_0 = 8, ORC_Q6_K = 14, ORC_BF16 = 30 };
 
 float orc_fp16_to_fp32(uint16_t h);
+float orc_bf16_to_fp32(uint16_t h);
 
 /* File-order blocks -> f32 weights, flat. */
 void orc_dequantize_q4_0(const uint8_t* blocks, uint64_t nblocks, float* out);

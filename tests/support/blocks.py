@@ -9,6 +9,10 @@
   four apart, as m; then LCG d and m; LCG codes.
 - q8_0_edge_blocks: tests/gpu/unpack_q8_0_test.cpp:22-39 — the same d edges,
   codes -128 and 127 first in every block, LCG codes.
+- f16_edge_values / bf16_edge_values: tests/gpu/unpack_f16_test.cpp:24-35 and
+  unpack_bf16_test.cpp:29-40 — +-0, the smallest and largest subnormals, the
+  smallest normal, the largest finite of either sign, 1 (and -2 for BF16),
+  then LCG values, never inf or NaN.
 - lcg_bytes: tests/formats_q6_k_repack_test.cpp:44-49's stored bytes.
 - q4_0_block: tests/quant_q4_0_test.cpp:70-84's make_block.
 
@@ -198,3 +202,29 @@ def fma_f32(a, b, c):
 
 def add_f32(a, b):
     return round_f32(Fraction(float(a)) + Fraction(float(b)))
+
+
+F16_EDGES = [0x0000, 0x8000, 0x0001, 0x83FF, 0x0400, 0x7BFF, 0xFBFF, 0x3C00]
+BF16_EDGES = [0x0000, 0x8000, 0x0001, 0x807F, 0x0080, 0x7F7F, 0xFF7F, 0x3F80, 0xC000]
+
+
+def _half_values(count, seed, edges, exponent_mask):
+    lcg = Lcg(seed)
+    out = np.empty(count, np.uint16)
+    for i in range(count):
+        state = lcg.next()
+        h = edges[i] if i < len(edges) else state >> 16
+        if (h & exponent_mask) == exponent_mask:  # never infinity or NaN
+            h &= 0xBFFF
+        out[i] = h
+    return out
+
+
+def f16_edge_values(count):
+    """F16 values as stored (little-endian bytes), unpack_f16_test.cpp:24-35."""
+    return _half_values(count, 0x6C078965, F16_EDGES, 0x7C00).tobytes()
+
+
+def bf16_edge_values(count):
+    """BF16 values as stored (little-endian bytes), unpack_bf16_test.cpp:29-40."""
+    return _half_values(count, 0x2545F491, BF16_EDGES, 0x7F80).tobytes()

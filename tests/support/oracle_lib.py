@@ -13,8 +13,8 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 ORACLE_DIR = os.path.join(ROOT, "oracle")
 
-F32, Q4_0, Q4_1, Q8_0, Q6_K = 0, 2, 3, 8, 14
-BLOCK = {F32: (1, 4), Q4_0: (32, 18), Q4_1: (32, 20), Q8_0: (32, 34), Q6_K: (256, 210)}
+F32, F16, Q4_0, Q4_1, Q8_0, Q6_K, BF16 = 0, 1, 2, 3, 8, 14, 30
+BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20), Q8_0: (32, 34), Q6_K: (256, 210)}
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -38,6 +38,8 @@ class Oracle:
         lib = ctypes.CDLL(path)
         lib.orc_fp16_to_fp32.restype = ctypes.c_float
         lib.orc_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        lib.orc_bf16_to_fp32.restype = ctypes.c_float
+        lib.orc_bf16_to_fp32.argtypes = [ctypes.c_uint16]
         for f in (lib.orc_dequantize_q4_0, lib.orc_dequantize_q6_k, lib.orc_dequantize_q8_0):
             f.argtypes = [_u8p, ctypes.c_uint64, _f32p]
         lib.orc_dequantize_q4_1.argtypes = [_u8p, ctypes.c_uint64, _f32p, _f32p]
@@ -77,12 +79,18 @@ class Oracle:
     def fp16_to_fp32(self, h):
         return self.lib.orc_fp16_to_fp32(h)
 
+    def bf16_to_fp32(self, h):
+        return self.lib.orc_bf16_to_fp32(h)
+
     def dequantize(self, gtype, blocks):
         """File-order blocks -> weights (Q4_1: its rounded answer)."""
         b = _bytes(blocks)
         per, nbytes = BLOCK[gtype]
         n = b.size // nbytes
         out = np.empty(n * per, np.float32)
+        if gtype in (F16, BF16):
+            assert self.lib.orc_dequantize_range(gtype, _ptr(b, _u8p), 0, n, _ptr(out, _f32p)) == 0
+            return out
         if gtype == Q4_1:
             self.lib.orc_dequantize_q4_1(_ptr(b, _u8p), n, _ptr(out, _f32p), None)
             return out

@@ -83,7 +83,10 @@ def test_unpack_decodes_every_block_as_ggml_does(oracle, gtype, count):
 # ---- the fixture's products (matmul_test.cpp:217-267) ----------------------
 
 
-FIXTURE = ["w_q4_0", "w_q6_k", "w_set2", "w_set3", "w_set4", "qkv_q", "ffn_gate"]
+# Every weight of the reference's own product test (matmul_test.cpp:226-227),
+# w_f32 among them.
+FIXTURE = ["w_q4_0", "w_q6_k", "w_set2", "w_set3", "w_set4", "qkv_q", "ffn_gate", "w_f32", "w_q8_0", "w_q4_1_1152",
+           "w_q4_1_3072"]
 STEPS = [2, 8, 9, 16, 17, 33, 64]
 ALONE = [0, 1, 7, 8, 15, 16, 32, 63]
 
@@ -446,7 +449,7 @@ def test_weights_uploaded_from_a_gguf_file(oracle, run, source, fixture_tensors)
 
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "matmul_rows.gguf")
     with mm.GgufFile(path) as f:
-        for name in ("w_q4_0", "w_q6_k", "qkv_q", "ffn_gate", "w_q4_1_1152", "w_q8_0"):
+        for name in ("w_q4_0", "w_q6_k", "qkv_q", "ffn_gate", "w_q4_1_1152", "w_q8_0", "w_f32"):
             t = fixture_tensors[name]
             w = f.upload(run.ctx, name)
             x = _rows_of(source, t.columns, 9)
@@ -455,16 +458,3 @@ def test_weights_uploaded_from_a_gguf_file(oracle, run, source, fixture_tensors)
                 got = run.write(w, x, tokens)
                 assert bits_equal(got, want[:tokens]), f"{name} tokens={tokens}: {first_difference(got, want[:tokens])}"
             w.free()
-        # An F32 tensor uploads (a gather's table) but no product reads it.
-        w = f.upload(run.ctx, "w_f32")
-        x = _rows_of(source, 768, 1)
-        from charlotte_amd import harness as hx
-
-        xb, yb = hx.Buffer.of(x), hx.Buffer(4 * 40)
-        with pytest.raises(mm.MatmulError) as e:
-            mm.launch(run.ctx, mm.MatmulLaunch([mm.Member(w)], xb.ptr, [yb.ptr]), 1)
-        assert e.value.status == mm.Status.UNSUPPORTED_TYPE
-        hx.sync()
-        xb.free()
-        yb.free()
-        w.free()

@@ -14,7 +14,7 @@ import pytest
 
 from tests.support import blocks as B
 from tests.support import gguf_fixture
-from tests.support.oracle_lib import BLOCK, F32, Q4_0, Q4_1, Q6_K, Q8_0
+from tests.support.oracle_lib import BF16, BLOCK, F16, F32, Q4_0, Q4_1, Q6_K, Q8_0
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 EMBEDDINGS = {F32: "embedding_f32", Q4_0: "embedding_q4_0", Q4_1: "embedding_q4_1", Q8_0: "embedding_q8_0",
@@ -234,3 +234,97 @@ def test_positions_add_the_column_row_and_the_row_row(oracle):
     for r in range(13):
         want = table[r % grid] + table[positions + r // grid]
         assert (_bits(out[r]) == _bits(want)).all()
+
+
+# ---- F16 and BF16 (formats/f16/f16.wgsl, formats/bf16/bf16.wgsl) ------------------
+
+
+def test_bf16_every_input_is_its_top_half_shift(oracle):
+    """ggml_bf16_to_fp32 (unpack_bf16_test.cpp:21): the value's 16 bits are the
+    top of an f32, so every input, NaN payloads and -0 included, keeps its bits."""
+    every = np.arange(65536, dtype=np.uint16)
+    got = oracle.dequantize(BF16, every.tobytes())  # bits straight from C: NaN payloads kept
+    want = (every.astype(np.uint32) << 16).view(np.float32)
+    assert (_bits(got) == _bits(want)).all()
+    # The scalar entry point agrees on every non-NaN input (a float return
+    # through Python would quiet a signalling NaN).
+    finite = [h for h in range(0, 65536, 7) if (h & 0x7F80) != 0x7F80 or (h & 0x7F) == 0]
+    assert all(np.float32(oracle.bf16_to_fp32(h)) == want[h] for h in finite)
+    # Known answers: 1.0, -2.0, the largest finite, the smallest subnormal.
+    assert oracle.bf16_to_fp32(0x3F80) == 1.0 and oracle.bf16_to_fp32(0xC000) == -2.0
+    assert oracle.bf16_to_fp32(0x7F7F) == np.float32(3.3895313892515355e38)
+    assert oracle.bf16_to_fp32(0x0001) == np.float32(2.0**-133)
+
+
+@pytest.mark.parametrize("count", [32, 96, 33 * 32])
+def test_f16_values_decode_as_numpy_and_the_reference(oracle, reference, count):
+    stored = B.f16_edge_values(count)
+    h = np.frombuffer(stored, np.uint16)
+    assert list(h[: len(B.F16_EDGES)]) == B.F16_EDGES
+    assert not ((h & 0x7C00) == 0x7C00).any()
+    got = oracle.dequantize(F16, stored)
+    assert (_bits(got) == _bits(h.view(np.float16).astype(np.float32))).all()
+    theirs = np.array([reference.fp16_to_fp32(int(v)) for v in h], np.float32)
+    assert (_bits(got) == _bits(theirs)).all()
+
+
+@pytest.mark.parametrize("count", [32, 96, 33 * 32])
+def test_bf16_values_decode_as_the_shift(oracle, count):
+    stored = B.bf16_edge_values(count)
+    h = np.frombuffer(stored, np.uint16)
+    assert list(h[: len(B.BF16_EDGES)]) == B.BF16_EDGES
+    assert not ((h & 0x7F80) == 0x7F80).any()
+    got = oracle.dequantize(BF16, stored)
+    assert (_bits(got) == _bits((h.astype(np.uint32) << 16).view(np.float32))).all()
+    # -0 keeps its sign; the subnormals keep their value.
+    assert _bits(got)[1] == 0x80000000 and got[2] == np.float32(2.0**-133)
+
+
+@pytest.mark.parametrize("gtype,make", [(F16, B.f16_edge_values), (BF16, B.bf16_edge_values)])
+def test_half_layouts_are_the_values_as_stored(oracle, gtype, make):
+    """kF16 = kBF16 = {{0, 2}} (device_layout.h:119-120): one stream, the file's
+    bytes as they lie; group g is values 32g .. 32g + 31 (f16.wgsl:6-13)."""
+    count = 7 * 32
+    stored = make(count)
+    device = oracle.lay_out(gtype, stored)
+    assert device.size == 2 * count and device.tobytes() == stored
+    want = oracle.dequantize(gtype, stored)
+    for g in range(7):
+        assert (_bits(oracle.unpack_group(gtype, device, count, g)) == _bits(want[32 * g : 32 * g + 32])).all()
+
+
+def _canonical_rows(w, x, groups):
+    """The reference's order in exact binary32 arithmetic (fractions), per row."""
+    out = []
+    for row in w:
+        total = np.float32(0.0)
+        for r in range(32):
+            s = np.float32(0.0)
+            for k in range(32 * (r * groups // 32), 32 * ((r + 1) * groups // 32)):
+                s = B.fma_f32(row[k], x[k], s)
+            total = B.add_f32(total, s)
+        out.append(total)
+    return np.array(out, np.float32)
+
+
+@pytest.mark.parametrize("gtype", [F32, F16, BF16])
+def test_float_format_products_follow_the_reference_order(oracle, gtype):
+    """The F32, F16 and BF16 products (capability.cpp:57-65 composes every
+    format with the one matmul): the oracle's bits are the canonical order's,
+    computed independently in exact arithmetic, and within gamma(2K) of f64."""
+    rng = np.random.default_rng(gtype + 100)
+    rows, columns = 3, 96
+    w = rng.standard_normal((rows, columns)).astype(np.float32)
+    if gtype == F32:
+        stored = w.tobytes()
+    elif gtype == F16:
+        stored = w.astype(np.float16).tobytes()
+    else:
+        stored = (w.view(np.uint32) >> 16).astype(np.uint16).tobytes()
+    wd = oracle.dequantize(gtype, stored).reshape(rows, columns)
+    x = (rng.standard_normal((2, columns)) * 1e3).astype(np.float32)
+    y = oracle.matmul_f32(gtype, stored, rows, columns, x)
+    for t in range(2):
+        assert (_bits(y[t]) == _bits(_canonical_rows(wd, x[t], columns // 32))).all()
+    y64, bound = oracle.matmul_f64(gtype, stored, rows, columns, x)
+    assert (np.abs(y.astype(np.float64) - y64) <= bound).all()

@@ -1,0 +1,195 @@
+"""The launch's plan without a device (charlotte_hip_matmul_plan_launch): which
+kernel each shape runs, and the launch's checks, on the CPU.
+
+The reference's launcher is pure and tested without a GPU
+(src/core/kernels/interface.h:29-34; tests/kernels_matmul_test.cpp). Here the
+plan query runs the same checks as charlotte_hip_matmul_launch, in the same
+order, over shape-only weights: descriptors whose sums would wrap 32 or 64
+bits are refused before any kernel could read or write outside a weight or an
+output; each BASELINE shape gets the kernel the design names for it; AUTO
+stays on the bit-exact tile whatever workspace is set; a divided step
+(row_divisor, interface.h:270-279) plans its rows.
+"""
+
+import pytest
+
+from charlotte_amd import matmul as mm
+
+F32, F16, BF16 = mm.TensorType.F32, mm.TensorType.F16, mm.TensorType.BF16
+Q4_0, Q6_K, Q8_0 = mm.TensorType.Q4_0, mm.TensorType.Q6_K, mm.TensorType.Q8_0
+K = mm.Kernel
+X, Y0, Y1, Y2 = 0x10000, 0x20000, 0x30000, 0x40000  # aligned stand-ins: the plan never touches them
+MI355X = mm.Target(compute_units=256)
+
+
+@pytest.fixture
+def shapes():
+    made = []
+
+    def make(gtype, rows, columns):
+        w = mm.Weight.shape(gtype, rows, columns)
+        made.append(w)
+        return w
+
+    yield make
+    for w in made:
+        w.free()
+
+
+def _write(w, **kw):
+    return mm.MatmulLaunch([mm.Member(w)], X, [Y0], **kw)
+
+
+def _refused(m, tokens, status=mm.Status.INVALID_ARGUMENT, target=MI355X, **kw):
+    with pytest.raises(mm.MatmulError) as e:
+        mm.plan_launch(m, tokens, target, **kw)
+    assert e.value.status == status, str(e.value)
+    return str(e.value)
+
+
+# ---- descriptors that would wrap past a check ------------------------------------
+
+
+def test_member_row_offset_that_wraps_64_bits_is_refused(shapes):
+    w = shapes(Q4_0, 64, 1024)
+    # row_offset + rows = 2^64 - 1 + 1 wraps to 0 in 64 bits.
+    msg = _refused(mm.MatmulLaunch([mm.Member(w, row_offset=2**64 - 1, rows=1)], X, [Y0]), 1)
+    assert "rows past its weight" in msg
+    _refused(mm.MatmulLaunch([mm.Member(w, row_offset=64, rows=1)], X, [Y0]), 1)
+    _refused(mm.MatmulLaunch([mm.Member(w, row_offset=1, rows=64)], X, [Y0]), 33)
+    _refused(mm.MatmulLaunch([mm.Member(w, row_offset=2**63, rows=2**63)], X, [Y0]), 1)
+    # The last row alone is inside.
+    assert mm.plan_launch(mm.MatmulLaunch([mm.Member(w, row_offset=63, rows=1)], X, [Y0]), 1).kernel != K.NONE
+
+
+def test_output_rows_that_wrap_32_bits_are_refused(shapes):
+    w = shapes(Q4_0, 64, 1024)
+    # out_row + rows wraps in 32 bits: 2^32 - 1 + 2.
+    m = mm.MatmulLaunch([mm.Member(w, rows=2, output_row=2**32 - 1)], X, [Y0], out_width=2**32 - 1)
+    assert "output rows past out_width" in _refused(m, 1)
+    # output_row past 2^32 is refused before it could be narrowed.
+    m = mm.MatmulLaunch([mm.Member(w, rows=2, output_row=2**32)], X, [Y0], out_width=2**32 - 1)
+    assert "output_row" in _refused(m, 1)
+    m = mm.MatmulLaunch([mm.Member(w)], X, [Y0], out_width=2**32)
+    assert "out_width" in _refused(m, 1)
+    # Inside: the member's last output is out_width - 1.
+    m = mm.MatmulLaunch([mm.Member(w, output_row=100)], X, [Y0], out_width=164)
+    assert mm.plan_launch(m, 2).kernel == K.GEMM_TILED
+    _refused(mm.MatmulLaunch([mm.Member(w, output_row=101)], X, [Y0], out_width=164), 2)
+
+
+def test_descriptor_checks_match_the_launchs(shapes):
+    w, v = shapes(Q4_0, 64, 1024), shapes(Q4_0, 64, 2048)
+    _refused(mm.MatmulLaunch([mm.Member(w)], 0, [Y0]), 1)  # no input
+    _refused(mm.MatmulLaunch([mm.Member(w)], X + 4, [Y0]), 1)  # misaligned input
+    _refused(mm.MatmulLaunch([mm.Member(w)], X, [0]), 1)  # no output
+    _refused(mm.MatmulLaunch([mm.Member(w), mm.Member(v)], X, [Y0, Y1], epilogue=mm.Epilogue.QKV), 1)
+    _refused(_write(w), 0)
+    _refused(mm.MatmulLaunch([mm.Member(w)], X, [Y0], epilogue=mm.Epilogue.GatedActivation), 1)
+    _refused(mm.MatmulLaunch([mm.Member(w)], X, [Y0], epilogue=mm.Epilogue.QKV, bias=Y1), 1)
+    _refused(mm.MatmulLaunch([mm.Member(w)], X, [Y0], epilogue=mm.Epilogue.GatedByInput), 1)
+
+
+# ---- the kernel each shape runs --------------------------------------------------
+
+
+def test_c2_head_is_the_streamed_q6_k_decode(shapes):
+    p = mm.plan_launch(_write(shapes(Q6_K, 262144, 1152)), 1)
+    assert (p.kernel, p.lanes_a_row, p.groups_a_lane, p.canonical) == (K.GEMV_STREAM, 4, 9, True)
+    assert p.tiles == 262144 // 16 and p.workgroups == 2 * 256 and p.launches == 1 and p.rows == 1
+    limbs = mm.plan_launch(_write(shapes(Q6_K, 262144, 1152)), 1, mm.Target(256, gemv_path=mm.GemvPath.INT8_LIMBS))
+    assert limbs.kernel == K.GEMV_STREAM and not limbs.canonical
+
+
+@pytest.mark.parametrize("rows,columns", [(151936, 1024), (128256, 2048)])
+def test_qwen_and_llama_heads_are_the_streamed_decode_of_k_1024_and_2048(shapes, rows, columns):
+    p = mm.plan_launch(_write(shapes(Q6_K, rows, columns)), 1)
+    assert p.kernel == K.GEMV_STREAM8 and p.canonical and p.tile_rows == 64 // (columns // 256)
+
+
+def test_c1_is_the_reference_mapping_in_one_workgroup_a_cu(shapes):
+    p = mm.plan_launch(_write(shapes(Q4_0, 3072, 1024)), 1)
+    assert (p.kernel, p.lanes_a_row, p.groups_a_lane) == (K.GEMV_RANGES, 32, 1)
+    # Two steps a wave: 4 waves x 2 steps x 2 rows = 16 rows a workgroup, 192 of them.
+    assert (p.steps_a_wave, p.tile_rows, p.tiles) == (2, 16, 192)
+
+
+def test_k_1152_other_than_whole_streamed_steps_takes_four_lanes_a_row(shapes):
+    assert mm.plan_launch(_write(shapes(Q4_0, 1000, 1152)), 1).kernel == K.GEMV_QUARTERS
+    assert mm.plan_launch(_write(shapes(Q6_K, 1000, 1152)), 1).kernel == K.GEMV_QUARTERS
+
+
+@pytest.mark.parametrize("columns,span", [(3072, 3), (4096, 4), (5120, 6), (8192, 8)])
+def test_decode_up_to_k_8192_stages_x_whole(shapes, columns, span):
+    p = mm.plan_launch(_write(shapes(Q4_0, 2048, columns)), 1)
+    assert (p.kernel, p.groups_a_lane) == (K.GEMV_RANGES, span)
+
+
+@pytest.mark.parametrize("columns", [8192 + 32, 9728, 14336, 65536])
+def test_decode_past_k_8192_stages_x_in_chunks(shapes, columns):
+    p = mm.plan_launch(_write(shapes(Q4_0, 4096, columns)), 1)
+    assert p.kernel == K.GEMV_CHUNKED and p.canonical and p.groups_a_lane == (columns // 32 + 31) // 32
+
+
+@pytest.mark.parametrize("gtype,columns,kernel", [
+    (F32, 1024, K.GEMV_RANGES), (F32, 2048, K.GEMV_RANGES), (F32, 3072, K.GEMV_CHUNKED),
+    (F16, 3072, K.GEMV_RANGES), (F16, 4096, K.GEMV_CHUNKED), (BF16, 1152, K.GEMV_RANGES),
+    (BF16, 12288, K.GEMV_CHUNKED),
+])
+def test_float_formats_decode(shapes, gtype, columns, kernel):
+    assert mm.plan_launch(_write(shapes(gtype, 512, columns)), 1).kernel == kernel
+
+
+def test_last_token_decodes_whatever_the_step(shapes):
+    p = mm.plan_launch(_write(shapes(Q6_K, 151936, 1024), rows=mm.Rows.LastToken), 33)
+    assert p.kernel == K.GEMV_STREAM8 and p.rows == 1
+
+
+def test_c4_prefill_is_the_bit_exact_tile_under_auto_with_or_without_a_workspace(shapes):
+    w = shapes(Q4_0, 8192, 2048)
+    room = mm.workspace_bytes(512, 2048)
+    for target in (MI355X, mm.Target(256, workspace_bytes=room), mm.Target(256, mm.GemmPath.CANONICAL, workspace_bytes=room)):
+        p = mm.plan_launch(_write(w), 512, target)
+        assert (p.kernel, p.canonical, p.tile_tokens, p.tile_rows) == (K.GEMM_TILED, True, 64, 128), target
+        assert p.tiles == 8 * 64
+    mfma = mm.plan_launch(_write(w), 512, mm.Target(256, mm.GemmPath.SPLIT_F16_MFMA, workspace_bytes=room))
+    assert mfma.kernel == K.GEMM_MFMA and not mfma.canonical and mfma.launches == 2
+    assert "workspace" in _refused(_write(w), 512, target=mm.Target(256, mm.GemmPath.SPLIT_F16_MFMA, workspace_bytes=room - 1))
+
+
+def test_the_matrix_cores_refuse_the_float_formats(shapes):
+    w = shapes(F16, 256, 1024)
+    target = mm.Target(256, mm.GemmPath.SPLIT_F16_MFMA, workspace_bytes=1 << 30)
+    _refused(_write(w), 64, mm.Status.UNSUPPORTED, target=target)
+    assert mm.plan_launch(_write(w), 64).kernel == K.GEMM_TILED
+
+
+def test_short_steps_split_along_k_when_the_gate_and_range_sums_allow(shapes):
+    w = shapes(Q4_0, 8192, 2048)
+    sums = 4 * mm.range_sum_floats(mm.Epilogue.Write, 8192, 2048, mm.kAlways)
+    p = mm.plan_launch(_write(w), 32, gate=mm.kAlways, range_sums_bytes=sums)
+    assert (p.kernel, p.launches, p.canonical, p.tile_tokens) == (K.GEMM_SPLIT, 2, True, 32) and p.chunks >= 2
+    # Range sums too small for the step, no gate, options or a gated product: the tile.
+    assert mm.plan_launch(_write(w), 32, gate=mm.kAlways, range_sums_bytes=sums // 64).kernel == K.GEMM_TILED
+    assert mm.plan_launch(_write(w), 32, gate=mm.kNever, range_sums_bytes=sums).kernel == K.GEMM_TILED
+    assert mm.plan_launch(_write(w, bias=Y1), 32, gate=mm.kAlways, range_sums_bytes=sums).kernel == K.GEMM_TILED
+    g = mm.MatmulLaunch([mm.Member(w), mm.Member(w)], X, [Y0], epilogue=mm.Epilogue.GatedActivation)
+    assert mm.plan_launch(g, 32, gate=mm.kAlways, range_sums_bytes=2 * sums).kernel == K.GEMM_TILED
+
+
+# ---- row_divisor (interface.h:270-279, 292; program.cpp:382-387) -------------------
+
+
+def test_a_divided_step_plans_its_rows(shapes):
+    w = shapes(Q8_0, 200, 1024)
+    for pooled in (1, 2, 7):
+        divided = mm.plan_launch(_write(w, row_divisor=9), 9 * pooled)
+        plain = mm.plan_launch(_write(w), pooled)
+        assert divided == plain and divided.rows == pooled
+    # Rounded down, as the reference's step_rows (matmul.wgsl:87-91).
+    assert mm.plan_launch(_write(w, row_divisor=9), 20).rows == 2
+    nothing = mm.plan_launch(_write(w, row_divisor=9), 8)
+    assert (nothing.kernel, nothing.launches) == (K.NONE, 0)
+    # 0 is undivided (a zero-initialised descriptor); over the last token, refused.
+    assert mm.plan_launch(_write(w, row_divisor=0), 5).rows == 5
+    assert "row divisor" in _refused(_write(w, row_divisor=9, rows=mm.Rows.LastToken), 18)
