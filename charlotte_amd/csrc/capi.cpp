@@ -158,8 +158,8 @@ Verdict describe(const charlotte_hip_matmul_desc* desc, uint32_t tokens, const c
         const charlotte_hip_matmul_member& m = d.members[i];
         const std::string who = "member " + std::to_string(i);
         if (!m.weight) return bad(who + " has no weight");
-        if (ctx && m.weight->ctx != ctx) return bad(who + " of another context");
         if (ctx && !m.weight->piece) return bad(who + " is a shape-only weight");
+        if (ctx && m.weight->ctx != ctx) return bad(who + " of another context");
         if (m.weight->type != head->type || m.weight->columns != head->columns)
             return bad("members differ in format or width");
         if (m.rows == 0 || m.row_offset > m.weight->rows || m.rows > m.weight->rows - m.row_offset)

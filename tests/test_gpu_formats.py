@@ -444,9 +444,6 @@ def test_gather_refusals(run):
     table = run.weight(F32, t.rows, t.columns, t.data)
     s = _Step([1, 2], t.columns)
     with pytest.raises(mm.MatmulError) as e:
-        mm.launch(run.ctx, mm.MatmulLaunch([mm.Member(table)], s.hidden.ptr, [s.hidden.ptr]), 1)
-    assert e.value.status == mm.Status.UNSUPPORTED_TYPE
-    with pytest.raises(mm.MatmulError) as e:
         mm.gather(run.ctx, table, s.ids.ptr, 2, s.hidden.ptr + 4)
     assert e.value.status == mm.Status.INVALID_ARGUMENT and "aligned" in str(e.value)
     with pytest.raises(mm.MatmulError) as e:
