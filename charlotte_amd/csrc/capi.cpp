@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -20,9 +21,17 @@
 #include "plan.hpp"
 #include "product.hpp"
 
+// The allocation-free launch's range sums (charlotte_hip_matmul_launch_static):
+// one array a device, in the code object, held from the library's load on
+// that device until the process ends. Host code never uses this name as an
+// address: each device's copy is found with hipGetSymbolAddress (below) and
+// kept per device.
+static __device__ __align__(256) float scratch[CHARLOTTE_HIP_MATMUL_STATIC_SCRATCH_BYTES / sizeof(float)];
+
 struct charlotte_hip_matmul_context {
     int device = 0;
     uint32_t compute_units = 0;
+    float* scratch = nullptr;   // this device's copy of `scratch`
     charlotte_hip_matmul_gemm_path gemm_path = CHARLOTTE_HIP_MATMUL_GEMM_AUTO;
     charlotte_hip_matmul_gemv_path gemv_path = CHARLOTTE_HIP_MATMUL_GEMV_CANONICAL;
     void* workspace = nullptr;  // the matrix-core path's, the caller's memory
@@ -251,6 +260,29 @@ Verdict plan_product(const chm::Product& a, uint32_t format, const Target& t, ch
 
 extern "C" {
 
+// Device `device`'s address of `scratch`, found once (with the device
+// current) and kept; later contexts on the device reuse it.
+static hipError_t scratch_of(int device, float** out) {
+    constexpr int kDevices = 64;
+    static std::mutex lock;
+    static float* found[kDevices] = {};
+    if (device < 0 || device >= kDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> hold(lock);
+    if (!found[device]) {
+        int previous = 0;
+        if (hipError_t e = hipGetDevice(&previous); e != hipSuccess) return e;
+        if (hipError_t e = hipSetDevice(device); e != hipSuccess) return e;
+        void* at = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&at, HIP_SYMBOL(scratch));
+        (void)hipSetDevice(previous);
+        if (e != hipSuccess) return e;
+        if (!at) return hipErrorInvalidSymbol;
+        found[device] = static_cast<float*>(at);
+    }
+    *out = found[device];
+    return hipSuccess;
+}
+
 charlotte_hip_matmul_status charlotte_hip_matmul_context_create(int device, charlotte_hip_matmul_context** out) {
     if (!out) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
     *out = nullptr;
@@ -259,10 +291,13 @@ charlotte_hip_matmul_status charlotte_hip_matmul_context_create(int device, char
     if (device < 0 || device >= count) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) != hipSuccess) return CHARLOTTE_HIP_MATMUL_HIP_ERROR;
+    float* device_scratch = nullptr;
+    if (scratch_of(device, &device_scratch) != hipSuccess) return CHARLOTTE_HIP_MATMUL_HIP_ERROR;
     auto* ctx = new (std::nothrow) charlotte_hip_matmul_context;
     if (!ctx) return CHARLOTTE_HIP_MATMUL_OUT_OF_MEMORY;
     ctx->device = device;
     ctx->compute_units = static_cast<uint32_t>(prop.multiProcessorCount);
+    ctx->scratch = device_scratch;
     *out = ctx;
     return CHARLOTTE_HIP_MATMUL_OK;
 }
@@ -470,6 +505,28 @@ charlotte_hip_matmul_status charlotte_hip_matmul_plan_launch(const charlotte_hip
     return CHARLOTTE_HIP_MATMUL_OK;
 }
 
+// Runs a planned product on ctx's device; `range_sums` serves a split plan.
+// No allocation: every buffer is the caller's or the library's static one.
+static Status run_plan(charlotte_hip_matmul_context* ctx, const chm::Product& a, uint32_t format, const chm::Plan& plan,
+                       float* range_sums, void* stream) {
+    if (plan.kernel == chm::kNoKernel) return ok(ctx);
+    if (hipError_t e = hipSetDevice(ctx->device); e != hipSuccess) return hip_fail(ctx, e, "launch: hipSetDevice");
+    auto* s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    switch (plan.kernel) {
+        case chm::kGemmMfma: e = chm::launch_gemm_mfma(a, format, plan, ctx->workspace, s); break;
+        case chm::kGemmTiled: e = chm::launch_gemm_canonical(a, format, plan, nullptr, s); break;
+        case chm::kGemmSplit: e = chm::launch_gemm_canonical(a, format, plan, range_sums, s); break;
+        default: e = chm::launch_gemv(a, format, plan, ctx->compute_units, s); break;
+    }
+    if (e != hipSuccess) return hip_fail(ctx, e, "launch");
+    return ok(ctx);
+}
+
+static Target target_of(const charlotte_hip_matmul_context* ctx) {
+    return Target{ctx->compute_units, ctx->gemm_path, ctx->gemv_path, ctx->workspace ? ctx->workspace_bytes : 0};
+}
+
 charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_context* ctx,
                                                         const charlotte_hip_matmul_desc* desc,
                                                         charlotte_hip_matmul_split_gate gate, void* range_sums,
@@ -479,24 +536,35 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
     uint32_t format = 0;
     Verdict v = describe(desc, tokens, ctx, &a, &format);
     chm::Plan plan;
-    const Target target{ctx->compute_units, ctx->gemm_path, ctx->gemv_path,
-                        ctx->workspace ? ctx->workspace_bytes : 0};
-    if (v.ok()) v = plan_product(a, format, target, gate, range_sums ? range_sums_bytes : 0, &plan);
+    if (v.ok()) v = plan_product(a, format, target_of(ctx), gate, range_sums ? range_sums_bytes : 0, &plan);
     if (!v.ok()) return fail(ctx, v.status, v.message);
-    if (plan.kernel == chm::kNoKernel) return ok(ctx);
     if (plan.kernel == chm::kGemmSplit && reinterpret_cast<uintptr_t>(range_sums) % 4 != 0)
         return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: range_sums not 4-byte aligned");
-    if (hipError_t e = hipSetDevice(ctx->device); e != hipSuccess) return hip_fail(ctx, e, "launch: hipSetDevice");
-    auto* s = static_cast<hipStream_t>(stream);
-    hipError_t e;
-    switch (plan.kernel) {
-        case chm::kGemmMfma: e = chm::launch_gemm_mfma(a, format, plan, ctx->workspace, s); break;
-        case chm::kGemmTiled: e = chm::launch_gemm_canonical(a, format, plan, nullptr, s); break;
-        case chm::kGemmSplit: e = chm::launch_gemm_canonical(a, format, plan, static_cast<float*>(range_sums), s); break;
-        default: e = chm::launch_gemv(a, format, plan, ctx->compute_units, s); break;
+    return run_plan(ctx, a, format, plan, static_cast<float*>(range_sums), stream);
+}
+
+charlotte_hip_matmul_status charlotte_hip_matmul_launch_static(charlotte_hip_matmul_context* ctx,
+                                                               const charlotte_hip_matmul_desc* desc,
+                                                               charlotte_hip_matmul_split_gate gate, uint32_t tokens,
+                                                               void* stream) {
+    if (!ctx) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
+    chm::Product a{};
+    uint32_t format = 0;
+    Verdict v = describe(desc, tokens, ctx, &a, &format);
+    chm::Plan plan;
+    // The plan with room for any split first: a step the gate splits whose
+    // range sums pass the static array is refused, not run another way.
+    if (v.ok()) v = plan_product(a, format, target_of(ctx), gate, ~uint64_t{0}, &plan);
+    if (!v.ok()) return fail(ctx, v.status, v.message);
+    if (plan.kernel == chm::kGemmSplit) {
+        const uint64_t need = uint64_t{4} * 32 * a.tokens * a.rows;
+        if (need > CHARLOTTE_HIP_MATMUL_STATIC_SCRATCH_BYTES)
+            return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT,
+                        "launch_static: the split's range sums need " + std::to_string(need) +
+                            " bytes, past the static scratch's " +
+                            std::to_string(uint64_t{CHARLOTTE_HIP_MATMUL_STATIC_SCRATCH_BYTES}));
     }
-    if (e != hipSuccess) return hip_fail(ctx, e, "launch");
-    return ok(ctx);
+    return run_plan(ctx, a, format, plan, ctx->scratch, stream);
 }
 
 charlotte_hip_matmul_status charlotte_hip_matmul_gather(charlotte_hip_matmul_context* ctx,

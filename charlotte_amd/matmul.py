@@ -226,6 +226,8 @@ SIGNATURES = {
         _c.c_int,
         [_c.c_void_p, _c.POINTER(_Desc), _Gate, _c.c_void_p, _c.c_uint64, _c.c_uint32, _c.c_void_p],
     ),
+    "charlotte_hip_matmul_launch_static": (
+        _c.c_int, [_c.c_void_p, _c.POINTER(_Desc), _Gate, _c.c_uint32, _c.c_void_p]),
     "charlotte_hip_matmul_plan_launch": (
         _c.c_int,
         [_c.POINTER(_Desc), _c.POINTER(_Target), _Gate, _c.c_uint64, _c.c_uint32, _c.POINTER(_Plan), _c.c_char_p,
@@ -482,6 +484,19 @@ def plan_launch(m: MatmulLaunch, tokens: int, target: Target = Target(), gate: S
         raise MatmulError(s, msg.value.decode())
     return Plan(Kernel(p.kernel), p.launches, bool(p.canonical), p.rows, p.lanes_a_row, p.groups_a_lane,
                 p.steps_a_wave, p.tile_tokens, p.tile_rows, p.chunks, p.tiles, p.workgroups)
+
+
+# The allocation-free launch's static range sums, a device (the header's constant).
+STATIC_SCRATCH_BYTES = 16 * 1024 * 1024
+
+
+def launch_static(ctx: Context, m: MatmulLaunch, tokens: int, gate: SplitGate = kNever, stream=None):
+    """charlotte_hip_matmul_launch_static: the launch with the split's range sums
+    in the library's static array (no allocation, no caller buffer). Calls that
+    overlap on one GPU race."""
+    if m._desc is None:
+        m._desc = m.desc()
+    ctx.check(lib.charlotte_hip_matmul_launch_static(ctx.handle, ctypes.byref(m._desc), _gate(gate), tokens, stream))
 
 
 # ---- the embedding gather (src/core/kernels/gather/gather.h:126-145) ------------

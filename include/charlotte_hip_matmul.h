@@ -332,6 +332,25 @@ charlotte_hip_matmul_status charlotte_hip_matmul_plan_launch(const charlotte_hip
                                                              charlotte_hip_matmul_plan* out, char* message,
                                                              uint64_t message_bytes);
 
+/* The allocation-free launch. No counterpart in the reference: for callers
+ * that cannot allocate device memory — code under HIP graph capture, tight
+ * serving loops, harnesses that forbid it. charlotte_hip_matmul_launch with
+ * the split's range sums taken from the library's own static array, one a
+ * device of CHARLOTTE_HIP_MATMUL_STATIC_SCRATCH_BYTES, held from the
+ * library's load on the device until the process ends, in place of the
+ * caller's buffer. It allocates nothing and frees nothing. A step the gate
+ * splits whose range sums (4 x 32 x tokens x rows bytes) pass the array is
+ * refused with INVALID_ARGUMENT; every other step runs as the ordinary
+ * launch runs it, with the same bits. Every call on one GPU shares that
+ * GPU's array and leaves its contents behind (nothing in it must start at
+ * zero): calls that overlap on one GPU — on two streams, or from two
+ * threads — race. */
+#define CHARLOTTE_HIP_MATMUL_STATIC_SCRATCH_BYTES (16u * 1024u * 1024u)
+charlotte_hip_matmul_status charlotte_hip_matmul_launch_static(charlotte_hip_matmul_context* ctx,
+                                                               const charlotte_hip_matmul_desc* desc,
+                                                               charlotte_hip_matmul_split_gate gate, uint32_t tokens,
+                                                               void* stream);
+
 /* matmul.h:648-659: the most tokens a step may hold for the product to split,
  * a whole number of 32-token tiles up to 512, or 1 when it never splits; and
  * the floats range_sums must hold for it. */
