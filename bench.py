@@ -19,6 +19,10 @@ A step is one pass of the hot path over one batch of synthetic input:
       (2048x8192 Q4_0): split along K (c6_split), tiled (c6_tiled), matrix cores
   c7  the embedding gather from Qwen3-0.6B's Q6_K table (151936x1024): a
       512-token step and a decode step
+  c8  large Q4_0 decodes: a Q4_0 LM head 151936x1024 and a 32768x8192 product
+Every row carries a roofline in the unit its kernel runs on: HBM GB/s for the
+decodes; TFLOP/s for the prefills, the VALU tile against the FP32 peak, the
+matrix cores against the dense FP16 peak and this design's useful half of it.
 Inputs are seeded synthetic data (BASELINE's distributions) resident in HBM
 before timing; a GEMV's weights rotate over copies totalling > 2x the 256 MB
 MALL so every step reads HBM. Each config's launches are captured once in a
@@ -160,7 +164,7 @@ def run_gemv(S, name, gtype, rows, columns, steps, warmup, rng, copies=None):
         state["i"] += 1
         mm.launch(S.ctx, m, 1, stream=S.stream.handle)
 
-    log(f"{name}: {rows}x{columns} {'Q4_0' if gtype == 2 else 'Q6_K'}, {copies} copies, setup {time.time() - t0:.1f}s")
+    log(f"{name}: {rows}x{columns} {mm.TensorType(gtype).name}, {copies} copies, setup {time.time() - t0:.1f}s")
     ms = S.time_graph(body, steps, warmup)
     spread = [round(t * 1e3, 2) for t in S.last_reps]
     single = S.time_single(body)
@@ -169,7 +173,9 @@ def run_gemv(S, name, gtype, rows, columns, steps, warmup, rng, copies=None):
     log(f"{name}: {ms * 1e3:.2f} us/launch (median of {spread} us), {gbs:.0f} GB/s "
         f"({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s); single launch {single * 1e3:.2f} us")
     return {"ms_per_step": ms, "bytes": nbytes, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "copies": copies,
-            "ms_single_launch": single, "stored": stored, "x": x, "weights": ws}
+            "ms_single_launch": single, "stored": stored, "x": x, "weights": ws,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
 
 
 def build_products(S, rng, plan, tokens, gtype=2):
@@ -247,7 +253,9 @@ def run_c3(S, steps, warmup, rng, fused=True):
     log(f"{tag}: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s aggregate, {1e3 / ms:.0f} tokens/s; "
         f"launched eagerly {single * 1e3:.1f} us/step")
     out = {"ms_per_step": ms, "bytes": total, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "launches": len(launches),
-           "tokens_per_s": 1e3 / ms, "ms_single_launch": single}
+           "tokens_per_s": 1e3 / ms, "ms_single_launch": single,
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
     if fused:
         out.update(decode_matches_prefill(S, launches, xs, rng))
     return out
@@ -319,12 +327,47 @@ def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=No
 
     ms = S.time_graph(body, steps, warmup)
     tflops = flops / (ms * 1e-3) / 1e12
-    log(f"{name}: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s ({100 * tflops / FP32_PEAK_TFLOPS:.1f}% of FP32 peak, "
-        f"{100 * tflops / F16_PEAK_TFLOPS:.1f}% of dense FP16 matrix peak)")
-    return {"ms_per_step": ms, "flops": flops, "TFLOP/s": tflops, "path": path.name,
-            "frac_fp32": tflops / FP32_PEAK_TFLOPS,
-            "frac_f16_matrix": tflops / F16_PEAK_TFLOPS,
+    roof = gemm_roofline(tflops, path, name)
+    log(f"{name}: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s ({100 * roof['frac']:.1f}% of its unit's peak, "
+        f"{roof['peak']} TFLOP/s {roof['bound']})")
+    return {"ms_per_step": ms, "flops": flops, "TFLOP/s": tflops, "path": path.name, "roofline": roof,
             "tokens_per_s": tokens / (ms * 1e-3), "launches": len(launches), "head_gemv_bytes": head_bytes}
+
+
+def gemm_roofline(tflops, path, name):
+    """The roofline of a prefill row in the unit its path runs on: the VALU
+    tile against the FP32 peak; the matrix cores against the dense FP16 peak,
+    and against the useful ceiling of this design (two f16 products an output
+    product: half the peak). Counter traffic where profiles/traffic_c4.json
+    holds it (c4)."""
+    mm_path = path.name
+    if mm_path == "SPLIT_F16_MFMA":
+        roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / F16_PEAK_TFLOPS, 4), "useful_peak": F16_PEAK_TFLOPS / 2,
+                "frac_of_useful": round(tflops / (F16_PEAK_TFLOPS / 2), 4)}
+    else:
+        roof = {"bound": "valu", "achieved": round(tflops, 1), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / FP32_PEAK_TFLOPS, 4)}
+    roof["traffic"] = gemm_traffic(name, mm_path)
+    return roof
+
+
+def gemm_traffic(name, path):
+    """HBM bytes a step of c4 from the counter runs in profiles/traffic_c4.json
+    (FETCH_SIZE and WRITE_SIZE, KiB a dispatch, scaled as traffic_c2.json's);
+    the matrix-core step adds prepare_x's. None for other configs."""
+    file = os.path.join(ROOT, "profiles", "traffic_c4.json")
+    if not name.startswith("c4") or not os.path.exists(file):
+        return None
+    t = json.load(open(file))
+    k = t["kernels"]
+
+    def b(e):
+        return (e["fetch_kib"] * t["fetch_scale"] + e["write_kib"] * t["write_scale"]) * 1024
+
+    if path == "SPLIT_F16_MFMA":
+        return int(round(b(k["mfma"]) + b(k["prepare_x"])))
+    return int(round(b(k["canonical"])))
 
 
 def run_gather(S, name, gtype, rows, columns, tokens, steps, warmup, rng):
@@ -347,7 +390,9 @@ def run_gather(S, name, gtype, rows, columns, tokens, steps, warmup, rng):
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"{name}: {tokens} rows of {rows}x{columns} (type {gtype}), setup {time.time() - t0:.1f}s: "
         f"{ms * 1e3:.2f} us/step, {gbs:.0f} GB/s")
-    return {"ms_per_step": ms, "bytes": nbytes, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "tokens": tokens}
+    return {"ms_per_step": ms, "bytes": nbytes, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "tokens": tokens,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
 
 
 def cpu_baseline_c2(stored, x, rows, columns, seconds=10.0):
@@ -476,7 +521,7 @@ def main():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--only", default="c1,c2,c3,c4,c5,c6,c7")
+    p.add_argument("--only", default="c1,c2,c3,c4,c5,c6,c7,c8")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-table", action="store_true",
                    help="time the CPU baseline table (C1-C5, f32 and f64, 1 and all threads) and exit")
@@ -509,12 +554,16 @@ def main():
             S.ctx.set_gemv_path(S.mm.GemvPath.CANONICAL)
             out["c2_limbs"] = {k: v for k, v in r.items() if k not in ("stored", "x", "weights")}
             out["c2_limbs"]["path"] = "INT8_LIMBS: within 1e-5 of the canonical order, not its bits"
-            out["c2_limbs"]["roofline"] = {"bound": "hbm", "achieved": round(r["GB/s"], 1), "peak": HBM_PEAK_GBS,
-                                           "unit": "GB/s", "frac": round(r["frac"], 4),
-                                           "traffic": measured_traffic(limbs=True)}
+            out["c2_limbs"]["roofline"]["traffic"] = measured_traffic(limbs=True)
         if "c1" in only:
             r = run_gemv(S, "c1", 2, 3072, 1024, max(args.steps, 100), args.warmup, np.random.default_rng(1))
             out["c1"] = {k: v for k, v in r.items() if k not in ("stored", "x", "weights")}
+        if "c8" in only:
+            # Large Q4_0 decodes: a Q4_0 LM head (151,936 x 1,024) and a wide
+            # product (32,768 x 8,192), weights rotated past the MALL.
+            for tag, rows, columns in (("c8_q4_0_head", 151936, 1024), ("c8_q4_0_wide", 32768, 8192)):
+                r = run_gemv(S, tag, 2, rows, columns, max(args.steps, 20), args.warmup, np.random.default_rng(8))
+                out[tag] = {k: v for k, v in r.items() if k not in ("stored", "x", "weights")}
         if "c3" in only:
             out["c3"] = run_c3(S, max(args.steps // 4, 3), args.warmup, rng)
             out["c3_unfused"] = run_c3(S, max(args.steps // 4, 3), args.warmup, rng, fused=False)
