@@ -1,8 +1,8 @@
 """The INT8_LIMBS decode on the GPU (x as three int8 limbs a 32-weight group,
 products on the dot instructions), held to the stated tolerance against the
 CPU oracle: max |y - y_f64| / max |y_f64| <= 1e-5, and each row's argmax the
-reference-order f32 product's wherever its top two differ by more than the
-error allows (BASELINE's bar, as the matrix-core prefill's tests hold it).
+reference-order f32 product's, with no allowance for near-ties (BASELINE's
+bar as stated, as the matrix-core prefill's tests hold it).
 
 The path is not bit-exact by design. These tests pin its error at the shapes
 it is built for (Q6_K, K = 1,152 and 1,024 with rows in 16s, 2,048 with rows
@@ -61,11 +61,8 @@ def _within(got, y64, canonical, what):
     err = np.abs(got.astype(np.float64) - y64).max()
     top = np.abs(y64).max()
     assert err <= TOLERANCE * top, f"{what}: max err {err:.3e} vs max |y| {top:.3e} ({err / top:.2e})"
-    for t in range(got.shape[0]):
-        a, b = int(np.argmax(got[t])), int(np.argmax(canonical[t]))
-        if a != b:
-            s = np.sort(y64[t])
-            assert s[-1] - s[-2] <= 2 * err, f"{what}: row argmax {a} vs {b}"
+    a, b = np.argmax(got, axis=1), np.argmax(canonical, axis=1)
+    assert (a == b).all(), f"{what}: rows {np.nonzero(a != b)[0].tolist()} change argmax"
     return err / top
 
 
@@ -207,7 +204,7 @@ def test_limbs_at_c2_size_against_canonical(run, canonical_run):
     err = np.abs(got.astype(np.float64) - want.astype(np.float64)).max()
     top = np.abs(want).max()
     assert err <= TOLERANCE * top, f"{err:.3e} vs {top:.3e}"
-    assert int(np.argmax(got)) == int(np.argmax(want)) or np.sort(want[0])[-1] - np.sort(want[0])[-2] <= 2 * err
+    assert int(np.argmax(got)) == int(np.argmax(want))
 
 
 def test_gemv_path_setter_refuses_an_unknown_path(ctx):

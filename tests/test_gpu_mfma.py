@@ -1,7 +1,7 @@
 """The matrix-core prefill (SPLIT_F16_MFMA) on the GPU, held to the stated
 tolerance against the CPU oracle: max |y - y_f64| / max |y_f64| <= 1e-5 and
-each token's argmax the same as the reference-order f32 product's wherever
-its top two differ by more than the error allows (BASELINE's bar; the
+each token's argmax the same as the reference-order f32 product's, with no
+allowance for near-ties (BASELINE's bar as stated; the
 reference's own bound is gamma(2K) sum |w x|, matmul_test.cpp:190-211, which
 the canonical path meets bit for bit and this path is not asked to).
 
@@ -56,11 +56,10 @@ def _within(got, y64, canonical, what):
     err = np.abs(got.astype(np.float64) - y64).max()
     top = np.abs(y64).max()
     assert err <= TOLERANCE * top, f"{what}: max err {err:.3e} vs max |y| {top:.3e} ({err / top:.2e})"
-    for t in range(got.shape[0]):
-        a, b = int(np.argmax(got[t])), int(np.argmax(canonical[t]))
-        if a != b:
-            s = np.sort(y64[t])
-            assert s[-1] - s[-2] <= 2 * err, f"{what}: token {t} argmax {a} vs {b}"
+    # BASELINE's argmax rule as stated: every token row's argmax the
+    # reference-order product's, with no allowance for near-ties.
+    a, b = np.argmax(got, axis=1), np.argmax(canonical, axis=1)
+    assert (a == b).all(), f"{what}: tokens {np.nonzero(a != b)[0].tolist()} change argmax"
     return err / top
 
 
