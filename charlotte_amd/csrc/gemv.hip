@@ -713,7 +713,24 @@ bool plan_gemv(const Product& a, uint32_t format, uint32_t compute_units, bool l
         const uint64_t target = per_cu * compute_units * kWaves * rows_a_step;
         uint32_t steps = 1;
         while (steps < max_steps && steps * target < a.rows) steps *= 2;
-        plan->steps = steps;
+        // Past one round of tiles on the resident workgroups (two a CU), the
+        // fewer steps whose rounds leave the fewest rows on the busiest
+        // workgroup: 151,936 rows at 32 steps are 594 tiles on 512
+        // workgroups, 82 of which run a second round (512 rows for the
+        // busiest); at 8 steps, 2,374 tiles, 320 rows (Q4_0 head: 28.5 ->
+        // 26 us).
+        const uint64_t resident = 2ull * compute_units;
+        auto makespan = [&](uint32_t st) {
+            const uint64_t rows_a_tile = uint64_t{kWaves} * st * rows_a_step;
+            const uint64_t tiles = (a.rows + rows_a_tile - 1) / rows_a_tile;
+            return (tiles + resident - 1) / resident * rows_a_tile;
+        };
+        uint32_t best = steps;
+        const uint64_t tiles_now = (a.rows + uint64_t{kWaves} * steps * rows_a_step - 1) / (uint64_t{kWaves} * steps * rows_a_step);
+        if (tiles_now > resident)
+            for (uint32_t st = steps / 2; st >= 8; st /= 2)
+                if (makespan(st) * 100 < makespan(best) * 97) best = st;
+        plan->steps = best;
     }
     plan->tile_rows = kWaves * plan->steps * rows_a_step;
     plan->tiles = (a.rows + plan->tile_rows - 1) / plan->tile_rows;

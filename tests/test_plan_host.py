@@ -114,6 +114,17 @@ def test_c1_is_the_reference_mapping_in_one_workgroup_a_cu(shapes):
     assert (p.steps_a_wave, p.tile_rows, p.tiles) == (2, 16, 192)
 
 
+def test_large_decodes_balance_their_rounds_of_tiles(shapes):
+    """A Q4_0 head of 151,936 rows: at 32 steps a wave, 594 tiles of 256 rows
+    on 512 resident workgroups leave 82 with a second round; 8 steps give
+    2,374 tiles of 64 rows, 5 rounds, 320 rows on the busiest."""
+    p = mm.plan_launch(_write(shapes(Q4_0, 151936, 1024)), 1)
+    assert (p.kernel, p.steps_a_wave, p.tile_rows, p.tiles) == (K.GEMV_RANGES, 8, 64, 2374)
+    # One round already balanced: left as it is.
+    p = mm.plan_launch(_write(shapes(Q4_0, 32768, 8192)), 1)
+    assert (p.steps_a_wave, p.tiles) == (8, 512)
+
+
 def test_k_1152_other_than_whole_streamed_steps_takes_four_lanes_a_row(shapes):
     assert mm.plan_launch(_write(shapes(Q4_0, 1000, 1152)), 1).kernel == K.GEMV_QUARTERS
     assert mm.plan_launch(_write(shapes(Q6_K, 1000, 1152)), 1).kernel == K.GEMV_QUARTERS
