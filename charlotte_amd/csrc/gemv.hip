@@ -642,6 +642,8 @@ static hipError_t launch_format(const Product& a, const Plan& plan, uint32_t cus
 // The decode's kernel and shape:
 //   - Q6_K at K = 1,152, 1,024 or 2,048 in whole steps: the LDS-streamed
 //     kernels (the INT8_LIMBS form there when asked);
+//   - Q4_0 at K = 2,048, 4,096 or 8,192 in whole steps: the LDS-streamed
+//     kernel (the INT8_LIMBS form is Q6_K's alone);
 //   - quantized K = 1,152 otherwise: 4 lanes a row, 9 groups each;
 //   - other K up to 8,192: the reference's 32 lanes a row, x in registers
 //     while a lane's slice is at most 3 groups, else staged whole in LDS
@@ -663,6 +665,17 @@ bool plan_gemv(const Product& a, uint32_t format, uint32_t compute_units, bool l
         plan->canonical = !limbs;
         plan->lanes = stream ? 4 : G / 8;
         plan->span = stream ? 9 : 8;
+        plan->steps = 1;
+        plan->tile_rows = step_rows;
+        plan->tiles = a.rows / step_rows;
+        plan->workgroups = std::min<uint64_t>(2ull * compute_units, (plan->tiles + 3) / 4);
+        return true;
+    }
+    if (gemv_stream4_takes(a, format)) {
+        const uint32_t step_rows = 64 / (G / 8);
+        plan->kernel = kGemvStream4;
+        plan->lanes = G / 8;
+        plan->span = 8;
         plan->steps = 1;
         plan->tile_rows = step_rows;
         plan->tiles = a.rows / step_rows;
@@ -742,6 +755,7 @@ hipError_t launch_gemv(const Product& a, uint32_t format, const Plan& plan, uint
                        hipStream_t stream) {
     if (plan.kernel == kGemvStream) return launch_gemv_stream(a, compute_units, plan.limbs, stream);
     if (plan.kernel == kGemvStream8) return launch_gemv_stream8(a, compute_units, plan.limbs, stream);
+    if (plan.kernel == kGemvStream4) return launch_gemv_stream4(a, compute_units, stream);
     switch (format) {
         case kQ4_0: return launch_format<kQ4_0>(a, plan, compute_units, stream);
         case kQ4_1: return launch_format<kQ4_1>(a, plan, compute_units, stream);

@@ -1,0 +1,216 @@
+// Decode of Q4_0 rows of K = 2,048, 4,096 and 8,192 (G = 64, 128, 256
+// groups) — down projections and the wide products of larger models —
+// streamed through LDS.
+//
+// Why: the reference's mapping (gemv.hip, lane r of a half-wave owns range
+// r) gives a lane G / 32 contiguous groups, so past K = 1,024 each load
+// instruction's lanes read 16 bytes at a stride of G / 2 bytes: 64 cache
+// lines an instruction at K = 8,192 against 8 at K = 1,024, and the
+// measured rate falls with it (32,768 x 8,192: 2.5 TB/s; 262,144 x 1,024:
+// 4.0). Here a wave copies a step of rows into its LDS stage with
+// global_load_lds_dwordx4 — the step's 8 KB of codes and 1 KB of scales are
+// contiguous in the piece, so every copy instruction reads 1 KB in a row —
+// and each lane then reads its own groups out of LDS, as gemv_stream8.hip
+// does for Q6_K.
+//
+// Mapping: every lane owns 8 groups (128 code bytes, 16 scale bytes): L = G /
+// 8 lanes a row (8, 16, 32), 64 / L rows a step (8, 4, 2). Lane j of a row
+// owns ranges (32 / L) j .. (32 / L)(j + 1) - 1, G / 32 groups each. Its
+// range sums are chained over the row's lanes in order — ((0 + sums of lane
+// 0) + sums of lane 1) + ... — by DPP row shifts for L = 8 and 16; for L = 32
+// the 32 sums go through LDS and one lane adds them in order. The bits are
+// every other kernel's.
+#include <algorithm>
+
+#include "decode.hpp"
+#include "plan.hpp"
+#include "product.hpp"
+#include "stream.hpp"
+
+namespace chm {
+
+namespace {
+
+constexpr int kWaves4 = 4;
+constexpr uint32_t kCodeChunks = 512, kScaleChunks = 64;  // 16-byte chunks a step: 8 KB codes, 1 KB scales
+constexpr uint32_t kSlice4 = 65;                          // x slice stride in float4: 8 groups of 8, one of padding
+
+// A lane's share of a step: its 8 groups' codes and their 8 fp16 scales.
+struct StepRun4 {
+    u32x4s_t codes[8];
+    u32x4s_t scales;
+};
+
+}  // namespace
+
+template <uint32_t G, bool FULL>
+__global__ __launch_bounds__(256, 2) void gemv_stream4(Product a, uint32_t steps) {
+    constexpr uint32_t L = G / 8;           // lanes a row
+    constexpr uint32_t kRows = 64 / L;      // rows a step
+    constexpr uint32_t kRanges = 32 / L;    // ranges a lane
+    constexpr uint32_t kPerRange = G / 32;  // groups a range
+    __shared__ u32x4s_t codes_a[kWaves4][kCodeChunks];
+    __shared__ u32x4s_t scales_a[kWaves4][kScaleChunks];
+    __shared__ u32x4s_t x_stage[kSlice4 * L];
+    __shared__ float sums_a[kWaves4][33 * kRows];  // a step's range sums, a row of 32 and one of padding
+    const float4* const xs = reinterpret_cast<const float4*>(x_stage);
+
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t rho = lane / L, j = lane % L;
+    const uint32_t waves = gridDim.x * kWaves4;
+    const uint32_t token = a.last_token ? a.tokens - 1 : 0;
+    u32x4s_t *const codes_s = codes_a[wave], *const scales_s = scales_a[wave];
+    float* const sums_s = sums_a[wave];
+
+    // Codes land swizzled: stage chunk 8l + k holds the step's chunk 8l + (k
+    // xor l mod 8), so the eight lanes that read one 128-byte row each (lane
+    // l, its group i at chunk 8l + (i xor l mod 8)) fall in eight different
+    // sets of four banks. A copy instruction still reads 1 KB in a row.
+    const uint32_t swizzled = (lane & ~7u) | ((lane ^ (lane >> 3)) & 7u);
+    auto issue = [&](uint32_t step) {
+        const Piece w = piece_of(a, step * kRows);
+        const uint64_t g0 = static_cast<uint64_t>(w.row) * G;  // the step's first group
+        const uint8_t* from = w.piece + 16 * g0;
+#pragma unroll
+        for (uint32_t i = 0; i < kCodeChunks / 64; ++i)
+            __builtin_amdgcn_global_load_lds(from + 16 * (64 * i + swizzled), (lds_void)(codes_s + 64 * i), 16, 0, 0);
+        copy_stream<kScaleChunks>(w.piece + 16 * w.blocks + 2 * g0, scales_s, lane);
+    };
+    // The stage's reads are instructions the compiler does not look into (it
+    // would wait for the copy in flight into the same stage); their wait is
+    // explicit, as in gemv_stream.hip. Lane l's groups are the step's 8l ..
+    // 8l + 7.
+    const uint32_t c_at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(codes_s)) + 128 * lane;
+    const uint32_t s_at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(scales_s)) + 16 * lane;
+    auto take = [&](StepRun4& run) {
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i)
+            __asm__ __volatile__("ds_read_b128 %0, %1" : "=v"(run.codes[i]) : "v"(c_at + 16 * (i ^ (lane & 7u))));
+        __asm__ __volatile__("ds_read_b128 %0, %1" : "=v"(run.scales) : "v"(s_at));
+        __asm__ __volatile__("s_waitcnt lgkmcnt(0)"
+                             : "+v"(run.codes[0]), "+v"(run.codes[1]), "+v"(run.codes[2]), "+v"(run.codes[3]),
+                               "+v"(run.codes[4]), "+v"(run.codes[5]), "+v"(run.codes[6]), "+v"(run.codes[7]),
+                               "+v"(run.scales)
+                             :
+                             : "memory");
+    };
+    const uint32_t out_token = a.last_token ? a.tokens - 1 : 0;
+    // The lane's range sums into the wave's LDS; the row's first lane then
+    // adds the 32 in order from zero — ((0 + s0) + s1) + ... + s31, the
+    // order of matmul.h:34-50.
+    auto decode = [&](uint32_t step, const StepRun4& run) {
+        float s = 0.0f;
+        // x a group ahead: group i + 1's words are read before group i's
+        // products, so the reads' latency runs under them.
+        float4 xa[2][8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) xa[0][v] = xs[kSlice4 * j + v];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (i + 1 < 8) {
+#pragma unroll
+                for (int v = 0; v < 8; ++v) xa[(i + 1) & 1][v] = xs[kSlice4 * j + 8 * (i + 1) + v];
+            }
+            float xg[32];
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+                const float4 q = xa[i & 1][v];
+                xg[4 * v] = q.x, xg[4 * v + 1] = q.y, xg[4 * v + 2] = q.z, xg[4 * v + 3] = q.w;
+            }
+            const uint32_t cw[4] = {run.codes[i][0], run.codes[i][1], run.codes[i][2], run.codes[i][3]};
+            const uint32_t d = (run.scales[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+            s = chain_q4_0(cw, d, xg, s);
+            if ((i + 1) % kPerRange == 0) {
+                sums_s[33 * rho + kRanges * j + i / kPerRange] = s;
+                s = 0.0f;
+            }
+        }
+        // The sums are this wave's own: a wave barrier orders the writes
+        // before the reads, and the reads before the next step's writes.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const uint32_t p = step * kRows + rho;
+        if (j == 0) {
+            float total = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 32; ++k) total = total + sums_s[33 * rho + k];
+            if (p < a.rows) emit<FULL>(a, p, 0, out_token, total, 0.0f);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+
+    // The first step's copy goes out before x is staged (the barrier below
+    // waits for both round trips at once).
+    uint32_t step = blockIdx.x * kWaves4 + wave;
+    if (step < steps) issue(step);
+    {
+        // float4 v of x sits at v + v / 64 (slice v / 64 of 64, one of
+        // padding), clamped where the product is clipped. The stores are
+        // instructions the compiler does not look into (it would wait for
+        // the copy just issued); their wait is explicit.
+        constexpr uint32_t kPer = G * 8 / 256;  // float4 a thread: 2, 4 or 8
+        const float4* src = reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(token) * G * 32);
+        const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(x_stage));
+        float4 xv[kPer];
+#pragma unroll
+        for (uint32_t k = 0; k < kPer; ++k) xv[k] = clamp_input(a, src[threadIdx.x + 256 * k]);
+#pragma unroll
+        for (uint32_t k = 0; k < kPer; ++k) {
+            const uint32_t v = threadIdx.x + 256 * k;
+            const u32x4s_t bits = {__float_as_uint(xv[k].x), __float_as_uint(xv[k].y), __float_as_uint(xv[k].z),
+                                   __float_as_uint(xv[k].w)};
+            __asm__ __volatile__("ds_write_b128 %0, %1" : : "v"(base + 16 * (v + v / 64)), "v"(bits));
+        }
+        __asm__ __volatile__("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    if (step >= steps) return;
+    while (true) {
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+        __asm__ __volatile__("" ::: "memory");
+        StepRun4 run;
+        take(run);
+        const uint32_t next = step + waves;
+        if (next < steps) issue(next);
+        decode(step, run);
+        if (next >= steps) break;
+        step = next;
+    }
+}
+
+// Whether this kernel takes the product: Q4_0, K = 2,048, 4,096 or 8,192,
+// every member's rows and first row a whole number of steps (so a step lies
+// in one member), not gated (a gated product interleaves its members' rows).
+bool gemv_stream4_takes(const Product& a, uint32_t format) {
+    if (format != kQ4_0 || (a.groups != 64 && a.groups != 128 && a.groups != 256)) return false;
+    const uint32_t rows = 64 / (a.groups / 8);
+    for (uint32_t m = 0; m < a.members; ++m)
+        if (a.m[m].rows % rows != 0 || a.m[m].row_offset % rows != 0) return false;
+    return a.epilogue != kGated;
+}
+
+template <uint32_t G>
+static void go4(const Product& a, uint32_t compute_units, hipStream_t stream) {
+    const uint32_t steps = a.rows / (64 / (G / 8));
+    const uint32_t blocks = std::min<uint32_t>(2 * compute_units, (steps + kWaves4 - 1) / kWaves4);
+    if (plain_epilogue(a))
+        hipLaunchKernelGGL((gemv_stream4<G, false>), dim3(blocks), dim3(256), 0, stream, a, steps);
+    else
+        hipLaunchKernelGGL((gemv_stream4<G, true>), dim3(blocks), dim3(256), 0, stream, a, steps);
+}
+
+hipError_t launch_gemv_stream4(const Product& a, uint32_t compute_units, hipStream_t stream) {
+    switch (a.groups) {
+        case 64: go4<64>(a, compute_units, stream); break;
+        case 128: go4<128>(a, compute_units, stream); break;
+        case 256: go4<256>(a, compute_units, stream); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace chm

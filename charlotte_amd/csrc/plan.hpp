@@ -22,6 +22,7 @@ enum Kernel : uint32_t {
     kGemvStream = 3,    // decode, LDS-streamed Q6_K, K = 1,152
     kGemvStream8 = 4,   // decode, LDS-streamed Q6_K, K = 1,024 and 2,048
     kGemvChunked = 5,   // decode past K = 8,192: x staged a chunk of groups at a time
+    kGemvStream4 = 6,   // decode, LDS-streamed Q4_0, K = 2,048, 4,096 and 8,192
     kGemmTiled = 16,    // prefill, the VALU tile
     kGemmSplit = 17,    // prefill split along K, then the ordered combine
     kGemmMfma = 18,     // prefill on the matrix cores, x split into two f16 parts
@@ -51,8 +52,10 @@ hipError_t launch_gemv(const Product& a, uint32_t format, const Plan& plan, uint
                        hipStream_t stream);
 bool gemv_stream_takes(const Product& a, uint32_t format);
 bool gemv_stream8_takes(const Product& a, uint32_t format);
+bool gemv_stream4_takes(const Product& a, uint32_t format);
 hipError_t launch_gemv_stream(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream);
 hipError_t launch_gemv_stream8(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream);
+hipError_t launch_gemv_stream4(const Product& a, uint32_t compute_units, hipStream_t stream);
 
 // Prefill on the VALU tile; `split` for the split along K.
 void plan_gemm_canonical(const Product& a, uint32_t compute_units, bool split, Plan* plan);

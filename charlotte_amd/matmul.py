@@ -90,6 +90,7 @@ class Kernel(enum.IntEnum):
     GEMV_STREAM = 3
     GEMV_STREAM8 = 4
     GEMV_CHUNKED = 5
+    GEMV_STREAM4 = 6
     GEMM_TILED = 16
     GEMM_SPLIT = 17
     GEMM_MFMA = 18

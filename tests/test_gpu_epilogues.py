@@ -116,9 +116,11 @@ def test_gated_wide_tiles(oracle, run):
 
 
 # 300 rows: the ranges and L = 4 decodes; 304 (whole 16-row steps): the
-# LDS-streamed Q6_K decodes at K = 1,152, 1,024 and 2,048.
+# LDS-streamed Q6_K decodes at K = 1,152, 1,024 and 2,048, and the streamed
+# Q4_0 decode at K = 2,048 and 8,192.
 @pytest.mark.parametrize("gtype,columns,rows", [(Q4_0, 2048, 300), (Q6_K, 1152, 300), (Q6_K, 1152, 304),
-                                                (Q6_K, 1024, 304), (Q6_K, 2048, 304)])
+                                                (Q6_K, 1024, 304), (Q6_K, 2048, 304), (Q4_0, 2048, 304),
+                                                (Q4_0, 8192, 304)])
 def test_gated_by_input(oracle, run, gtype, columns, rows):
     from charlotte_amd import matmul as mm
 

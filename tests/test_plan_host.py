@@ -121,8 +121,8 @@ def test_large_decodes_balance_their_rounds_of_tiles(shapes):
     p = mm.plan_launch(_write(shapes(Q4_0, 151936, 1024)), 1)
     assert (p.kernel, p.steps_a_wave, p.tile_rows, p.tiles) == (K.GEMV_RANGES, 8, 64, 2374)
     # One round already balanced: left as it is.
-    p = mm.plan_launch(_write(shapes(Q4_0, 32768, 8192)), 1)
-    assert (p.steps_a_wave, p.tiles) == (8, 512)
+    p = mm.plan_launch(_write(shapes(Q8_0, 32768, 8192)), 1)
+    assert (p.kernel, p.steps_a_wave, p.tiles) == (K.GEMV_RANGES, 8, 512)
 
 
 def test_k_1152_other_than_whole_streamed_steps_takes_four_lanes_a_row(shapes):
@@ -132,8 +132,35 @@ def test_k_1152_other_than_whole_streamed_steps_takes_four_lanes_a_row(shapes):
 
 @pytest.mark.parametrize("columns,span", [(3072, 3), (4096, 4), (5120, 6), (8192, 8)])
 def test_decode_up_to_k_8192_stages_x_whole(shapes, columns, span):
-    p = mm.plan_launch(_write(shapes(Q4_0, 2048, columns)), 1)
+    # 2,049 rows: no whole number of the streamed Q4_0 decode's steps
+    p = mm.plan_launch(_write(shapes(Q4_0, 2049, columns)), 1)
     assert (p.kernel, p.groups_a_lane) == (K.GEMV_RANGES, span)
+    p = mm.plan_launch(_write(shapes(Q8_0, 2048, columns)), 1)
+    assert (p.kernel, p.groups_a_lane) == (K.GEMV_RANGES, span)
+
+
+@pytest.mark.parametrize("columns,step_rows", [(2048, 8), (4096, 4), (8192, 2)])
+def test_q4_0_k_2048_to_8192_in_whole_steps_is_the_streamed_decode(shapes, columns, step_rows):
+    rows = 32768 * 8192 // columns
+    p = mm.plan_launch(_write(shapes(Q4_0, rows, columns)), 1)
+    assert (p.kernel, p.canonical, p.lanes_a_row, p.groups_a_lane) == (K.GEMV_STREAM4, True, columns // 256, 8)
+    assert (p.tile_rows, p.tiles, p.workgroups) == (step_rows, rows // step_rows, 512)
+    # the INT8_LIMBS path is Q6_K's: Q4_0 stays canonical
+    limbs = mm.plan_launch(_write(shapes(Q4_0, rows, columns)), 1, mm.Target(256, gemv_path=mm.GemvPath.INT8_LIMBS))
+    assert limbs.kernel == K.GEMV_STREAM4 and limbs.canonical
+    w = shapes(Q4_0, 1024, columns)
+    # a member starting inside a step, or not whole steps long: the reference mapping
+    assert mm.plan_launch(mm.MatmulLaunch([mm.Member(w, row_offset=1, rows=step_rows)], X, [Y0]), 1).kernel == \
+        K.GEMV_RANGES
+    assert mm.plan_launch(mm.MatmulLaunch([mm.Member(w, rows=step_rows + 1)], X, [Y0]), 1).kernel == K.GEMV_RANGES
+    three = [mm.Member(w, rows=256), mm.Member(w, row_offset=256, rows=64), mm.Member(w, row_offset=512, rows=64)]
+    assert mm.plan_launch(mm.MatmulLaunch(three, X, [Y0, Y1, Y2], epilogue=mm.Epilogue.QKV), 1).kernel == \
+        K.GEMV_STREAM4
+    # a gated product interleaves its members' rows: the reference mapping
+    gated = mm.MatmulLaunch([mm.Member(w), mm.Member(w)], X, [Y0], epilogue=mm.Epilogue.GatedActivation, out_width=1024)
+    assert mm.plan_launch(gated, 1).kernel == K.GEMV_RANGES
+    # other quantized formats at these K: the reference mapping
+    assert mm.plan_launch(_write(shapes(mm.TensorType.Q4_1, 1024, columns)), 1).kernel == K.GEMV_RANGES
 
 
 @pytest.mark.parametrize("columns", [8192 + 32, 9728, 14336, 65536])
