@@ -58,6 +58,58 @@ __device__ __forceinline__ float chain_q4_0(const uint32_t w[4], uint32_t d_bits
     return s;
 }
 
+// (a & mask) | bits in one v_and_or_b32 (with both constants literals the
+// compiler emits an and and an or).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    __asm__("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(bits));
+    return r;
+}
+
+// chain_q4_0's bits in fewer operations, for the throughput-bound streamed
+// decode (the latency-bound ones keep chain_q4_0, whose first product starts
+// sooner). A code dword's 8 nibbles become four binary16 pairs in 5
+// operations instead of 6: with 0x54 for the high byte a half is 64 + m / 16
+// for its low byte m, so
+//   - (w & 0x000F000F) | 0x54005400: 64 + l0 / 16, 64 + l2 / 16;
+//   - (w & 0x00F000F0) | 0x54005400: 64 + h0, 64 + h2;
+//   - p = bytes 1 and 3 under 0x54 (one v_perm_b32), then p & 0xFF0FFF0F:
+//     64 + l1 / 16, 64 + l3 / 16; p & 0xFFF0FFF0: 64 + h1, 64 + h3;
+// all exact (binary16 steps by 1/16 in [64, 128)). The weights:
+// (64 + l / 16) 16d - 1032 d = (l - 8) d and (64 + h) d - 72 d = (h - 8) d,
+// each one fma of exact terms whose result is exact (16d, 1032d and 72d are
+// exact in f32: d has 11 significant bits).
+__device__ __forceinline__ float chain_q4_0_wide(const uint32_t w[4], uint32_t d_bits, const float* x, float s) {
+    const float d = half_to_float(d_bits);
+    const float d16 = 16.0f * d, low_offset = -1032.0f * d, high_offset = -72.0f * d;
+    uint32_t a[4], b[4], c[4], e[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t p = __builtin_amdgcn_perm(0x54545454u, w[k], 0x04030401u);  // 0x54:b1, 0x54:b3
+        a[k] = and_or(w[k], 0x000F000Fu, 0x54005400u);
+        b[k] = p & 0xFF0FFF0Fu;
+        c[k] = and_or(w[k], 0x00F000F0u, 0x54005400u);
+        e[k] = p & 0xFFF0FFF0u;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const half2_t u = __builtin_bit_cast(half2_t, a[k]), v = __builtin_bit_cast(half2_t, b[k]);
+        s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(u.x), d16, low_offset), x[4 * k], s);
+        s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(v.x), d16, low_offset), x[4 * k + 1], s);
+        s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(u.y), d16, low_offset), x[4 * k + 2], s);
+        s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(v.y), d16, low_offset), x[4 * k + 3], s);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const half2_t u = __builtin_bit_cast(half2_t, c[k]), v = __builtin_bit_cast(half2_t, e[k]);
+        s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(u.x), d, high_offset), x[16 + 4 * k], s);
+        s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(v.x), d, high_offset), x[16 + 4 * k + 1], s);
+        s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(u.y), d, high_offset), x[16 + 4 * k + 2], s);
+        s = __builtin_fmaf(__builtin_fmaf(static_cast<float>(v.y), d, high_offset), x[16 + 4 * k + 3], s);
+    }
+    return s;
+}
+
 // A Q6_K group: 4 lo dwords, 2 hi dwords, its two int8 scales (low 16 bits
 // of sc), its super-block's fp16 d bits.
 __device__ __forceinline__ float chain_q6_k(const uint32_t lo[4], const uint32_t hi[2], uint32_t sc, uint32_t d_bits,

@@ -679,7 +679,7 @@ bool plan_gemv(const Product& a, uint32_t format, uint32_t compute_units, bool l
         plan->steps = 1;
         plan->tile_rows = step_rows;
         plan->tiles = a.rows / step_rows;
-        plan->workgroups = std::min<uint64_t>(2ull * compute_units, (plan->tiles + 3) / 4);
+        plan->workgroups = gemv_stream4_workgroups(G, compute_units, plan->tiles);
         return true;
     }
     if (G * 32 > kMaxStagedK || (format == kF32 && G > 64) || (plain_values(format) && G > 96)) {

@@ -31,7 +31,10 @@ namespace chm {
 
 namespace {
 
-constexpr int kWaves4 = 4;
+// Waves a workgroup and workgroups a CU, by G = 64, 128, 256.
+constexpr uint32_t kS4Waves[3] = {4, 4, 4};
+constexpr uint32_t kS4Blocks[3] = {2, 2, 2};
+constexpr uint32_t s4_index(uint32_t G) { return G == 64 ? 0 : G == 128 ? 1 : 2; }
 constexpr uint32_t kCodeChunks = 512, kScaleChunks = 64;  // 16-byte chunks a step: 8 KB codes, 1 KB scales
 constexpr uint32_t kSlice4 = 65;                          // x slice stride in float4: 8 groups of 8, one of padding
 
@@ -43,22 +46,23 @@ struct StepRun4 {
 
 }  // namespace
 
-template <uint32_t G, bool FULL>
-__global__ __launch_bounds__(256, 2) void gemv_stream4(Product a, uint32_t steps) {
+template <uint32_t G, bool FULL, uint32_t W>
+__global__ __launch_bounds__(64 * W) void gemv_stream4(Product a, uint32_t steps) {
     constexpr uint32_t L = G / 8;           // lanes a row
     constexpr uint32_t kRows = 64 / L;      // rows a step
     constexpr uint32_t kRanges = 32 / L;    // ranges a lane
     constexpr uint32_t kPerRange = G / 32;  // groups a range
-    __shared__ u32x4s_t codes_a[kWaves4][kCodeChunks];
-    __shared__ u32x4s_t scales_a[kWaves4][kScaleChunks];
+    __shared__ u32x4s_t codes_a[W][kCodeChunks];
+    __shared__ u32x4s_t scales_a[W][kScaleChunks];
     __shared__ u32x4s_t x_stage[kSlice4 * L];
-    __shared__ float sums_a[kWaves4][33 * kRows];  // a step's range sums, a row of 32 and one of padding
+    constexpr uint32_t kBatch = 16 / kRows;  // steps whose range sums wait for one ordered pass
+    __shared__ float sums_a[W][33 * 16];    // 16 rows' range sums, a row of 32 and one of padding  // a step's range sums, a row of 32 and one of padding
     const float4* const xs = reinterpret_cast<const float4*>(x_stage);
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t rho = lane / L, j = lane % L;
-    const uint32_t waves = gridDim.x * kWaves4;
+    const uint32_t waves = gridDim.x * W;
     const uint32_t token = a.last_token ? a.tokens - 1 : 0;
     u32x4s_t *const codes_s = codes_a[wave], *const scales_s = scales_a[wave];
     float* const sums_s = sums_a[wave];
@@ -96,10 +100,9 @@ __global__ __launch_bounds__(256, 2) void gemv_stream4(Product a, uint32_t steps
                              : "memory");
     };
     const uint32_t out_token = a.last_token ? a.tokens - 1 : 0;
-    // The lane's range sums into the wave's LDS; the row's first lane then
-    // adds the 32 in order from zero — ((0 + s0) + s1) + ... + s31, the
-    // order of matmul.h:34-50.
-    auto decode = [&](uint32_t step, const StepRun4& run) {
+    // A step's range sums go to the wave's LDS, the step's rows at slot
+    // `slot` of kBatch.
+    auto decode = [&](uint32_t slot, const StepRun4& run) {
         float s = 0.0f;
         // x a group ahead: group i + 1's words are read before group i's
         // products, so the reads' latency runs under them.
@@ -120,22 +123,29 @@ __global__ __launch_bounds__(256, 2) void gemv_stream4(Product a, uint32_t steps
             }
             const uint32_t cw[4] = {run.codes[i][0], run.codes[i][1], run.codes[i][2], run.codes[i][3]};
             const uint32_t d = (run.scales[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-            s = chain_q4_0(cw, d, xg, s);
+            s = chain_q4_0_wide(cw, d, xg, s);
             if ((i + 1) % kPerRange == 0) {
-                sums_s[33 * rho + kRanges * j + i / kPerRange] = s;
+                sums_s[33 * (slot * kRows + rho) + kRanges * j + i / kPerRange] = s;
                 s = 0.0f;
             }
         }
-        // The sums are this wave's own: a wave barrier orders the writes
-        // before the reads, and the reads before the next step's writes.
+    };
+    // Every kBatch steps (and after the last): lane t adds row t's 32 sums in
+    // order from zero — ((0 + s0) + s1) + ... + s31, the order of
+    // matmul.h:34-50 — and emits it. The serial adds run once for 16 rows
+    // instead of once a step. The sums are this wave's own: a wave barrier
+    // orders the writes before the reads, and the reads before the next
+    // batch's writes. `first` is the batch's first step; its steps are
+    // `waves` apart.
+    auto flush = [&](uint32_t first, uint32_t count) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const uint32_t p = step * kRows + rho;
-        if (j == 0) {
+        if (lane < count * kRows) {
             float total = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 32; ++k) total = total + sums_s[33 * rho + k];
+            for (int k = 0; k < 32; ++k) total = total + sums_s[33 * lane + k];
+            const uint32_t p = (first + (lane / kRows) * waves) * kRows + lane % kRows;
             if (p < a.rows) emit<FULL>(a, p, 0, out_token, total, 0.0f);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -145,22 +155,24 @@ __global__ __launch_bounds__(256, 2) void gemv_stream4(Product a, uint32_t steps
 
     // The first step's copy goes out before x is staged (the barrier below
     // waits for both round trips at once).
-    uint32_t step = blockIdx.x * kWaves4 + wave;
+    uint32_t step = blockIdx.x * W + wave;
     if (step < steps) issue(step);
     {
         // float4 v of x sits at v + v / 64 (slice v / 64 of 64, one of
         // padding), clamped where the product is clipped. The stores are
         // instructions the compiler does not look into (it would wait for
         // the copy just issued); their wait is explicit.
-        constexpr uint32_t kPer = G * 8 / 256;  // float4 a thread: 2, 4 or 8
+        constexpr uint32_t kThreads = 64 * W, kPer = (G * 8 + kThreads - 1) / kThreads;  // float4 a thread
         const float4* src = reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(token) * G * 32);
         const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(x_stage));
         float4 xv[kPer];
 #pragma unroll
-        for (uint32_t k = 0; k < kPer; ++k) xv[k] = clamp_input(a, src[threadIdx.x + 256 * k]);
+        for (uint32_t k = 0; k < kPer; ++k)
+            if (threadIdx.x + kThreads * k < G * 8) xv[k] = clamp_input(a, src[threadIdx.x + kThreads * k]);
 #pragma unroll
         for (uint32_t k = 0; k < kPer; ++k) {
-            const uint32_t v = threadIdx.x + 256 * k;
+            const uint32_t v = threadIdx.x + kThreads * k;
+            if (v >= G * 8) break;
             const u32x4s_t bits = {__float_as_uint(xv[k].x), __float_as_uint(xv[k].y), __float_as_uint(xv[k].z),
                                    __float_as_uint(xv[k].w)};
             __asm__ __volatile__("ds_write_b128 %0, %1" : : "v"(base + 16 * (v + v / 64)), "v"(bits));
@@ -169,6 +181,7 @@ __global__ __launch_bounds__(256, 2) void gemv_stream4(Product a, uint32_t steps
         __syncthreads();
     }
     if (step >= steps) return;
+    uint32_t slot = 0, first = step;
     while (true) {
         __builtin_amdgcn_s_waitcnt(kVmcnt0);
         __asm__ __volatile__("" ::: "memory");
@@ -176,7 +189,12 @@ __global__ __launch_bounds__(256, 2) void gemv_stream4(Product a, uint32_t steps
         take(run);
         const uint32_t next = step + waves;
         if (next < steps) issue(next);
-        decode(step, run);
+        decode(slot, run);
+        if (++slot == kBatch || next >= steps) {
+            flush(first, slot);
+            slot = 0;
+            first = next;
+        }
         if (next >= steps) break;
         step = next;
     }
@@ -193,14 +211,20 @@ bool gemv_stream4_takes(const Product& a, uint32_t format) {
     return a.epilogue != kGated;
 }
 
+uint64_t gemv_stream4_workgroups(uint32_t groups, uint32_t compute_units, uint64_t steps) {
+    const uint32_t i = s4_index(groups);
+    return std::min<uint64_t>(uint64_t{kS4Blocks[i]} * compute_units, (steps + kS4Waves[i] - 1) / kS4Waves[i]);
+}
+
 template <uint32_t G>
 static void go4(const Product& a, uint32_t compute_units, hipStream_t stream) {
+    constexpr uint32_t W = kS4Waves[s4_index(G)];
     const uint32_t steps = a.rows / (64 / (G / 8));
-    const uint32_t blocks = std::min<uint32_t>(2 * compute_units, (steps + kWaves4 - 1) / kWaves4);
+    const uint32_t blocks = static_cast<uint32_t>(gemv_stream4_workgroups(G, compute_units, steps));
     if (plain_epilogue(a))
-        hipLaunchKernelGGL((gemv_stream4<G, false>), dim3(blocks), dim3(256), 0, stream, a, steps);
+        hipLaunchKernelGGL((gemv_stream4<G, false, W>), dim3(blocks), dim3(64 * W), 0, stream, a, steps);
     else
-        hipLaunchKernelGGL((gemv_stream4<G, true>), dim3(blocks), dim3(256), 0, stream, a, steps);
+        hipLaunchKernelGGL((gemv_stream4<G, true, W>), dim3(blocks), dim3(64 * W), 0, stream, a, steps);
 }
 
 hipError_t launch_gemv_stream4(const Product& a, uint32_t compute_units, hipStream_t stream) {
