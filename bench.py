@@ -199,7 +199,7 @@ def run_gemv(S, name, gtype, rows, columns, steps, warmup, rng, copies=None):
     return {"ms_per_step": ms, "bytes": nbytes, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "copies": copies,
             "ms_first_replay": S.last_first, "ms_single_launch": single, "stored": stored, "x": x, "weights": ws,
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": gemv_traffic(name)}}
 
 
 def build_products(S, rng, plan, tokens, gtype=2):
@@ -392,6 +392,20 @@ def gemm_traffic(name, path):
     if path == "SPLIT_F16_MFMA":
         return int(round(b(k["mfma"]) + b(k["prepare_x"])))
     return int(round(b(k["canonical"])))
+
+
+def gemv_traffic(name):
+    """HBM bytes a launch of a c8 decode from the counter runs in
+    profiles/traffic_c8.json (FETCH_SIZE and WRITE_SIZE, KiB a dispatch,
+    scaled as traffic_c2.json's); None for other configs or when absent."""
+    file = os.path.join(ROOT, "profiles", "traffic_c8.json")
+    if not os.path.exists(file):
+        return None
+    t = json.load(open(file))
+    k = t["kernels"].get(name)
+    if k is None:
+        return None
+    return int(round((k["fetch_kib"] * t["fetch_scale"] + k["write_kib"] * t["write_scale"]) * 1024))
 
 
 def run_gather(S, name, gtype, rows, columns, tokens, steps, warmup, rng):
