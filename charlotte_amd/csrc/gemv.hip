@@ -76,8 +76,13 @@ constexpr int batch_of(int span) {
 
 template <uint32_t F, int SPAN, bool XREG, bool FULL, int B>
 __global__ __launch_bounds__(256, kRangesMinBlocks) void gemv_ranges(Product a, uint32_t steps, uint32_t tiles) {
-    __shared__ float partials[kWaves][kWaveRows * kPad];
-    extern __shared__ float4 xs4[];  // x, staged when it is not held in registers
+    // Dynamic LDS: each wave's range sums, then x when it is staged rather
+    // than held in registers. A workgroup is kWaves waves, or one (small
+    // products with x in registers: ranges_waves).
+    extern __shared__ float4 dynamic_lds[];
+    const uint32_t waves_a_block = blockDim.x >> 6;
+    float* const partials = reinterpret_cast<float*>(dynamic_lds);
+    float4* const xs4 = dynamic_lds + waves_a_block * (kWaveRows * kPad / 4);
 
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t half = lane >> 5, r = lane & 31u;
@@ -101,7 +106,7 @@ __global__ __launch_bounds__(256, kRangesMinBlocks) void gemv_ranges(Product a, 
     // rows after, so x's round trip overlaps the weights' and the first
     // decode waits for its own row and x only. (The grid never exceeds the
     // tiles, so every workgroup has a first tile.)
-    const uint32_t first_wave_row = (blockIdx.x * kWaves + wave) * steps * 2;
+    const uint32_t first_wave_row = (blockIdx.x * waves_a_block + wave) * steps * 2;
     load_row(raw[0], first_wave_row, 0);
 
     float xr[XREG ? SPAN * 32 : 1];
@@ -147,10 +152,10 @@ __global__ __launch_bounds__(256, kRangesMinBlocks) void gemv_ranges(Product a, 
 #pragma unroll
     for (int b = 1; b < B; ++b) load_row(raw[b], first_wave_row, b);
 
-    float* mine = partials[wave];
+    float* mine = partials + wave * (kWaveRows * kPad);
     bool loaded = true;  // the first batch already is
     for (uint32_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-        const uint32_t wave_first = (tile * kWaves + wave) * steps * 2;
+        const uint32_t wave_first = (tile * waves_a_block + wave) * steps * 2;
         for (uint32_t step0 = 0; step0 < steps; step0 += B) {
             if (!loaded) {
 #pragma unroll
@@ -536,19 +541,28 @@ static uint32_t resident(K kernel, size_t lds) {
 }
 
 template <uint32_t F, int SPAN, bool XREG, bool FULL, int B>
-static void launch_ranges(const Product& a, uint32_t steps, uint32_t tiles, size_t lds, uint32_t compute_units,
-                          hipStream_t stream) {
+static void launch_ranges(const Product& a, uint32_t steps, uint32_t tiles, uint32_t waves, size_t x_lds,
+                          uint32_t compute_units, hipStream_t stream) {
+    const size_t lds = waves * kWaveRows * kPad * sizeof(float) + x_lds;
     thread_local size_t cached_lds = ~size_t{0};
     thread_local uint32_t per_cu = 1;
-    if (cached_lds != lds) per_cu = resident(gemv_ranges<F, SPAN, XREG, FULL, B>, lds), cached_lds = lds;
+    if (cached_lds != lds) {
+        int blocks = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, gemv_ranges<F, SPAN, XREG, FULL, B>, 64 * waves,
+                                                         lds) != hipSuccess ||
+            blocks < 1)
+            blocks = 1;
+        per_cu = static_cast<uint32_t>(blocks), cached_lds = lds;
+    }
     const dim3 grid(std::min(tiles, per_cu * compute_units));
-    hipLaunchKernelGGL((gemv_ranges<F, SPAN, XREG, FULL, B>), grid, dim3(256), lds, stream, a, steps, tiles);
+    hipLaunchKernelGGL((gemv_ranges<F, SPAN, XREG, FULL, B>), grid, dim3(64 * waves), lds, stream, a, steps, tiles);
 }
 
 // A grid of at most the workgroups the GPU holds at once, each looping over
 // tiles, so no tail round runs part-empty.
 template <uint32_t F, int L, int SPAN, bool XREG, bool FULL>
-static void go_epilogue(const Product& a, uint32_t steps, uint32_t tiles, uint32_t compute_units, hipStream_t stream) {
+static void go_epilogue(const Product& a, uint32_t steps, uint32_t tiles, uint32_t waves, uint32_t compute_units,
+                        hipStream_t stream) {
     // x staged: L = 32, SPAN float4 a thread (range-interleaved); L = 4, x in
     // order with a pad.
     const size_t lds = XREG ? 0
@@ -560,15 +574,15 @@ static void go_epilogue(const Product& a, uint32_t steps, uint32_t tiles, uint32
         constexpr uint32_t most = batch_of<F>(SPAN);
         const uint32_t b = std::min(steps, most);
         if (b == 1) {
-            launch_ranges<F, SPAN, XREG, FULL, 1>(a, steps, tiles, lds, compute_units, stream);
+            launch_ranges<F, SPAN, XREG, FULL, 1>(a, steps, tiles, waves, lds, compute_units, stream);
         } else if constexpr (most >= 2) {
             if (b == 2) {
-                launch_ranges<F, SPAN, XREG, FULL, 2>(a, steps, tiles, lds, compute_units, stream);
+                launch_ranges<F, SPAN, XREG, FULL, 2>(a, steps, tiles, waves, lds, compute_units, stream);
             } else if constexpr (most >= 4) {
                 if (b == 4)
-                    launch_ranges<F, SPAN, XREG, FULL, 4>(a, steps, tiles, lds, compute_units, stream);
+                    launch_ranges<F, SPAN, XREG, FULL, 4>(a, steps, tiles, waves, lds, compute_units, stream);
                 else if constexpr (most >= 8)
-                    launch_ranges<F, SPAN, XREG, FULL, 8>(a, steps, tiles, lds, compute_units, stream);
+                    launch_ranges<F, SPAN, XREG, FULL, 8>(a, steps, tiles, waves, lds, compute_units, stream);
             }
         }
     } else {
@@ -581,11 +595,12 @@ static void go_epilogue(const Product& a, uint32_t steps, uint32_t tiles, uint32
 }
 
 template <uint32_t F, int L, int SPAN, bool XREG>
-static void go(const Product& a, uint32_t steps, uint32_t tiles, uint32_t compute_units, hipStream_t stream) {
+static void go(const Product& a, uint32_t steps, uint32_t tiles, uint32_t waves, uint32_t compute_units,
+               hipStream_t stream) {
     if (plain_epilogue(a))
-        go_epilogue<F, L, SPAN, XREG, false>(a, steps, tiles, compute_units, stream);
+        go_epilogue<F, L, SPAN, XREG, false>(a, steps, tiles, waves, compute_units, stream);
     else
-        go_epilogue<F, L, SPAN, XREG, true>(a, steps, tiles, compute_units, stream);
+        go_epilogue<F, L, SPAN, XREG, true>(a, steps, tiles, waves, compute_units, stream);
 }
 
 template <uint32_t F, int STEPS>
@@ -612,25 +627,25 @@ static hipError_t launch_format(const Product& a, const Plan& plan, uint32_t cus
     }
     if (plan.kernel == kGemvQuarters) {
         if constexpr (!plain_values(F)) {
-            go<F, 4, 9, false>(a, plan.steps, tiles, cus, stream);
+            go<F, 4, 9, false>(a, plan.steps, tiles, plan.waves, cus, stream);
             return hipGetLastError();
         }
         return hipErrorInvalidValue;
     }
     switch (plan.span) {
-        case 1: go<F, 32, 1, true>(a, plan.steps, tiles, cus, stream); break;
-        case 2: go<F, 32, 2, true>(a, plan.steps, tiles, cus, stream); break;
+        case 1: go<F, 32, 1, true>(a, plan.steps, tiles, plan.waves, cus, stream); break;
+        case 2: go<F, 32, 2, true>(a, plan.steps, tiles, plan.waves, cus, stream); break;
         case 3:
-            if constexpr (F != kF32) go<F, 32, 3, true>(a, plan.steps, tiles, cus, stream);
+            if constexpr (F != kF32) go<F, 32, 3, true>(a, plan.steps, tiles, plan.waves, cus, stream);
             else return hipErrorInvalidValue;
             break;
         default:
             // x staged in LDS: the quantized formats only (the others take
             // the chunked kernel past three groups a lane).
             if constexpr (!plain_values(F)) {
-                if (plan.span == 4) go<F, 32, 4, false>(a, plan.steps, tiles, cus, stream);
-                else if (plan.span == 6) go<F, 32, 6, false>(a, plan.steps, tiles, cus, stream);
-                else if (plan.span == 8) go<F, 32, 8, false>(a, plan.steps, tiles, cus, stream);
+                if (plan.span == 4) go<F, 32, 4, false>(a, plan.steps, tiles, plan.waves, cus, stream);
+                else if (plan.span == 6) go<F, 32, 6, false>(a, plan.steps, tiles, plan.waves, cus, stream);
+                else if (plan.span == 8) go<F, 32, 8, false>(a, plan.steps, tiles, plan.waves, cus, stream);
                 else return hipErrorInvalidValue;
             } else {
                 return hipErrorInvalidValue;
@@ -744,8 +759,15 @@ bool plan_gemv(const Product& a, uint32_t format, uint32_t compute_units, bool l
             for (uint32_t st = steps / 2; st >= 8; st /= 2)
                 if (makespan(st) * 100 < makespan(best) * 97) best = st;
         plan->steps = best;
+        // A small product with x in registers (under 2^20 groups: one
+        // workgroup a CU at most) runs its waves as workgroups of one: they
+        // spread over every CU rather than four to a CU on three quarters of
+        // them (Q4_0 3,072 x 1,024: 4.03 -> 3.81 us; the Qwen3 0.6B decode
+        // step 633 -> 589 us). A large one keeps four a workgroup (the Q4_0
+        // head of 151,936 rows: 23.0 against 24.1 us).
+        if (plan->xreg && per_cu == 1) plan->waves = 1;
     }
-    plan->tile_rows = kWaves * plan->steps * rows_a_step;
+    plan->tile_rows = plan->waves * plan->steps * rows_a_step;
     plan->tiles = (a.rows + plan->tile_rows - 1) / plan->tile_rows;
     plan->workgroups = plan->tiles;  // at most; the launch caps it at what the GPU holds
     return true;

@@ -37,6 +37,7 @@ struct Plan {
     uint32_t lanes = 0;        // decode: lanes a row
     uint32_t span = 0;         // decode: the most groups a lane holds
     uint32_t steps = 0;        // decode: steps a wave
+    uint32_t waves = 4;        // decode (L = 32): waves a workgroup, 4 or 1
     uint32_t tile_tokens = 0;  // prefill: tokens a workgroup's tile (decode: 1)
     uint32_t tile_rows = 0;    // product rows a workgroup's tile
     uint32_t token_tiles = 0, row_tiles = 0;

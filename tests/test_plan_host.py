@@ -107,11 +107,20 @@ def test_qwen_and_llama_heads_are_the_streamed_decode_of_k_1024_and_2048(shapes,
     assert p.kernel == K.GEMV_STREAM8 and p.canonical and p.tile_rows == 64 // (columns // 256)
 
 
-def test_c1_is_the_reference_mapping_in_one_workgroup_a_cu(shapes):
+def test_c1_is_the_reference_mapping_in_workgroups_of_one_wave(shapes):
     p = mm.plan_launch(_write(shapes(Q4_0, 3072, 1024)), 1)
     assert (p.kernel, p.lanes_a_row, p.groups_a_lane) == (K.GEMV_RANGES, 32, 1)
-    # Two steps a wave: 4 waves x 2 steps x 2 rows = 16 rows a workgroup, 192 of them.
-    assert (p.steps_a_wave, p.tile_rows, p.tiles) == (2, 16, 192)
+    # Two steps a wave (the fewest that would bring four-wave workgroups down to
+    # one a CU), the waves as workgroups of one: 2 steps x 2 rows = 4 rows a
+    # workgroup, 768 of them over every CU.
+    assert (p.steps_a_wave, p.tile_rows, p.tiles) == (2, 4, 768)
+    # x staged in LDS (K past 3,072) or 2^20 groups and more: four waves a workgroup
+    p = mm.plan_launch(_write(shapes(Q4_0, 3001, 4096)), 1)  # 3,001 rows: not whole streamed steps
+    assert p.kernel == K.GEMV_RANGES and p.tile_rows == 4 * p.steps_a_wave * 2
+    p = mm.plan_launch(_write(shapes(Q4_0, 32768, 1024)), 1)
+    assert p.kernel == K.GEMV_RANGES and p.tile_rows == 4 * p.steps_a_wave * 2
+    p = mm.plan_launch(_write(shapes(Q4_0, 32767, 1024)), 1)
+    assert p.kernel == K.GEMV_RANGES and p.tile_rows == p.steps_a_wave * 2
 
 
 def test_large_decodes_balance_their_rounds_of_tiles(shapes):
