@@ -157,16 +157,22 @@ def test_q4_0_k_2048_to_8192_in_whole_steps_is_the_streamed_decode(shapes, colum
     # the INT8_LIMBS path is Q6_K's: Q4_0 stays canonical
     limbs = mm.plan_launch(_write(shapes(Q4_0, rows, columns)), 1, mm.Target(256, gemv_path=mm.GemvPath.INT8_LIMBS))
     assert limbs.kernel == K.GEMV_STREAM4 and limbs.canonical
-    w = shapes(Q4_0, 1024, columns)
+    w = shapes(Q4_0, 65536, columns)
+    big = 2**20 // (columns // 32)  # rows of 2^20 groups: the smallest product streamed
     # a member starting inside a step, or not whole steps long: the reference mapping
-    assert mm.plan_launch(mm.MatmulLaunch([mm.Member(w, row_offset=1, rows=step_rows)], X, [Y0]), 1).kernel == \
+    assert mm.plan_launch(mm.MatmulLaunch([mm.Member(w, row_offset=1, rows=big)], X, [Y0]), 1).kernel == \
         K.GEMV_RANGES
-    assert mm.plan_launch(mm.MatmulLaunch([mm.Member(w, rows=step_rows + 1)], X, [Y0]), 1).kernel == K.GEMV_RANGES
-    three = [mm.Member(w, rows=256), mm.Member(w, row_offset=256, rows=64), mm.Member(w, row_offset=512, rows=64)]
+    assert mm.plan_launch(mm.MatmulLaunch([mm.Member(w, rows=big + 1)], X, [Y0]), 1).kernel == K.GEMV_RANGES
+    # under 2^20 groups: the reference mapping's one-wave workgroups
+    p = mm.plan_launch(mm.MatmulLaunch([mm.Member(w, rows=big - step_rows)], X, [Y0]), 1)
+    assert p.kernel == K.GEMV_RANGES
+    three = [mm.Member(w, rows=big // 2), mm.Member(w, row_offset=big // 2, rows=big // 4),
+             mm.Member(w, row_offset=3 * big // 4, rows=big // 4)]
     assert mm.plan_launch(mm.MatmulLaunch(three, X, [Y0, Y1, Y2], epilogue=mm.Epilogue.QKV), 1).kernel == \
         K.GEMV_STREAM4
     # a gated product interleaves its members' rows: the reference mapping
-    gated = mm.MatmulLaunch([mm.Member(w), mm.Member(w)], X, [Y0], epilogue=mm.Epilogue.GatedActivation, out_width=1024)
+    gated = mm.MatmulLaunch([mm.Member(w), mm.Member(w)], X, [Y0], epilogue=mm.Epilogue.GatedActivation,
+                            out_width=65536)
     assert mm.plan_launch(gated, 1).kernel == K.GEMV_RANGES
     # other quantized formats at these K: the reference mapping
     assert mm.plan_launch(_write(shapes(mm.TensorType.Q4_1, 1024, columns)), 1).kernel == K.GEMV_RANGES
