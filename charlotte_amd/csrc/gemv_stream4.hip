@@ -16,10 +16,8 @@
 // Mapping: every lane owns 8 groups (128 code bytes, 16 scale bytes): L = G /
 // 8 lanes a row (8, 16, 32), 64 / L rows a step (8, 4, 2). Lane j of a row
 // owns ranges (32 / L) j .. (32 / L)(j + 1) - 1, G / 32 groups each. Its
-// range sums are chained over the row's lanes in order — ((0 + sums of lane
-// 0) + sums of lane 1) + ... — by DPP row shifts for L = 8 and 16; for L = 32
-// the 32 sums go through LDS and one lane adds them in order. The bits are
-// every other kernel's.
+// range sums go to the wave's LDS, 16 rows' at a time, and lane t then adds
+// row t's 32 sums in order from zero. The bits are every other kernel's.
 #include <algorithm>
 
 #include "decode.hpp"
