@@ -657,8 +657,9 @@ static hipError_t launch_format(const Product& a, const Plan& plan, uint32_t cus
 // The decode's kernel and shape:
 //   - Q6_K at K = 1,152, 1,024 or 2,048 in whole steps: the LDS-streamed
 //     kernels (the INT8_LIMBS form there when asked);
-//   - Q4_0 at K = 2,048, 4,096 or 8,192 in whole steps: the LDS-streamed
-//     kernel (the INT8_LIMBS form is Q6_K's alone);
+//   - Q4_0 at K = 1,024, 2,048, 4,096 or 8,192, 2^20 groups or more, in
+//     whole steps: the LDS-streamed kernel (the INT8_LIMBS form is Q6_K's
+//     alone);
 //   - quantized K = 1,152 otherwise: 4 lanes a row, 9 groups each;
 //   - other K up to 8,192: the reference's 32 lanes a row, x in registers
 //     while a lane's slice is at most 3 groups, else staged whole in LDS

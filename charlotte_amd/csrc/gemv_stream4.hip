@@ -1,6 +1,6 @@
-// Decode of Q4_0 rows of K = 2,048, 4,096 and 8,192 (G = 64, 128, 256
-// groups) — down projections and the wide products of larger models —
-// streamed through LDS.
+// Decode of Q4_0 rows of K = 1,024, 2,048, 4,096 and 8,192 (G = 32, 64, 128,
+// 256 groups) — vocabulary heads, down projections and the wide products of
+// larger models — streamed through LDS.
 //
 // Why: the reference's mapping (gemv.hip, lane r of a half-wave owns range
 // r) gives a lane G / 32 contiguous groups, so past K = 1,024 each load
@@ -14,10 +14,11 @@
 // does for Q6_K.
 //
 // Mapping: every lane owns 8 groups (128 code bytes, 16 scale bytes): L = G /
-// 8 lanes a row (8, 16, 32), 64 / L rows a step (8, 4, 2). Lane j of a row
-// owns ranges (32 / L) j .. (32 / L)(j + 1) - 1, G / 32 groups each. Its
-// range sums go to the wave's LDS, 16 rows' at a time, and lane t then adds
-// row t's 32 sums in order from zero. The bits are every other kernel's.
+// 8 lanes a row (4, 8, 16, 32), 64 / L rows a step (16, 8, 4, 2). Lane j of
+// a row owns ranges (32 / L) j .. (32 / L)(j + 1) - 1, G / 32 groups each.
+// Its range sums wait in the wave's LDS for a batch of steps, and lane t
+// then adds row t's 32 sums in order from zero. The bits are every other
+// kernel's.
 #include <algorithm>
 
 #include "decode.hpp"
@@ -29,10 +30,16 @@ namespace chm {
 
 namespace {
 
-// Waves a workgroup and workgroups a CU, by G = 64, 128, 256.
-constexpr uint32_t kS4Waves[3] = {4, 4, 4};
-constexpr uint32_t kS4Blocks[3] = {2, 2, 2};
-constexpr uint32_t s4_index(uint32_t G) { return G == 64 ? 0 : G == 128 ? 1 : 2; }
+// Waves a workgroup and workgroups a CU, by G = 32, 64, 128, 256.
+constexpr uint32_t kS4Waves[4] = {4, 4, 4, 4};
+constexpr uint32_t kS4Blocks[4] = {2, 2, 2, 2};
+constexpr uint32_t s4_index(uint32_t G) { return G == 32 ? 0 : G == 64 ? 1 : G == 128 ? 2 : 3; }
+// Rows whose range sums wait in LDS for one ordered pass, by G: as many as
+// two workgroups a CU leave LDS for beside the stage and x (64 rows' sums, 8.4
+// KB a wave, at G = 32 and 64; 32 at 128; 16 at 256, where x takes 33 KB).
+// Fewer, fuller passes: 131,072 x 2,048 34.0 -> 31.2 us, 262,144 x 1,024
+// 34.4 -> 31.8 us against 16 rows a pass.
+constexpr uint32_t kSumRows[4] = {64, 64, 32, 16};
 constexpr uint32_t kCodeChunks = 512, kScaleChunks = 64;  // 16-byte chunks a step: 8 KB codes, 1 KB scales
 constexpr uint32_t kSlice4 = 65;                          // x slice stride in float4: 8 groups of 8, one of padding
 
@@ -53,8 +60,9 @@ __global__ __launch_bounds__(64 * W) void gemv_stream4(Product a, uint32_t steps
     __shared__ u32x4s_t codes_a[W][kCodeChunks];
     __shared__ u32x4s_t scales_a[W][kScaleChunks];
     __shared__ u32x4s_t x_stage[kSlice4 * L];
-    constexpr uint32_t kBatch = 16 / kRows;  // steps whose range sums wait for one ordered pass
-    __shared__ float sums_a[W][33 * 16];    // 16 rows' range sums, a row of 32 and one of padding  // a step's range sums, a row of 32 and one of padding
+    constexpr uint32_t kSums = kSumRows[s4_index(G)];
+    constexpr uint32_t kBatch = kSums / kRows;  // steps whose range sums wait for one ordered pass
+    __shared__ float sums_a[W][33 * kSums];     // a row's 32 range sums and one of padding
     const float4* const xs = reinterpret_cast<const float4*>(x_stage);
 
     const uint32_t lane = threadIdx.x & 63u;
@@ -130,7 +138,7 @@ __global__ __launch_bounds__(64 * W) void gemv_stream4(Product a, uint32_t steps
     };
     // Every kBatch steps (and after the last): lane t adds row t's 32 sums in
     // order from zero — ((0 + s0) + s1) + ... + s31, the order of
-    // matmul.h:34-50 — and emits it. The serial adds run once for 16 rows
+    // matmul.h:34-50 — and emits it. The serial adds run once for kSums rows
     // instead of once a step. The sums are this wave's own: a wave barrier
     // orders the writes before the reads, and the reads before the next
     // batch's writes. `first` is the batch's first step; its steps are
@@ -198,15 +206,15 @@ __global__ __launch_bounds__(64 * W) void gemv_stream4(Product a, uint32_t steps
     }
 }
 
-// Whether this kernel takes the product: Q4_0, K = 2,048, 4,096 or 8,192,
-// 2^20 groups or more, every member's rows and first row a whole number of
+// Whether this kernel takes the product: Q4_0, K = 1,024, 2,048, 4,096 or
+// 8,192, 2^20 groups or more, every member's rows and first row a whole number of
 // steps (so a step lies in one member), not gated (a gated product
 // interleaves its members' rows). A smaller product is bound by dispatch and
 // one memory round trip, and goes to the 32-lane mapping's one-wave
 // workgroups, which spread over every CU (Qwen3 0.6B's o projection, 1,024 x
 // 2,048: its decode step 590 -> 559 us).
 bool gemv_stream4_takes(const Product& a, uint32_t format) {
-    if (format != kQ4_0 || (a.groups != 64 && a.groups != 128 && a.groups != 256)) return false;
+    if (format != kQ4_0 || (a.groups != 32 && a.groups != 64 && a.groups != 128 && a.groups != 256)) return false;
     if (static_cast<uint64_t>(a.rows) * a.groups < (1u << 20)) return false;
     const uint32_t rows = 64 / (a.groups / 8);
     for (uint32_t m = 0; m < a.members; ++m)
@@ -232,6 +240,7 @@ static void go4(const Product& a, uint32_t compute_units, hipStream_t stream) {
 
 hipError_t launch_gemv_stream4(const Product& a, uint32_t compute_units, hipStream_t stream) {
     switch (a.groups) {
+        case 32: go4<32>(a, compute_units, stream); break;
         case 64: go4<64>(a, compute_units, stream); break;
         case 128: go4<128>(a, compute_units, stream); break;
         case 256: go4<256>(a, compute_units, stream); break;

@@ -1,4 +1,4 @@
-"""The streamed Q4_0 decode at K = 2,048, 4,096 and 8,192 (gemv_stream4.hip)
+"""The streamed Q4_0 decode at K = 1,024, 2,048, 4,096 and 8,192 (gemv_stream4.hip)
 on the GPU: the oracle's bits at every shape it takes — from its smallest
 product, 2^20 groups, to 32,768 x 8,192 — through members at row offsets,
 epilogues and the head's last token; smaller products, and rows that are
@@ -53,11 +53,11 @@ def _smallest(columns):
     return 2**20 // (columns // 32)
 
 
-# Steps are 8, 4 and 2 rows at K = 2,048, 4,096 and 8,192; the smallest
-# streamed products are 16,384, 8,192 and 4,096 rows.
-SHAPES = [(16384, 2048), (16392, 2048), (8192, 4096), (8196, 4096), (14336, 4096), (4096, 8192), (4098, 8192),
+# Steps are 16, 8, 4 and 2 rows at K = 1,024, 2,048, 4,096 and 8,192; the
+# smallest streamed products are 32,768, 16,384, 8,192 and 4,096 rows.
+SHAPES = [(32768, 1024), (32784, 1024), (151936, 1024), (262144, 1024), (16384, 2048), (16392, 2048), (8192, 4096), (8196, 4096), (14336, 4096), (4096, 8192), (4098, 8192),
           (32768, 8192)]
-SMALL = [(8, 2048), (24, 2048), (8192, 2048), (16376, 2048), (4, 4096), (4100, 4096), (2, 8192), (6, 8192),
+SMALL = [(16, 1024), (32752, 1024), (8, 2048), (24, 2048), (8192, 2048), (16376, 2048), (4, 4096), (4100, 4096), (2, 8192), (6, 8192),
          (4094, 8192)]
 
 
@@ -89,7 +89,7 @@ def test_products_under_2_20_groups_take_the_reference_mapping(oracle, run, rows
     w.free()
 
 
-@pytest.mark.parametrize("rows,columns", [(16388, 2048), (8194, 4096), (4097, 8192)])
+@pytest.mark.parametrize("rows,columns", [(32776, 1024), (16388, 2048), (8194, 4096), (4097, 8192)])
 def test_rows_not_whole_steps_take_the_reference_mapping(oracle, run, rows, columns):
     from charlotte_amd import matmul as mm
     from tests.support.gpu import bits_equal, first_difference
@@ -103,7 +103,7 @@ def test_rows_not_whole_steps_take_the_reference_mapping(oracle, run, rows, colu
     w.free()
 
 
-@pytest.mark.parametrize("columns", [2048, 4096, 8192])
+@pytest.mark.parametrize("columns", [1024, 2048, 4096, 8192])
 def test_stream4_members_epilogues_and_the_head(oracle, run, columns):
     """QKV members — one of them rows 64..191 of a larger weight — at their
     output rows, Write with clip, bias and activation, and the last of three
@@ -141,7 +141,7 @@ def test_stream4_members_epilogues_and_the_head(oracle, run, columns):
         w.free()
 
 
-@pytest.mark.parametrize("rows,columns", [(16384, 2048), (14336, 4096), (32768, 8192)])
+@pytest.mark.parametrize("rows,columns", [(151936, 1024), (16384, 2048), (14336, 4096), (32768, 8192)])
 def test_stream4_decode_matches_prefill(run, rows, columns):
     """A token decoded alone and the same token prefilled in a step of 5: the
     same bits (the consistency the reference tracks), at full size."""

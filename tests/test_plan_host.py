@@ -117,17 +117,17 @@ def test_c1_is_the_reference_mapping_in_workgroups_of_one_wave(shapes):
     # x staged in LDS (K past 3,072) or 2^20 groups and more: four waves a workgroup
     p = mm.plan_launch(_write(shapes(Q4_0, 3001, 4096)), 1)  # 3,001 rows: not whole streamed steps
     assert p.kernel == K.GEMV_RANGES and p.tile_rows == 4 * p.steps_a_wave * 2
-    p = mm.plan_launch(_write(shapes(Q4_0, 32768, 1024)), 1)
+    p = mm.plan_launch(_write(shapes(Q4_0, 32776, 1024)), 1)  # 32,776 rows: not whole streamed steps
     assert p.kernel == K.GEMV_RANGES and p.tile_rows == 4 * p.steps_a_wave * 2
     p = mm.plan_launch(_write(shapes(Q4_0, 32767, 1024)), 1)
     assert p.kernel == K.GEMV_RANGES and p.tile_rows == p.steps_a_wave * 2
 
 
 def test_large_decodes_balance_their_rounds_of_tiles(shapes):
-    """A Q4_0 head of 151,936 rows: at 32 steps a wave, 594 tiles of 256 rows
+    """A Q4_1 head of 151,936 rows: at 32 steps a wave, 594 tiles of 256 rows
     on 512 resident workgroups leave 82 with a second round; 8 steps give
     2,374 tiles of 64 rows, 5 rounds, 320 rows on the busiest."""
-    p = mm.plan_launch(_write(shapes(Q4_0, 151936, 1024)), 1)
+    p = mm.plan_launch(_write(shapes(mm.TensorType.Q4_1, 151936, 1024)), 1)
     assert (p.kernel, p.steps_a_wave, p.tile_rows, p.tiles) == (K.GEMV_RANGES, 8, 64, 2374)
     # One round already balanced: left as it is.
     p = mm.plan_launch(_write(shapes(Q8_0, 32768, 8192)), 1)
@@ -148,8 +148,8 @@ def test_decode_up_to_k_8192_stages_x_whole(shapes, columns, span):
     assert (p.kernel, p.groups_a_lane) == (K.GEMV_RANGES, span)
 
 
-@pytest.mark.parametrize("columns,step_rows", [(2048, 8), (4096, 4), (8192, 2)])
-def test_q4_0_k_2048_to_8192_in_whole_steps_is_the_streamed_decode(shapes, columns, step_rows):
+@pytest.mark.parametrize("columns,step_rows", [(1024, 16), (2048, 8), (4096, 4), (8192, 2)])
+def test_q4_0_k_1024_to_8192_in_whole_steps_is_the_streamed_decode(shapes, columns, step_rows):
     rows = 32768 * 8192 // columns
     p = mm.plan_launch(_write(shapes(Q4_0, rows, columns)), 1)
     assert (p.kernel, p.canonical, p.lanes_a_row, p.groups_a_lane) == (K.GEMV_STREAM4, True, columns // 256, 8)
