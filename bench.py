@@ -20,6 +20,10 @@ A step is one pass of the hot path over one batch of synthetic input:
   c7  the embedding gather from Qwen3-0.6B's Q6_K table (151936x1024): a
       512-token step and a decode step
   c8  large Q4_0 decodes: a Q4_0 LM head 151936x1024 and a 32768x8192 product
+c2 and c8 also time a read floor: the same bytes read by the streamed decodes'
+copy (global_load_lds_dwordx4, 9 KB a wave a step) with nothing decoded, the
+practical ceiling under the 8 TB/s peak; frac_of_read_floor is the decode's
+rate over it.
 Every row carries a roofline in the unit its kernel runs on: HBM GB/s for the
 decodes; TFLOP/s for the prefills, the VALU tile against the FP32 peak, the
 matrix cores against the dense FP16 peak and this design's useful half of it.
@@ -200,6 +204,33 @@ def run_gemv(S, name, gtype, rows, columns, steps, warmup, rng, copies=None):
             "ms_first_replay": S.last_first, "ms_single_launch": single, "stored": stored, "x": x, "weights": ws,
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": gemv_traffic(name)}}
+
+
+def run_read_floor(S, name, nbytes, copies, steps, warmup):
+    """The same bytes read and nothing else (harness chx_read: the LDS-streamed
+    decodes' copy, 9 KB a wave a step, with no decode), over `copies` buffers
+    rotated as the decode's weight copies are: the rate the decode would reach
+    were its arithmetic free — the practical ceiling under the 8 TB/s peak."""
+    hx = S.hx
+    nbytes = nbytes // 1024 * 1024
+    bufs = [S.buffer(nbytes=nbytes) for _ in range(copies)]
+    sink = S.buffer(nbytes=hx.read_sink_bytes())
+    state = {"i": 0}
+
+    def body():
+        b = bufs[state["i"] % len(bufs)]
+        state["i"] += 1
+        hx.read(b.ptr, nbytes, sink.ptr, sink.nbytes, S.stream)
+
+    ms = S.time_graph(body, steps, warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"{name}: {ms * 1e3:.2f} us/launch, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s), "
+        f"{nbytes} bytes read, nothing decoded")
+    for b in bufs + [sink]:
+        b.free()
+        S.buffers.remove(b)
+    return {"kernel": "harness read_kernel: global_load_lds_dwordx4, 9 KB a wave a step, no decode",
+            "bytes": nbytes, "ms_per_step": ms, "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def build_products(S, rng, plan, tokens, gtype=2):
@@ -596,6 +627,10 @@ def main():
             out["c2_limbs"] = {k: v for k, v in r.items() if k not in ("stored", "x", "weights")}
             out["c2_limbs"]["path"] = "INT8_LIMBS: within 1e-5 of the canonical order, not its bits"
             out["c2_limbs"]["roofline"]["traffic"] = measured_traffic(limbs=True)
+            floor = run_read_floor(S, "c2_read_floor", c2["bytes"], c2["copies"], max(args.steps, 20), args.warmup)
+            out["c2_read_floor"] = floor
+            for r in (c2, out["c2_limbs"]):
+                r["frac_of_read_floor"] = round(r["GB/s"] / floor["GB/s"], 4)
         if "c1" in only:
             r = run_gemv(S, "c1", 2, 3072, 1024, max(args.steps, 100), args.warmup, np.random.default_rng(1))
             out["c1"] = {k: v for k, v in r.items() if k not in ("stored", "x", "weights")}
@@ -605,6 +640,10 @@ def main():
             for tag, rows, columns in (("c8_q4_0_head", 151936, 1024), ("c8_q4_0_wide", 32768, 8192)):
                 r = run_gemv(S, tag, 2, rows, columns, max(args.steps, 20), args.warmup, np.random.default_rng(8))
                 out[tag] = {k: v for k, v in r.items() if k not in ("stored", "x", "weights")}
+                floor = run_read_floor(S, tag + "_read_floor", r["bytes"], r["copies"], max(args.steps, 20),
+                                       args.warmup)
+                out[tag]["read_floor"] = floor
+                out[tag]["frac_of_read_floor"] = round(r["GB/s"] / floor["GB/s"], 4)
         if "c3" in only:
             out["c3"] = run_c3(S, max(args.steps // 4, 3), args.warmup, rng)
             out["c3_unfused"] = run_c3(S, max(args.steps // 4, 3), args.warmup, rng, fused=False)
@@ -659,6 +698,8 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(c2["GB/s"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(c2["frac"], 4), "traffic": measured_traffic()},
             "cpu_baseline": cpu,
+            "read_floor": out.get("c2_read_floor"),
+            "frac_of_read_floor": c2.get("frac_of_read_floor"),
         })
     result["configs"] = out
     print(json.dumps(result), flush=True)

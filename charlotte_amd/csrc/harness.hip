@@ -6,7 +6,11 @@
 //     it to the CPU dequant bit for bit (tests/gpu/support/unpack.h:30-109's
 //     role);
 //   chx_copy — a plain copy of known size, the yardstick rocprofv3's
-//     FETCH_SIZE / WRITE_SIZE counters are scaled by.
+//     FETCH_SIZE / WRITE_SIZE counters are scaled by;
+//   chx_read — a streaming read of known size and nothing else, copied a
+//     9 KB step a wave at a time into LDS by global_load_lds_dwordx4 as the
+//     LDS-streamed decodes copy their weights: the rate a decode of the same
+//     bytes could reach were its arithmetic free.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -35,6 +39,34 @@ __global__ void copy_kernel(const float4* __restrict__ src, float4* __restrict__
 }
 
 __global__ void null_kernel() {}
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_void_t;
+constexpr uint32_t kReadChunks = 9;  // 1 KB chunks a step: 9 KB, a streamed Q4_0 step's size
+constexpr uint32_t kReadWaves = 4;
+
+// Each wave copies steps of kReadChunks 1 KB chunks into its own LDS stage,
+// one step in flight, and waits for it; steps are grid-strided. `sink`
+// takes one word a thread from the stage at the end, so the copies have a
+// reader.
+__global__ __launch_bounds__(64 * kReadWaves) void read_kernel(const uint8_t* src, uint64_t chunks, uint32_t* sink) {
+    __shared__ u32x4_t stage[kReadWaves][kReadChunks * 64];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    const uint64_t steps = (chunks + kReadChunks - 1) / kReadChunks;
+    for (uint64_t s = static_cast<uint64_t>(blockIdx.x) * kReadWaves + wave; s < steps;
+         s += static_cast<uint64_t>(gridDim.x) * kReadWaves) {
+#pragma unroll
+        for (uint32_t i = 0; i < kReadChunks; ++i) {
+            const uint64_t c = s * kReadChunks + i;
+            if (c < chunks)
+                __builtin_amdgcn_global_load_lds(src + 1024 * c + 16 * lane, (lds_void_t)(stage[wave] + 64 * i), 16, 0,
+                                                 0);
+        }
+        __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));  // vmcnt(0)
+    }
+    __syncthreads();
+    sink[static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = stage[wave][lane].x;
+}
 
 }  // namespace
 
@@ -141,6 +173,29 @@ int chx_copy(const void* src, void* dst, uint64_t bytes, void* s) {
     const uint32_t blocks = static_cast<uint32_t>(std::min<uint64_t>((n + 255) / 256, 65536));
     hipLaunchKernelGGL(copy_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(s),
                        static_cast<const float4*>(src), static_cast<float4*>(dst), n);
+    return hipGetLastError();
+}
+
+// Reads `bytes` (whole KB, 16-byte aligned) at `src` with read_kernel on
+// two workgroups of four waves a CU; `sink` holds a word a thread
+// (chx_read_sink_bytes).
+int chx_read_sink_bytes(uint64_t* bytes) {
+    int device = 0, cus = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess) return e;
+    *bytes = static_cast<uint64_t>(2 * cus) * 64 * kReadWaves * 4;
+    return hipSuccess;
+}
+
+int chx_read(const void* src, uint64_t bytes, void* sink, uint64_t sink_bytes, void* s) {
+    uint64_t need = 0;
+    const int e = chx_read_sink_bytes(&need);
+    if (e != hipSuccess) return e;
+    if (bytes % 1024 != 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0 || sink_bytes < need) return hipErrorInvalidValue;
+    const uint32_t blocks = static_cast<uint32_t>(need / (64 * kReadWaves * 4));
+    hipLaunchKernelGGL(read_kernel, dim3(blocks), dim3(64 * kReadWaves), 0, static_cast<hipStream_t>(s),
+                       static_cast<const uint8_t*>(src), bytes / 1024, static_cast<uint32_t*>(sink));
     return hipGetLastError();
 }
 

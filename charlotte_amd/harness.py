@@ -40,6 +40,8 @@ _SIGS = {
     "chx_unpack": (_c.c_int, [_c.c_uint32, _c.c_void_p, _c.c_uint64, _c.c_uint64, _c.c_void_p, _c.c_void_p]),
     "chx_copy": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
     "chx_null": (_c.c_int, [_c.c_void_p]),
+    "chx_read_sink_bytes": (_c.c_int, [_c.POINTER(_c.c_uint64)]),
+    "chx_read": (_c.c_int, [_c.c_void_p, _c.c_uint64, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
 }
 
 
@@ -183,6 +185,19 @@ def unpack(gguf_type, piece_ptr, blocks_in_piece, groups, out_ptr, stream=None):
 
 def copy(src_ptr, dst_ptr, nbytes, stream=None):
     check(lib.chx_copy(src_ptr, dst_ptr, nbytes, stream.handle if isinstance(stream, Stream) else stream), "copy")
+
+
+def read_sink_bytes():
+    n = _c.c_uint64()
+    check(lib.chx_read_sink_bytes(_c.byref(n)), "read sink bytes")
+    return n.value
+
+
+def read(src_ptr, nbytes, sink_ptr, sink_bytes, stream=None):
+    """A streaming read of nbytes (whole KB) and nothing else: the copy
+    pattern of the LDS-streamed decodes with their arithmetic taken away."""
+    check(lib.chx_read(src_ptr, nbytes, sink_ptr, sink_bytes, stream.handle if isinstance(stream, Stream) else stream),
+          "read")
 
 
 def null(stream=None):
