@@ -312,8 +312,62 @@ def run_c3(S, steps, warmup, rng, fused=True):
            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
     if fused:
+        out["floors"] = c3_floors(S, launches, steps, warmup)
         out.update(decode_matches_prefill(S, launches, xs, rng))
     return out
+
+
+def c3_floors(S, launches, steps, warmup):
+    """Two floors under a decode step's launches, each timed as a graph of as
+    many launches as the step: `launch_us`, an empty kernel of one workgroup
+    a launch (what launching costs); `memory_us`, each product's bytes read
+    in its own launch shape with nothing decoded — the 32-lane products'
+    one-wave workgroups (chx_touch: as many waves as the plan's, the
+    product's stored bytes split among them), the streamed products by the
+    streamed copy (chx_read). Reads walk one buffer longer than the MALL, a
+    product's bytes after the last's, as the step's weights do."""
+    from charlotte_amd import synthetic
+
+    hx, mm = S.hx, S.mm
+    parts = []
+    for m in launches:
+        p = mm.plan_launch(m, 1)
+        nbytes = sum(synthetic.stored_bytes(int(x.weight.type), x.rows or x.weight.rows, x.weight.columns)
+                     for x in m.members)
+        if p.kernel in (mm.Kernel.GEMV_STREAM, mm.Kernel.GEMV_STREAM8, mm.Kernel.GEMV_STREAM4):
+            parts.append(("read", nbytes // 1024 * 1024, 0))
+        else:
+            waves = p.tile_rows // (p.steps_a_wave * (64 // p.lanes_a_row)) * min(p.tiles, p.workgroups)
+            kib = max(1, nbytes // (waves * 1024))
+            waves = min(waves, nbytes // (kib * 1024))
+            parts.append(("touch", waves, kib))
+    total = sum(a if k == "read" else a * c * 1024 for k, a, c in parts)
+    buf = S.buffer(nbytes=max(total, 2 * MALL_BYTES) + (1 << 20))
+    sink_bytes = max(hx.read_sink_bytes(), 64 * 4 * max(a for k, a, c in parts if k == "touch"))
+    sink = S.buffer(nbytes=sink_bytes)
+
+    def memory():
+        at = 0
+        for k, a, c in parts:
+            if k == "read":
+                hx.read(buf.ptr + at, a, sink.ptr, sink_bytes, S.stream)
+                at += a
+            else:
+                hx.touch(buf.ptr + at, a, c, sink.ptr, sink_bytes, S.stream)
+                at += a * c * 1024
+
+    def empty():
+        for _ in parts:
+            hx.null(S.stream)
+
+    launch_ms = S.time_graph(empty, steps, warmup)
+    memory_ms = S.time_graph(memory, steps, warmup)
+    log(f"c3 floors: {len(parts)} empty launches {launch_ms * 1e3:.1f} us; the products' reads alone "
+        f"{memory_ms * 1e3:.1f} us ({total / 1e6:.1f} MB)")
+    for b in (buf, sink):
+        b.free()
+        S.buffers.remove(b)
+    return {"launch_us": round(launch_ms * 1e3, 1), "memory_us": round(memory_ms * 1e3, 1), "memory_bytes": total}
 
 
 def decode_matches_prefill(S, launches, xs, rng, tokens=4):

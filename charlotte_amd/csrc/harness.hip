@@ -10,7 +10,10 @@
 //   chx_read — a streaming read of known size and nothing else, copied a
 //     9 KB step a wave at a time into LDS by global_load_lds_dwordx4 as the
 //     LDS-streamed decodes copy their weights: the rate a decode of the same
-//     bytes could reach were its arithmetic free.
+//     bytes could reach were its arithmetic free;
+//   chx_touch — one-wave workgroups that each read a few KB and write a
+//     word: a small decode's dispatch and memory round trip with its
+//     arithmetic, reduction and epilogue taken away.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -66,6 +69,24 @@ __global__ __launch_bounds__(64 * kReadWaves) void read_kernel(const uint8_t* sr
     }
     __syncthreads();
     sink[static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = stage[wave][lane].x;
+}
+
+// Wave w (a workgroup of one) reads `kib` 1 KB runs from src + w * kib KB,
+// 16 bytes a lane a run, eight runs' loads issued before any is used, and
+// writes one word a lane.
+__global__ __launch_bounds__(64) void touch_kernel(const u32x4_t* src, uint32_t kib, uint32_t* sink) {
+    const u32x4_t* p = src + static_cast<uint64_t>(blockIdx.x) * kib * 64 + threadIdx.x;
+    uint32_t acc = 0;
+    for (uint32_t i = 0; i < kib; i += 8) {
+        u32x4_t v[8];
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j)
+            if (i + j < kib) v[j] = p[64 * (i + j)];
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j)
+            if (i + j < kib) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    }
+    sink[static_cast<uint64_t>(blockIdx.x) * 64 + threadIdx.x] = acc;
 }
 
 }  // namespace
@@ -196,6 +217,17 @@ int chx_read(const void* src, uint64_t bytes, void* sink, uint64_t sink_bytes, v
     const uint32_t blocks = static_cast<uint32_t>(need / (64 * kReadWaves * 4));
     hipLaunchKernelGGL(read_kernel, dim3(blocks), dim3(64 * kReadWaves), 0, static_cast<hipStream_t>(s),
                        static_cast<const uint8_t*>(src), bytes / 1024, static_cast<uint32_t*>(sink));
+    return hipGetLastError();
+}
+
+// `waves` one-wave workgroups reading `kib` KB each from `src` (16-byte
+// aligned, waves * kib KB long); `sink` holds 64 words a wave.
+int chx_touch(const void* src, uint32_t waves, uint32_t kib, void* sink, uint64_t sink_bytes, void* s) {
+    if (waves == 0 || kib == 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0 ||
+        sink_bytes < static_cast<uint64_t>(waves) * 64 * 4)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(touch_kernel, dim3(waves), dim3(64), 0, static_cast<hipStream_t>(s),
+                       static_cast<const u32x4_t*>(src), kib, static_cast<uint32_t*>(sink));
     return hipGetLastError();
 }
 

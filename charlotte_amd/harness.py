@@ -42,6 +42,7 @@ _SIGS = {
     "chx_null": (_c.c_int, [_c.c_void_p]),
     "chx_read_sink_bytes": (_c.c_int, [_c.POINTER(_c.c_uint64)]),
     "chx_read": (_c.c_int, [_c.c_void_p, _c.c_uint64, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
+    "chx_touch": (_c.c_int, [_c.c_void_p, _c.c_uint32, _c.c_uint32, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
 }
 
 
@@ -198,6 +199,13 @@ def read(src_ptr, nbytes, sink_ptr, sink_bytes, stream=None):
     pattern of the LDS-streamed decodes with their arithmetic taken away."""
     check(lib.chx_read(src_ptr, nbytes, sink_ptr, sink_bytes, stream.handle if isinstance(stream, Stream) else stream),
           "read")
+
+
+def touch(src_ptr, waves, kib, sink_ptr, sink_bytes, stream=None):
+    """`waves` one-wave workgroups each reading `kib` KB and writing a word:
+    a small decode's dispatch and round trip with nothing decoded."""
+    check(lib.chx_touch(src_ptr, waves, kib, sink_ptr, sink_bytes,
+                        stream.handle if isinstance(stream, Stream) else stream), "touch")
 
 
 def null(stream=None):
