@@ -11,7 +11,10 @@
 // global_load_lds_dwordx4 — the step's 8 KB of codes and 1 KB of scales are
 // contiguous in the piece, so every copy instruction reads 1 KB in a row —
 // and each lane then reads its own groups out of LDS, as gemv_stream8.hip
-// does for Q6_K.
+// does for Q6_K. At K = 1,024 the reference's mapping reads coalesced, but
+// with one group a lane a row it spends 4.2 VALU instructions a weight on
+// its loads' addresses and each row's reduction, against 2.9 here (the
+// Q4_0 head, 151,936 x 1,024: 22.3-24.3 -> 21.6-23.3 us).
 //
 // Mapping: every lane owns 8 groups (128 code bytes, 16 scale bytes): L = G /
 // 8 lanes a row (4, 8, 16, 32), 64 / L rows a step (16, 8, 4, 2). Lane j of
