@@ -317,18 +317,13 @@ def run_c3(S, steps, warmup, rng, fused=True):
     return out
 
 
-def c3_floors(S, launches, steps, warmup):
-    """Two floors under a decode step's launches, each timed as a graph of as
-    many launches as the step: `launch_us`, an empty kernel of one workgroup
-    a launch (what launching costs); `memory_us`, each product's bytes read
-    in its own launch shape with nothing decoded — the 32-lane products'
-    one-wave workgroups (chx_touch: as many waves as the plan's, the
-    product's stored bytes split among them), the streamed products by the
-    streamed copy (chx_read). Reads walk one buffer longer than the MALL, a
-    product's bytes after the last's, as the step's weights do."""
+def floor_parts(mm, launches):
+    """Each launch's reads-alone stand-in: ("read", bytes, 0) for a streamed
+    product (its stored bytes, whole KB), ("touch", waves, kib) for the
+    others — the plan's waves, each reading kib whole KB of the product's
+    stored bytes (never more than them)."""
     from charlotte_amd import synthetic
 
-    hx, mm = S.hx, S.mm
     parts = []
     for m in launches:
         p = mm.plan_launch(m, 1)
@@ -341,6 +336,20 @@ def c3_floors(S, launches, steps, warmup):
             kib = max(1, nbytes // (waves * 1024))
             waves = min(waves, nbytes // (kib * 1024))
             parts.append(("touch", waves, kib))
+    return parts
+
+
+def c3_floors(S, launches, steps, warmup):
+    """Two floors under a decode step's launches, each timed as a graph of as
+    many launches as the step: `launch_us`, an empty kernel of one workgroup
+    a launch (what launching costs); `memory_us`, each product's bytes read
+    in its own launch shape with nothing decoded — the 32-lane products'
+    one-wave workgroups (chx_touch: as many waves as the plan's, the
+    product's stored bytes split among them), the streamed products by the
+    streamed copy (chx_read). Reads walk one buffer longer than the MALL, a
+    product's bytes after the last's, as the step's weights do."""
+    hx = S.hx
+    parts = floor_parts(S.mm, launches)
     total = sum(a if k == "read" else a * c * 1024 for k, a, c in parts)
     buf = S.buffer(nbytes=max(total, 2 * MALL_BYTES) + (1 << 20))
     sink_bytes = max(hx.read_sink_bytes(), 64 * 4 * max(a for k, a, c in parts if k == "touch"))

@@ -25,6 +25,46 @@ def test_gemv_bytes_are_the_algorithmic_figures():
     assert total == 378_487_296
 
 
+def test_decode_step_floor_reads_each_product_in_its_launch_shape():
+    """The reads-alone floor of the Qwen3 0.6B step: each 32-lane product's
+    plan's waves reading whole KB of its stored bytes (never more), the Q6_K
+    head by the streamed copy."""
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+
+    Q4_0, Q6_K = mm.TensorType.Q4_0, mm.TensorType.Q6_K
+    made = []
+
+    def w(gtype, rows, columns):
+        made.append(mm.Weight.shape(gtype, rows, columns))
+        return made[-1]
+
+    X, Y = 16, 16
+    launches = [
+        mm.MatmulLaunch([mm.Member(w(Q4_0, 2048, 1024)), mm.Member(w(Q4_0, 1024, 1024)),
+                         mm.Member(w(Q4_0, 1024, 1024))], X, [Y, Y, Y], epilogue=mm.Epilogue.QKV),
+        mm.MatmulLaunch([mm.Member(w(Q4_0, 1024, 2048))], X, [Y]),
+        mm.MatmulLaunch([mm.Member(w(Q4_0, 3072, 1024)), mm.Member(w(Q4_0, 3072, 1024))], X, [Y],
+                        epilogue=mm.Epilogue.GatedActivation),
+        mm.MatmulLaunch([mm.Member(w(Q4_0, 1024, 3072))], X, [Y]),
+        mm.MatmulLaunch([mm.Member(w(Q6_K, 151936, 1024))], X, [Y]),
+    ]
+    try:
+        parts = bench.floor_parts(mm, launches)
+        assert [k for k, _, _ in parts] == ["touch"] * 4 + ["read"]
+        for m, (kind, a, c) in zip(launches, parts):
+            stored = sum(synthetic.stored_bytes(int(x.weight.type), x.weight.rows, x.weight.columns) for x in m.members)
+            if kind == "read":
+                assert a == stored // 1024 * 1024
+            else:
+                p = mm.plan_launch(m, 1)
+                assert a == p.workgroups  # one-wave workgroups, one a tile
+                assert 0 < a * c * 1024 <= stored < (a + 1) * (c + 1) * 1024
+    finally:
+        for x in made:
+            x.free()
+
+
 def test_cpu_baseline_reports_its_fields_on_a_sample():
     from charlotte_amd import synthetic
 
