@@ -24,6 +24,7 @@
 #include "decode.hpp"
 #include "plan.hpp"
 #include "product.hpp"
+#include "stream.hpp"
 
 namespace chm {
 
@@ -37,27 +38,6 @@ constexpr int kWaves = 4;     // waves a workgroup
 constexpr int kPad = 33;      // a row's 32 range sums, padded
 constexpr int kRowPad = 36;   // gemv_ranges: the same, each row 16-byte aligned
 
-// A row's 32 range sums added in order from zero — ((0 + s0) + s1) + ...,
-// the order of matmul.h:34-50 — read from LDS in eight 16-byte reads issued
-// together: one LDS round trip, where reads of a pair at a time between the
-// adds took four (Q4_0 3,072 x 1,024: 3.55 -> 3.42 us). `row` is 16-byte
-// aligned; the reads claim memory, so the row's stores stay above them.
-__device__ __forceinline__ float ordered_total(const float* row) {
-    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-    const uint32_t at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(row));
-    u32x4_t v[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-        __asm__ __volatile__("ds_read_b128 %0, %1 offset:%2" : "=v"(v[k]) : "v"(at), "i"(16 * k) : "memory");
-    __asm__ __volatile__("s_waitcnt lgkmcnt(0)"
-                         : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
-    float total = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) total = total + __uint_as_float(v[k][e]);
-    return total;
-}
 constexpr int kWaveRows = 64; // rows a wave covers at most (steps * 64 / L)
 constexpr uint32_t kMaxStagedK = 8192;
 constexpr int kChunkGroups = 8;  // past kMaxStagedK: groups a range x is staged for at a time
@@ -684,6 +664,8 @@ static hipError_t launch_format(const Product& a, const Plan& plan, uint32_t cus
 //   - Q4_0 at K = 1,024, 2,048, 4,096 or 8,192, 2^20 groups or more, in
 //     whole steps: the LDS-streamed kernel (the INT8_LIMBS form is Q6_K's
 //     alone);
+//   - Q4_0 at K = 9,216 .. 16,384 in whole 1,024s: the LDS-streamed kernel
+//     with a lane a range (gemv_wide.hip);
 //   - quantized K = 1,152 otherwise: 4 lanes a row, 9 groups each;
 //   - other K up to 8,192: the reference's 32 lanes a row, x in registers
 //     while a lane's slice is at most 3 groups, else staged whole in LDS
@@ -720,6 +702,16 @@ bool plan_gemv(const Product& a, uint32_t format, uint32_t compute_units, bool l
         plan->tile_rows = step_rows;
         plan->tiles = a.rows / step_rows;
         plan->workgroups = gemv_stream4_workgroups(G, compute_units, plan->tiles);
+        return true;
+    }
+    if (gemv_wide_takes(a, format)) {
+        plan->kernel = kGemvWide;
+        plan->lanes = 32;
+        plan->span = G / 32;
+        plan->steps = 1;
+        plan->tile_rows = 2;
+        plan->tiles = (a.rows + 1) / 2;
+        plan->workgroups = gemv_wide_workgroups(compute_units, plan->tiles);
         return true;
     }
     if (G * 32 > kMaxStagedK || (format == kF32 && G > 64) || (plain_values(format) && G > 96)) {
@@ -803,6 +795,7 @@ hipError_t launch_gemv(const Product& a, uint32_t format, const Plan& plan, uint
     if (plan.kernel == kGemvStream) return launch_gemv_stream(a, compute_units, plan.limbs, stream);
     if (plan.kernel == kGemvStream8) return launch_gemv_stream8(a, compute_units, plan.limbs, stream);
     if (plan.kernel == kGemvStream4) return launch_gemv_stream4(a, compute_units, stream);
+    if (plan.kernel == kGemvWide) return launch_gemv_wide(a, compute_units, stream);
     switch (format) {
         case kQ4_0: return launch_format<kQ4_0>(a, plan, compute_units, stream);
         case kQ4_1: return launch_format<kQ4_1>(a, plan, compute_units, stream);

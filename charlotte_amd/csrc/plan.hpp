@@ -22,7 +22,8 @@ enum Kernel : uint32_t {
     kGemvStream = 3,    // decode, LDS-streamed Q6_K, K = 1,152
     kGemvStream8 = 4,   // decode, LDS-streamed Q6_K, K = 1,024 and 2,048
     kGemvChunked = 5,   // decode past K = 8,192: x staged a chunk of groups at a time
-    kGemvStream4 = 6,   // decode, LDS-streamed Q4_0, K = 2,048, 4,096 and 8,192
+    kGemvStream4 = 6,   // decode, LDS-streamed Q4_0, K = 1,024 .. 8,192 (powers of two)
+    kGemvWide = 7,      // decode, LDS-streamed Q4_0, K = 9,216 .. 16,384 (whole 1,024s), a lane a range
     kGemmTiled = 16,    // prefill, the VALU tile
     kGemmSplit = 17,    // prefill split along K, then the ordered combine
     kGemmMfma = 18,     // prefill on the matrix cores, x split into two f16 parts
@@ -58,6 +59,9 @@ hipError_t launch_gemv_stream(const Product& a, uint32_t compute_units, bool lim
 hipError_t launch_gemv_stream8(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream);
 hipError_t launch_gemv_stream4(const Product& a, uint32_t compute_units, hipStream_t stream);
 uint64_t gemv_stream4_workgroups(uint32_t groups, uint32_t compute_units, uint64_t steps);
+bool gemv_wide_takes(const Product& a, uint32_t format);
+hipError_t launch_gemv_wide(const Product& a, uint32_t compute_units, hipStream_t stream);
+uint64_t gemv_wide_workgroups(uint32_t compute_units, uint64_t steps);
 
 // Prefill on the VALU tile; `split` for the split along K.
 void plan_gemm_canonical(const Product& a, uint32_t compute_units, bool split, Plan* plan);

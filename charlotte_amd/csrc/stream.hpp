@@ -1,6 +1,6 @@
-// What the LDS-streamed decodes (gemv_stream.hip, gemv_stream8.hip) share:
-// the DMA copy of a stream's 16-byte chunks into a wave's LDS stage, and the
-// wait for it.
+// What the LDS-streamed decodes share: the DMA copy of a stream's 16-byte
+// chunks into a wave's LDS stage, the wait for it, and a row's ordered total
+// from its range sums in LDS.
 #pragma once
 
 #include "limbs.hpp"
@@ -23,6 +23,27 @@ __device__ __forceinline__ void copy_stream(const uint8_t* from, u32x4s_t* to, u
         if (64 * i + 64 <= kChunks || 64 * i + lane < kChunks)
             __builtin_amdgcn_global_load_lds(from + 16 * (64 * i + lane), (lds_void)(to + 64 * i), 16, 0, 0);
     }
+}
+
+// A row's 32 range sums added in order from zero — ((0 + s0) + s1) + ...,
+// the order of matmul.h:34-50 — read from LDS in eight 16-byte reads issued
+// together: one LDS round trip, where reads of a pair at a time between the
+// adds took four (Q4_0 3,072 x 1,024: 3.55 -> 3.42 us). `row` is 16-byte
+// aligned; the reads claim memory, so the row's stores stay above them.
+__device__ __forceinline__ float ordered_total(const float* row) {
+    const uint32_t at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(row));
+    u32x4s_t v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        __asm__ __volatile__("ds_read_b128 %0, %1 offset:%2" : "=v"(v[k]) : "v"(at), "i"(16 * k) : "memory");
+    __asm__ __volatile__("s_waitcnt lgkmcnt(0)"
+                         : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
+    float total = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) total = total + __uint_as_float(v[k][e]);
+    return total;
 }
 
 }  // namespace chm

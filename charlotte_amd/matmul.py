@@ -91,6 +91,7 @@ class Kernel(enum.IntEnum):
     GEMV_STREAM8 = 4
     GEMV_CHUNKED = 5
     GEMV_STREAM4 = 6
+    GEMV_WIDE = 7
     GEMM_TILED = 16
     GEMM_SPLIT = 17
     GEMM_MFMA = 18

@@ -5,9 +5,10 @@ ranges of matmul.wgsl:134-137 are defined for every G). Past 8,192 x no
 longer fits the LDS stage the shorter decodes use, so the kernel stages it a
 chunk of groups at a time and every row's chains run on across chunks; the
 order of addition is unchanged, so decode is still prefill's bits. Shapes:
-just past 8,192, K = 9,728 and 14,336 (Llama 3 8B's down projection,
-4,096 x 14,336, in full), rows not whole tiles, every format, the fused
-epilogues, the head's last token.
+just past 8,192, K = 9,728, 13,824 and 14,336 (Llama 3 8B's down
+projection, 4,096 x 14,336 in full — Q4_0 there runs the streamed kernel of
+gemv_wide.hip, tests/test_gpu_wide.py), rows not whole tiles, every format,
+the fused epilogues, the head's last token.
 """
 
 import numpy as np
@@ -52,8 +53,8 @@ def _check(got, want, what):
 
 
 @pytest.mark.parametrize("gtype,rows,columns", [
-    (Q4_0, 300, 8224), (Q4_0, 1001, 9728), (Q4_0, 77, 14336), (Q6_K, 512, 9728), (Q6_K, 333, 14336),
-    (Q8_0, 300, 9728), (Q4_1, 200, 14336), (F16, 160, 14336), (BF16, 96, 9728), (Q4_0, 1, 16384),
+    (Q4_0, 300, 8224), (Q4_0, 1001, 9728), (Q4_0, 77, 13824), (Q6_K, 512, 9728), (Q6_K, 333, 14336),
+    (Q8_0, 300, 9728), (Q4_1, 200, 14336), (F16, 160, 14336), (BF16, 96, 9728), (Q4_0, 1, 17408),
 ])
 def test_long_k_decode_is_the_oracles_bits_and_prefills(oracle, run, gtype, rows, columns):
     from charlotte_amd import matmul as mm

@@ -178,10 +178,29 @@ def test_q4_0_k_1024_to_8192_in_whole_steps_is_the_streamed_decode(shapes, colum
     assert mm.plan_launch(_write(shapes(mm.TensorType.Q4_1, 1024, columns)), 1).kernel == K.GEMV_RANGES
 
 
-@pytest.mark.parametrize("columns", [8192 + 32, 9728, 14336, 65536])
+@pytest.mark.parametrize("columns", [8192 + 32, 9728, 13824, 17408, 65536])
 def test_decode_past_k_8192_stages_x_in_chunks(shapes, columns):
+    # Q4_0 past K = 8,192 other than whole 1,024s up to 16,384
     p = mm.plan_launch(_write(shapes(Q4_0, 4096, columns)), 1)
     assert p.kernel == K.GEMV_CHUNKED and p.canonical and p.groups_a_lane == (columns // 32 + 31) // 32
+    # other formats at any K past 8,192
+    assert mm.plan_launch(_write(shapes(mm.TensorType.Q8_0, 4096, 14336)), 1).kernel == K.GEMV_CHUNKED
+
+
+@pytest.mark.parametrize("rows,columns", [(4096, 9216), (4096, 14336), (1, 14336), (4097, 16384), (14336, 12288)])
+def test_q4_0_k_9216_to_16384_in_whole_1024s_is_the_wide_streamed_decode(shapes, rows, columns):
+    """A lane a range (K / 1,024 groups each), two rows a wave step, one
+    workgroup of four waves a CU at most."""
+    p = mm.plan_launch(_write(shapes(Q4_0, rows, columns)), 1)
+    steps = (rows + 1) // 2
+    assert (p.kernel, p.canonical, p.lanes_a_row, p.groups_a_lane) == (K.GEMV_WIDE, True, 32, columns // 1024)
+    assert (p.tile_rows, p.tiles, p.workgroups) == (2, steps, min(256, (steps + 3) // 4))
+    # members anywhere and gated products: rows are copied one at a time
+    w = shapes(Q4_0, 2 * rows + 3, columns)
+    assert mm.plan_launch(mm.MatmulLaunch([mm.Member(w, row_offset=3, rows=rows)], X, [Y0]), 1).kernel == K.GEMV_WIDE
+    gated = mm.MatmulLaunch([mm.Member(w, rows=rows), mm.Member(w, row_offset=rows, rows=rows)], X, [Y0],
+                            epilogue=mm.Epilogue.GatedActivation, out_width=rows)
+    assert mm.plan_launch(gated, 1).kernel == K.GEMV_WIDE
 
 
 @pytest.mark.parametrize("gtype,columns,kernel", [
