@@ -206,6 +206,35 @@ def run_gemv(S, name, gtype, rows, columns, steps, warmup, rng, copies=None):
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": gemv_traffic(name)}}
 
 
+def parse_shapes(spec):
+    """ROWSxCOLUMNS[:TYPE],... -> [(rows, columns, gguf_type)], Q4_0 (2) when
+    no type is given."""
+    shapes = []
+    for item in spec.split(","):
+        shape, _, t = item.strip().partition(":")
+        rows, columns = (int(v) for v in shape.lower().split("x"))
+        shapes.append((rows, columns, int(t or 2)))
+    return shapes
+
+
+def time_decode_shapes(spec, steps, warmup, settle_ms):
+    """One decode product a shape, timed as the configs are (weights rotated
+    past the MALL, graph replays): {"ROWSxCOLUMNS:TYPE": {us, GB/s, frac}}."""
+    S = Setup()
+    S.settle_ms = settle_ms
+    rng = np.random.default_rng(1)
+    out = {}
+    try:
+        for rows, columns, gtype in parse_shapes(spec):
+            tag = f"{rows}x{columns}:{gtype}"
+            r = run_gemv(S, tag, gtype, rows, columns, steps, warmup, rng)
+            out[tag] = {"us": round(r["ms_per_step"] * 1e3, 2), "GB/s": round(r["GB/s"], 1),
+                        "frac": round(r["frac"], 4), "bytes": r["bytes"]}
+    finally:
+        S.close()
+    return out
+
+
 def run_read_floor(S, name, nbytes, copies, steps, warmup):
     """The same bytes read and nothing else (harness chx_read: the LDS-streamed
     decodes' copy, 9 KB a wave a step, with no decode), over `copies` buffers
@@ -659,9 +688,15 @@ def main():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-table", action="store_true",
                    help="time the CPU baseline table (C1-C5, f32 and f64, 1 and all threads) and exit")
+    p.add_argument("--decode", metavar="SHAPES",
+                   help="time decode products of the given shapes and exit: a comma list of ROWSxCOLUMNS[:TYPE], "
+                        "TYPE a GGUF type number (2 Q4_0, default; 3 Q4_1; 8 Q8_0; 14 Q6_K, repacked)")
     args = p.parse_args()
     if args.cpu_table:
         print(json.dumps(cpu_table(min(os.cpu_count() or 1, 16))), flush=True)
+        return
+    if args.decode:
+        print(json.dumps(time_decode_shapes(args.decode, args.steps, args.warmup, args.settle_ms)), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this path is measured on one MI355X); got --gpus {args.gpus}",

@@ -82,3 +82,8 @@ def test_more_than_one_gpu_is_refused():
                        timeout=120)
     assert r.returncode != 0
     assert "one GPU" in r.stderr
+
+
+def test_decode_shapes_parse_with_q4_0_by_default():
+    assert bench.parse_shapes("4096x14336,151936x1024:14, 3072X1024:8") == [
+        (4096, 14336, 2), (151936, 1024, 14), (3072, 1024, 8)]
