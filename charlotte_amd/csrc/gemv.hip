@@ -61,7 +61,7 @@ __device__ __forceinline__ void finish_rows(const Product& a, uint32_t first, ui
     const uint32_t p = first + lane;
     float partner = 0.0f;
     if (FULL && a.epilogue == kGated) partner = __shfl_xor(total, 1);
-    if (lane < count && p < a.rows) emit<FULL>(a, p, 0, a.last_token ? a.tokens - 1 : 0, total, partner);
+    if (lane < count && p < a.rows) emit<FULL, true>(a, p, 0, a.last_token ? a.tokens - 1 : 0, total, partner);
 }
 
 // L = 32: lane r of a half-wave owns range r — at most SPAN groups, its
