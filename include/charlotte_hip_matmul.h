@@ -287,7 +287,7 @@ typedef enum {
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMV_QUARTERS = 2, /* decode, 4 lanes a row of 9 groups each (K = 1,152) */
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMV_STREAM = 3,   /* decode, Q6_K at K = 1,152 streamed through LDS */
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMV_STREAM8 = 4,  /* decode, Q6_K at K = 1,024 or 2,048 streamed through LDS */
-    CHARLOTTE_HIP_MATMUL_KERNEL_GEMV_CHUNKED = 5,  /* decode past K = 8,192: x staged a chunk at a time */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMV_CHUNKED = 5,  /* decode past K = 8,192 (GEMV_WIDE aside): x staged a chunk at a time */
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMV_STREAM4 = 6,  /* decode, Q4_0 at K = 1,024 .. 8,192 (powers of two) streamed through LDS */
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMV_WIDE = 7,     /* decode, Q4_0 at K = 9,216 .. 16,384 (whole 1,024s) streamed through LDS */
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_TILED = 16,   /* prefill, the VALU tile */
