@@ -217,11 +217,14 @@ def parse_shapes(spec):
     return shapes
 
 
-def time_decode_shapes(spec, steps, warmup, settle_ms):
+def time_decode_shapes(spec, steps, warmup, settle_ms, limbs=False):
     """One decode product a shape, timed as the configs are (weights rotated
-    past the MALL, graph replays): {"ROWSxCOLUMNS:TYPE": {us, GB/s, frac}}."""
+    past the MALL, graph replays): {"ROWSxCOLUMNS:TYPE": {us, GB/s, frac}};
+    `limbs` decodes on the INT8_LIMBS path where it applies."""
     S = Setup()
     S.settle_ms = settle_ms
+    if limbs:
+        S.ctx.set_gemv_path(S.mm.GemvPath.INT8_LIMBS)
     rng = np.random.default_rng(1)
     out = {}
     try:
@@ -691,12 +694,14 @@ def main():
     p.add_argument("--decode", metavar="SHAPES",
                    help="time decode products of the given shapes and exit: a comma list of ROWSxCOLUMNS[:TYPE], "
                         "TYPE a GGUF type number (2 Q4_0, default; 3 Q4_1; 8 Q8_0; 14 Q6_K, repacked)")
+    p.add_argument("--limbs", action="store_true", help="with --decode: the INT8_LIMBS decode path")
     args = p.parse_args()
     if args.cpu_table:
         print(json.dumps(cpu_table(min(os.cpu_count() or 1, 16))), flush=True)
         return
     if args.decode:
-        print(json.dumps(time_decode_shapes(args.decode, args.steps, args.warmup, args.settle_ms)), flush=True)
+        print(json.dumps(time_decode_shapes(args.decode, args.steps, args.warmup, args.settle_ms, args.limbs)),
+              flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this path is measured on one MI355X); got --gpus {args.gpus}",
@@ -742,6 +747,15 @@ def main():
                                        args.warmup)
                 out[tag]["read_floor"] = floor
                 out[tag]["frac_of_read_floor"] = round(r["GB/s"] / floor["GB/s"], 4)
+                if columns > 2048:
+                    continue  # the INT8_LIMBS form is built for K = 1,024 and 2,048
+                S.ctx.set_gemv_path(S.mm.GemvPath.INT8_LIMBS)
+                r = run_gemv(S, tag + "_limbs", 2, rows, columns, max(args.steps, 20), args.warmup,
+                             np.random.default_rng(8))
+                S.ctx.set_gemv_path(S.mm.GemvPath.CANONICAL)
+                out[tag + "_limbs"] = {k: v for k, v in r.items() if k not in ("stored", "x", "weights")}
+                out[tag + "_limbs"]["path"] = "INT8_LIMBS: within 1e-5 of the canonical order, not its bits"
+                out[tag + "_limbs"]["frac_of_read_floor"] = round(r["GB/s"] / floor["GB/s"], 4)
         if "c3" in only:
             out["c3"] = run_c3(S, max(args.steps // 4, 3), args.warmup, rng)
             out["c3_unfused"] = run_c3(S, max(args.steps // 4, 3), args.warmup, rng, fused=False)

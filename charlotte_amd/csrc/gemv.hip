@@ -662,8 +662,8 @@ static hipError_t launch_format(const Product& a, const Plan& plan, uint32_t cus
 //   - Q6_K at K = 1,152, 1,024 or 2,048 in whole steps: the LDS-streamed
 //     kernels (the INT8_LIMBS form there when asked);
 //   - Q4_0 at K = 1,024, 2,048, 4,096 or 8,192, 2^20 groups or more, in
-//     whole steps: the LDS-streamed kernel (the INT8_LIMBS form is Q6_K's
-//     alone);
+//     whole steps: the LDS-streamed kernel (the INT8_LIMBS form at K =
+//     1,024 and 2,048 when asked);
 //   - Q4_0 at K = 9,216 .. 16,384 in whole 1,024s: the LDS-streamed kernel
 //     with a lane a range (gemv_wide.hip);
 //   - quantized K = 1,152 otherwise: 4 lanes a row, 9 groups each;
@@ -696,6 +696,11 @@ bool plan_gemv(const Product& a, uint32_t format, uint32_t compute_units, bool l
     if (gemv_stream4_takes(a, format)) {
         const uint32_t step_rows = 64 / (G / 8);
         plan->kernel = kGemvStream4;
+        // the limbs form at K = 1,024 and 2,048 only: at 4,096 and 8,192 it
+        // measured slower than the canonical decode (21.4 against 20.4 us,
+        // 37.9 against 33.7), where at 1,024 and 2,048 it is 9-10% faster
+        plan->limbs = limbs && G <= 64;
+        plan->canonical = !plan->limbs;
         plan->lanes = G / 8;
         plan->span = 8;
         plan->steps = 1;
@@ -794,7 +799,7 @@ hipError_t launch_gemv(const Product& a, uint32_t format, const Plan& plan, uint
                        hipStream_t stream) {
     if (plan.kernel == kGemvStream) return launch_gemv_stream(a, compute_units, plan.limbs, stream);
     if (plan.kernel == kGemvStream8) return launch_gemv_stream8(a, compute_units, plan.limbs, stream);
-    if (plan.kernel == kGemvStream4) return launch_gemv_stream4(a, compute_units, stream);
+    if (plan.kernel == kGemvStream4) return launch_gemv_stream4(a, compute_units, plan.limbs, stream);
     if (plan.kernel == kGemvWide) return launch_gemv_wide(a, compute_units, stream);
     switch (format) {
         case kQ4_0: return launch_format<kQ4_0>(a, plan, compute_units, stream);

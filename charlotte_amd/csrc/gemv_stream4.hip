@@ -54,7 +54,7 @@ struct StepRun4 {
 
 }  // namespace
 
-template <uint32_t G, bool FULL, uint32_t W>
+template <uint32_t G, bool FULL, uint32_t W, bool LIMBS>
 __global__ __launch_bounds__(64 * W) void gemv_stream4(Product a, uint32_t steps) {
     constexpr uint32_t L = G / 8;           // lanes a row
     constexpr uint32_t kRows = 64 / L;      // rows a step
@@ -132,7 +132,19 @@ __global__ __launch_bounds__(64 * W) void gemv_stream4(Product a, uint32_t steps
             }
             const uint32_t cw[4] = {run.codes[i][0], run.codes[i][1], run.codes[i][2], run.codes[i][3]};
             const uint32_t d = (run.scales[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-            s = chain_q4_0_wide(cw, d, xg, s);
+            if constexpr (LIMBS) {
+                // the record's words, as staged: the float4 reads carry them
+                u32x4s_t g[8];
+#pragma unroll
+                for (int v = 0; v < 8; ++v) {
+                    const float4 q = xa[i & 1][v];
+                    g[v] = u32x4s_t{__float_as_uint(q.x), __float_as_uint(q.y), __float_as_uint(q.z),
+                                    __float_as_uint(q.w)};
+                }
+                s = group_limbs_q4_0(cw, half_to_float(d), g, s);
+            } else {
+                s = chain_q4_0_wide(cw, d, xg, s);
+            }
             if ((i + 1) % kPerRange == 0) {
                 sums_s[33 * (slot * kRows + rho) + kRanges * j + i / kPerRange] = s;
                 s = 0.0f;
@@ -166,7 +178,30 @@ __global__ __launch_bounds__(64 * W) void gemv_stream4(Product a, uint32_t steps
     // waits for both round trips at once).
     uint32_t step = blockIdx.x * W + wave;
     if (step < steps) issue(step);
-    {
+    if constexpr (LIMBS) {
+        // Group g's limb record (limbs.hpp, bias 8) in the place of its
+        // eight float4, at 8 g + g / 8; four lanes a group, a quad.
+        // Every pass's loads before any record is worked out: one round trip.
+        constexpr uint32_t kThreads = 64 * W, kPasses = (4 * G + kThreads - 1) / kThreads;
+        const float* xrow = a.x + static_cast<uint64_t>(token) * G * 32;
+        const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(x_stage));
+        float4 xv[kPasses][2];
+#pragma unroll
+        for (uint32_t k = 0; k < kPasses; ++k) {
+            const uint32_t t = threadIdx.x + kThreads * k;
+            if (t < 4 * G) {
+                const float4* src = reinterpret_cast<const float4*>(xrow + 8 * t);
+                xv[k][0] = clamp_input(a, src[0]), xv[k][1] = clamp_input(a, src[1]);
+            }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kPasses; ++k) {
+            const uint32_t t = threadIdx.x + kThreads * k, group = t >> 2;
+            if (t < 4 * G) stage_limbs<8>(xv[k][0], xv[k][1], t & 3u, base + 16 * (8 * group + group / 8));
+        }
+        __asm__ __volatile__("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+    } else {
         // float4 v of x sits at v + v / 64 (slice v / 64 of 64, one of
         // padding), clamped where the product is clipped. The stores are
         // instructions the compiler does not look into (it would wait for
@@ -230,26 +265,31 @@ uint64_t gemv_stream4_workgroups(uint32_t groups, uint32_t compute_units, uint64
     return std::min<uint64_t>(uint64_t{kS4Blocks[i]} * compute_units, (steps + kS4Waves[i] - 1) / kS4Waves[i]);
 }
 
-template <uint32_t G>
+template <uint32_t G, bool LIMBS>
 static void go4(const Product& a, uint32_t compute_units, hipStream_t stream) {
     constexpr uint32_t W = kS4Waves[s4_index(G)];
     const uint32_t steps = a.rows / (64 / (G / 8));
     const uint32_t blocks = static_cast<uint32_t>(gemv_stream4_workgroups(G, compute_units, steps));
     if (plain_epilogue(a))
-        hipLaunchKernelGGL((gemv_stream4<G, false, W>), dim3(blocks), dim3(64 * W), 0, stream, a, steps);
+        hipLaunchKernelGGL((gemv_stream4<G, false, W, LIMBS>), dim3(blocks), dim3(64 * W), 0, stream, a, steps);
     else
-        hipLaunchKernelGGL((gemv_stream4<G, true, W>), dim3(blocks), dim3(64 * W), 0, stream, a, steps);
+        hipLaunchKernelGGL((gemv_stream4<G, true, W, LIMBS>), dim3(blocks), dim3(64 * W), 0, stream, a, steps);
 }
 
-hipError_t launch_gemv_stream4(const Product& a, uint32_t compute_units, hipStream_t stream) {
+template <bool LIMBS>
+static hipError_t launch4(const Product& a, uint32_t compute_units, hipStream_t stream) {
     switch (a.groups) {
-        case 32: go4<32>(a, compute_units, stream); break;
-        case 64: go4<64>(a, compute_units, stream); break;
-        case 128: go4<128>(a, compute_units, stream); break;
-        case 256: go4<256>(a, compute_units, stream); break;
+        case 32: go4<32, LIMBS>(a, compute_units, stream); break;
+        case 64: go4<64, LIMBS>(a, compute_units, stream); break;
+        case 128: go4<128, LIMBS>(a, compute_units, stream); break;
+        case 256: go4<256, LIMBS>(a, compute_units, stream); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_gemv_stream4(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream) {
+    return limbs ? launch4<true>(a, compute_units, stream) : launch4<false>(a, compute_units, stream);
 }
 
 }  // namespace chm

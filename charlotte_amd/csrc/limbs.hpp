@@ -26,6 +26,13 @@
 // sum (q - 32) X rounded once. The group's contribution is
 // d ldexp(fma(sc_1, P_1, sc_0 P_0), -s): the power of two applied to the
 // group's sum, exact wherever that sum is a normal f32.
+//
+// Q4_0 (codes q in 0..15, weight (q - 8) d, one scale a group) stages its
+// records with a bias of 8 over the whole group: [24, 27) hold -8 (sum of
+// a, sum of b, sum of c) over weights 0..31 and [27, 30) zero. A = sum
+// (q - 8) a has |A| <= 32 * 8 * 64 = 2^14, Z = 256 A + B is exact, P =
+// fma(Z, 256, C) is sum (q - 8) X rounded once, and the contribution is
+// d ldexp(P + poison, -s).
 #pragma once
 
 #include "decode.hpp"
@@ -41,6 +48,9 @@ constexpr uint32_t kLimbRecord = 32;  // dwords a group
 // v1) and writes its share of the record at LDS byte address `record`; the
 // four lanes are a quad (the group's max and sums meet by DPP). Stores are
 // inline ds_writes: the caller waits for them (lgkmcnt) before its barrier.
+// kBias 32 (Q6_K): the sums over each 16-weight half; 8 (Q4_0): over the
+// whole group.
+template <int kBias = 32>
 __device__ __forceinline__ void stage_limbs(float4 v0, float4 v1, uint32_t part, uint32_t record) {
     const float e[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
     float m = 0.0f;
@@ -77,14 +87,21 @@ __device__ __forceinline__ void stage_limbs(float4 v0, float4 v1, uint32_t part,
     sa += __builtin_amdgcn_mov_dpp(sa, 0xB1, 0xF, 0xF, false);
     sb += __builtin_amdgcn_mov_dpp(sb, 0xB1, 0xF, 0xF, false);
     sc += __builtin_amdgcn_mov_dpp(sc, 0xB1, 0xF, 0xF, false);
+    if constexpr (kBias == 8) {
+        // and the group's: the two halves' (quad_perm [2, 3, 0, 1])
+        sa += __builtin_amdgcn_mov_dpp(sa, 0x4E, 0xF, 0xF, false);
+        sb += __builtin_amdgcn_mov_dpp(sb, 0x4E, 0xF, 0xF, false);
+        sc += __builtin_amdgcn_mov_dpp(sc, 0x4E, 0xF, 0xF, false);
+    }
     __asm__ __volatile__("ds_write_b64 %0, %1" : : "v"(record + 8 * part), "v"(u32x2s_t{wa[0], wa[1]}));
     __asm__ __volatile__("ds_write_b64 %0, %1" : : "v"(record + 32 + 8 * part), "v"(u32x2s_t{wb[0], wb[1]}));
     __asm__ __volatile__("ds_write_b64 %0, %1" : : "v"(record + 64 + 8 * part), "v"(u32x2s_t{wc[0], wc[1]}));
     if (part == 0 || part == 2) {
         const uint32_t at = record + (part == 0 ? 96 : 108);
-        __asm__ __volatile__("ds_write_b32 %0, %1" : : "v"(at), "v"(static_cast<uint32_t>(-32 * sa)));
-        __asm__ __volatile__("ds_write_b32 %0, %1" : : "v"(at + 4), "v"(static_cast<uint32_t>(-32 * sb)));
-        __asm__ __volatile__("ds_write_b32 %0, %1" : : "v"(at + 8), "v"(static_cast<uint32_t>(-32 * sc)));
+        const bool live = kBias == 32 || part == 0;
+        __asm__ __volatile__("ds_write_b32 %0, %1" : : "v"(at), "v"(live ? static_cast<uint32_t>(-kBias * sa) : 0u));
+        __asm__ __volatile__("ds_write_b32 %0, %1" : : "v"(at + 4), "v"(live ? static_cast<uint32_t>(-kBias * sb) : 0u));
+        __asm__ __volatile__("ds_write_b32 %0, %1" : : "v"(at + 8), "v"(live ? static_cast<uint32_t>(-kBias * sc) : 0u));
     }
     if (part == 1) {
         const float poison = finite ? 0.0f : __builtin_nanf("");
@@ -129,6 +146,27 @@ __device__ __forceinline__ float group_limbs_q6_k(const uint32_t lo[4], const ui
     const float second = static_cast<float>(static_cast<int8_t>((sc >> 8) & 0xFFu));
     const float t = __builtin_fmaf(second, part[1], __builtin_fmaf(first, part[0], __uint_as_float(g[7][3])));
     return __builtin_fmaf(d, __builtin_ldexpf(t, static_cast<int>(g[7][2])), sum);
+}
+
+// One Q4_0 group against its record g (staged with kBias 8), added to the
+// lane's sum: fma(d, ldexp(P + poison, -s), sum). Byte b of code dword c
+// holds weights 4c + b (low nibble) and 16 + 4c + b (high), so the low
+// nibbles of dword c meet the record's dword c and the high ones dword 4 + c.
+__device__ __forceinline__ float group_limbs_q4_0(const uint32_t w[4], float d, const u32x4s_t g[8], float sum) {
+    constexpr uint32_t kNib = 0x0F0F0F0Fu;
+    int A = static_cast<int>(g[6][0]), B = static_cast<int>(g[6][1]), C = static_cast<int>(g[6][2]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int lo = static_cast<int>(w[c] & kNib), hi = static_cast<int>((w[c] >> 4) & kNib);
+        A = __builtin_amdgcn_sdot4(lo, static_cast<int>(g[0][c]), A, false);
+        B = __builtin_amdgcn_sdot4(lo, static_cast<int>(g[2][c]), B, false);
+        C = __builtin_amdgcn_sdot4(lo, static_cast<int>(g[4][c]), C, false);
+        A = __builtin_amdgcn_sdot4(hi, static_cast<int>(g[1][c]), A, false);
+        B = __builtin_amdgcn_sdot4(hi, static_cast<int>(g[3][c]), B, false);
+        C = __builtin_amdgcn_sdot4(hi, static_cast<int>(g[5][c]), C, false);
+    }
+    const float P = __builtin_fmaf(static_cast<float>(A * 256 + B), 256.0f, static_cast<float>(C));
+    return __builtin_fmaf(d, __builtin_ldexpf(P + __uint_as_float(g[7][3]), static_cast<int>(g[7][2])), sum);
 }
 
 }  // namespace chm

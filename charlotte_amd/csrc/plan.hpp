@@ -57,7 +57,7 @@ bool gemv_stream8_takes(const Product& a, uint32_t format);
 bool gemv_stream4_takes(const Product& a, uint32_t format);
 hipError_t launch_gemv_stream(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream);
 hipError_t launch_gemv_stream8(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream);
-hipError_t launch_gemv_stream4(const Product& a, uint32_t compute_units, hipStream_t stream);
+hipError_t launch_gemv_stream4(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream);
 uint64_t gemv_stream4_workgroups(uint32_t groups, uint32_t compute_units, uint64_t steps);
 bool gemv_wide_takes(const Product& a, uint32_t format);
 hipError_t launch_gemv_wide(const Product& a, uint32_t compute_units, hipStream_t stream);

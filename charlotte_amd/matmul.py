@@ -100,8 +100,9 @@ class Kernel(enum.IntEnum):
 class GemvPath(enum.IntEnum):
     """The decode kernel: CANONICAL (bit-exact, the default) or INT8_LIMBS (x as
     three int8 limbs on the dot instructions, within 1e-5; built for the streamed
-    Q6_K shapes, K = 1,024 or 1,152 with rows in 16s and K = 2,048 with rows in
-    8s; other shapes decode canonically)."""
+    shapes: Q6_K at K = 1,024 or 1,152 with rows in 16s and K = 2,048 with rows
+    in 8s, Q4_0 at K = 1,024 or 2,048 in products of 2^20 groups or more; other
+    shapes decode canonically)."""
 
     CANONICAL = 0
     INT8_LIMBS = 1

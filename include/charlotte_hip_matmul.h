@@ -136,10 +136,12 @@ typedef enum {
  * instructions, 16 weights at a time, before the scales and an f32 sum:
  * within max|err| / max|y| <= 1e-5 of the canonical order, not its bits, and
  * not batch-invariant with prefill; a non-finite input makes the outputs NaN.
- * It is built for the shapes of the streamed Q6_K decodes (K = 1,024 or
+ * It is built for the shapes of the streamed decodes: Q6_K at K = 1,024 or
  * 1,152 with each member's rows and first row multiples of 16, K = 2,048
- * with multiples of 8; any epilogue but the gated one); every other decode
- * runs CANONICAL whatever the setting. */
+ * with multiples of 8; Q4_0 at K = 1,024 or 2,048 in products of 2^20
+ * groups or more, rows and first rows multiples of 16 or 8; any epilogue
+ * but the gated one. Every other decode runs CANONICAL whatever the
+ * setting. */
 typedef enum {
     CHARLOTTE_HIP_MATMUL_GEMV_CANONICAL = 0,
     CHARLOTTE_HIP_MATMUL_GEMV_INT8_LIMBS = 1

@@ -171,7 +171,8 @@ def test_limbs_epilogues(oracle, run):
 
 
 @pytest.mark.parametrize("gtype,rows,columns",
-                         [(Q6_K, 100, K), (Q6_K, 100, 1024), (Q6_K, 60, 2048), (Q6_K, 64, 3072), (Q4_0, 3072, 1024)])
+                         [(Q6_K, 100, K), (Q6_K, 100, 1024), (Q6_K, 60, 2048), (Q6_K, 64, 3072), (Q4_0, 3072, 1024),
+                          (Q4_0, 8192, 4096), (Q4_0, 4096, 8192)])
 def test_other_decodes_stay_canonical(oracle, run, gtype, rows, columns):
     """Shapes the path is not built for decode in the canonical order: the
     oracle's bits, whatever the setting."""
@@ -213,3 +214,116 @@ def test_gemv_path_setter_refuses_an_unknown_path(ctx):
     with pytest.raises(mm.MatmulError) as e:
         ctx.set_gemv_path(7)
     assert e.value.status == mm.Status.INVALID_ARGUMENT
+
+
+# Q4_0 on the streamed kernel (K = 1,024 and 2,048, 2^20 groups or more): the
+# limbs form's records carry the -8 bias over the whole group.
+Q4_SHAPES = [(32768, 1024), (16384, 2048), (65536, 1024), (20000, 2048)]
+
+
+@pytest.mark.parametrize("rows,columns", Q4_SHAPES)
+def test_limbs_q4_0_within_tolerance(oracle, run, rows, columns):
+    stored, x = _data(rows, seed=rows + 7, columns=columns, gtype=Q4_0)
+    w = run.weight(Q4_0, rows, columns, stored)
+    got = run.write(w, x, 1)
+    y64, _ = oracle.matmul_f64(Q4_0, stored, rows, columns, x)
+    canonical = oracle.matmul_f32(Q4_0, stored, rows, columns, x, threads=8)
+    ratio = _within(got, y64, canonical, f"Q4_0 {rows} x {columns}")
+    assert ratio < 2e-6, f"Q4_0 {rows} x {columns}: error {ratio:.2e} well above the path's usual"
+    w.free()
+
+
+@pytest.mark.parametrize("kind", ["1e-30", "1e30", "outliers", "one-hot", "zero-groups", "mixed-scales"])
+def test_limbs_q4_0_input_scaling(oracle, run, kind):
+    rows, columns = 32768, 1024
+    stored, x = _data(rows, seed=13, columns=columns, gtype=Q4_0)
+    rng = np.random.default_rng(14)
+    if kind in ("1e-30", "1e30"):
+        x = x * np.float32(float(kind))
+    elif kind == "outliers":
+        x[0, rng.choice(columns, 12, replace=False)] *= np.float32(1000.0)
+    elif kind == "one-hot":
+        x[:] = 0.0
+        x[0, 333] = -1.75
+    elif kind == "zero-groups":
+        x[0, (np.arange(columns) // 32) % 3 == 0] = 0.0
+    else:
+        x[0] *= np.repeat(np.float32(10.0) ** rng.integers(-12, 12, columns // 32), 32).astype(np.float32)
+    w = run.weight(Q4_0, rows, columns, stored)
+    got = run.write(w, x, 1)
+    y64, _ = oracle.matmul_f64(Q4_0, stored, rows, columns, x)
+    canonical = oracle.matmul_f32(Q4_0, stored, rows, columns, x, threads=8)
+    _within(got, y64, canonical, f"Q4_0 {kind}")
+    w.free()
+
+
+@pytest.mark.parametrize("bad", [np.nan, np.inf])
+def test_limbs_q4_0_non_finite_input_makes_nan(run, bad):
+    stored, x = _data(16384, seed=15, columns=2048, gtype=Q4_0)
+    x[0, 1500] = bad
+    w = run.weight(Q4_0, 16384, 2048, stored)
+    got = run.write(w, x, 1)
+    assert np.isnan(got).all()
+    w.free()
+
+
+def test_limbs_q4_0_epilogues(oracle, run):
+    """QKV members in whole steps, Write with clip, bias and activation,
+    GatedByInput and the head's last-token row."""
+    from charlotte_amd import matmul as mm
+
+    columns = 1024
+    widths = [16384, 8192, 8192]
+    data = [_data(r, seed=190 + i, columns=columns, gtype=Q4_0) for i, r in enumerate(widths)]
+    x = data[0][1]
+    ws = [run.weight(Q4_0, r, columns, d[0]) for r, d in zip(widths, data)]
+    totals64 = [oracle.matmul_f64(Q4_0, d[0], r, columns, x)[0] for r, d in zip(widths, data)]
+    f32 = [oracle.matmul_f32(Q4_0, d[0], r, columns, x, threads=8) for r, d in zip(widths, data)]
+    got = run.product([mm.Member(w) for w in ws], x, 1, widths, epilogue=mm.Epilogue.QKV)
+    for i in range(3):
+        _within(got[i], totals64[i], f32[i], f"Q4_0 QKV member {i}")
+    big_stored = data[1][0] + data[2][0] + data[1][0] + data[2][0]  # stored blocks, row after row
+    big = [run.weight(Q4_0, 32768, columns, big_stored)]
+    t64 = np.concatenate([totals64[1], totals64[2], totals64[1], totals64[2]], axis=1)
+    t32 = np.concatenate([f32[1], f32[2], f32[1], f32[2]], axis=1)
+    u = np.random.default_rng(195).standard_normal((1, 32768), dtype=np.float32)
+    got = run.product([mm.Member(big[0])], x, 1, [32768], epilogue=mm.Epilogue.GatedByInput, gate_input=u,
+                      gate_input_stride=32768, activation=mm.Activation.SiLU)[0]
+    want = oracle.gated_by_input(t64.astype(np.float32), u, activation=0)
+    _within(got, want.astype(np.float64), want, "Q4_0 GatedByInput")
+    clip = np.array([-1.0, 1.5, -3.0, 2.5], np.float32)
+    bias = np.linspace(-0.5, 0.5, 32768, dtype=np.float32)
+    xc = oracle.clamp(x, clip[0], clip[1])
+    c64, _ = oracle.matmul_f64(Q4_0, big_stored, 32768, columns, xc)
+    got = run.product([mm.Member(big[0])], x, 1, [32768], clip=clip, bias=bias, activated=True,
+                      activation=mm.Activation.GeluTanh)[0]
+    want = oracle.finish(c64.astype(np.float32), clip=clip, bias=bias, activated=True,
+                         activation=int(mm.Activation.GeluTanh))
+    _within(got, want.astype(np.float64), want, "Q4_0 Write with options")
+    xs = np.concatenate([np.random.default_rng(196).standard_normal((2, columns), dtype=np.float32), x])
+    got = run.write(big[0], xs, 3, rows=mm.Rows.LastToken)
+    _within(got, t64, t32, "Q4_0 last token")
+    for w in ws + big:
+        w.free()
+
+
+def test_limbs_q4_0_head_against_canonical(run, canonical_run):
+    """A Q4_0 vocabulary head (151,936 x 1,024, Qwen3's vocabulary): the limbs
+    path within the bar of the canonical path, the oracle's bits at every size."""
+    from charlotte_amd import synthetic
+
+    rows, columns = 151936, 1024
+    rng = np.random.default_rng(0xC8)
+    stored = synthetic.weight(rng, Q4_0, rows, columns)
+    x = synthetic.activations(rng, 1, columns)
+    w = run.weight(Q4_0, rows, columns, stored)
+    got = run.write(w, x, 1)
+    w.free()
+    wc = canonical_run.weight(Q4_0, rows, columns, stored)
+    want = canonical_run.write(wc, x, 1)
+    wc.free()
+    assert np.isfinite(got).all()
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64)).max()
+    top = np.abs(want).max()
+    assert err <= TOLERANCE * top, f"{err:.3e} vs {top:.3e}"
+    assert int(np.argmax(got)) == int(np.argmax(want))

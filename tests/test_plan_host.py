@@ -154,9 +154,14 @@ def test_q4_0_k_1024_to_8192_in_whole_steps_is_the_streamed_decode(shapes, colum
     p = mm.plan_launch(_write(shapes(Q4_0, rows, columns)), 1)
     assert (p.kernel, p.canonical, p.lanes_a_row, p.groups_a_lane) == (K.GEMV_STREAM4, True, columns // 256, 8)
     assert (p.tile_rows, p.tiles, p.workgroups) == (step_rows, rows // step_rows, 512)
-    # the INT8_LIMBS path is Q6_K's: Q4_0 stays canonical
+    # INT8_LIMBS: the same kernel's limbs form at K = 1,024 and 2,048; canonical past them
     limbs = mm.plan_launch(_write(shapes(Q4_0, rows, columns)), 1, mm.Target(256, gemv_path=mm.GemvPath.INT8_LIMBS))
-    assert limbs.kernel == K.GEMV_STREAM4 and limbs.canonical
+    assert limbs.kernel == K.GEMV_STREAM4 and limbs.canonical == (columns > 2048)
+    assert (limbs.tile_rows, limbs.tiles, limbs.workgroups) == (step_rows, rows // step_rows, 512)
+    # a product under 2^20 groups goes to the 32-lane kernel, canonical whatever the setting
+    small = mm.plan_launch(_write(shapes(Q4_0, 2**20 // (columns // 32) - step_rows, columns)), 1,
+                           mm.Target(256, gemv_path=mm.GemvPath.INT8_LIMBS))
+    assert small.kernel == K.GEMV_RANGES and small.canonical
     w = shapes(Q4_0, 65536, columns)
     big = 2**20 // (columns // 32)  # rows of 2^20 groups: the smallest product streamed
     # a member starting inside a step, or not whole steps long: the reference mapping
