@@ -22,6 +22,13 @@
 // Its range sums wait in the wave's LDS for a batch of steps, and lane t
 // then adds row t's 32 sums in order from zero. The bits are every other
 // kernel's.
+//
+// The LIMBS form (the GEMV path INT8_LIMBS at K = 1,024 and 2,048,
+// limbs.hpp) stages x as int8 limb records in the places of its float4 and
+// decodes a group with 24 v_dot4_i32_i8: about half the VALU work a step
+// (Q4_0 head 23.3 -> 21.1 us). At K = 4,096 and 8,192 it measured slower
+// than the canonical decode and is not used there. Not the canonical bits:
+// within 1e-5 of them.
 #include <algorithm>
 
 #include "decode.hpp"
