@@ -150,14 +150,16 @@ __device__ __forceinline__ float4 clamp_input(const Product& a, float4 v) {
 // plain ones — QKV, and a Write with no options — which store the total
 // and keep the registers the rest would hold.
 //
-// THROUGH stores at system scope (sc0 sc1), written through the L2: a small
-// decode's few outputs then leave nothing dirty for the end of the kernel to
-// write back (Qwen3 0.6B's decode step 486 -> 479 us); large outputs (the
-// prefill tiles) store the ordinary way, at less than half the rate through.
+// THROUGH stores at system scope (a relaxed atomic store: global_store_dword
+// sc0 sc1, which the compiler sees and counts), written through the L2: a
+// small decode's few outputs then leave nothing dirty for the end of the
+// kernel to write back (Qwen3 0.6B's decode step 486 -> 479 us); large
+// outputs (the prefill tiles) store the ordinary way, at less than half the
+// rate through.
 template <bool THROUGH>
 __device__ __forceinline__ void put(float v, float* at) {
     if constexpr (THROUGH)
-        __asm__ __volatile__("global_store_dword %0, %1, off sc0 sc1" : : "v"(at), "v"(v) : "memory");
+        __hip_atomic_store(at, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     else
         *at = v;
 }
