@@ -6,7 +6,8 @@ bar as stated, as the matrix-core prefill's tests hold it).
 
 The path is not bit-exact by design. These tests pin its error at the shapes
 it is built for (Q6_K, K = 1,152 and 1,024 with rows in 16s, 2,048 with rows
-in 8s), over inputs of every scale,
+in 8s; Q4_0, K = 1,024 and 2,048 in products of 2^20 groups or more), over
+inputs of every scale,
 with outliers, zeros and non-finite values, through each epilogue it takes;
 and that every other decode still runs in the canonical order, bit for bit.
 """
