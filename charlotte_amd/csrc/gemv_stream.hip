@@ -305,11 +305,11 @@ hipError_t launch_gemv_stream(const Product& a, uint32_t compute_units, bool lim
     const uint32_t steps = a.rows / kStepRows;
     const uint32_t blocks = std::min<uint32_t>(2 * compute_units, (steps + kStreamWaves - 1) / kStreamWaves);
     const bool plain = plain_epilogue(a);
-    // Every wave's steps but the last round's, and that round's steps on the
-    // first half of the grid: C2 (8 steps a wave) 49.6 -> 48.5 and 51.0 ->
-    // 49.7 us canonical, the INT8_LIMBS form unchanged (A/B on one box).
-    const uint32_t waves = blocks * kStreamWaves, rounds = steps / waves;
-    const uint32_t common = rounds >= 2 ? (rounds - 1) * waves : steps;
+    // One round's worth of steps, the last, on the first half of the grid
+    // alone: C2 (8 steps a wave) 49.6 -> 48.5 and 51.0 -> 49.7 us canonical,
+    // the INT8_LIMBS form unchanged (A/B on one box).
+    const uint32_t waves = blocks * kStreamWaves;
+    const uint32_t common = steps >= 2 * waves ? steps - waves : steps;
     if (limbs) {
         if (plain)
             hipLaunchKernelGGL((gemv_stream<false, true>), dim3(blocks), dim3(256), 0, stream, a, steps, common);

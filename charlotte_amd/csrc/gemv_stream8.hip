@@ -43,7 +43,7 @@ struct StepRun8 {
 }  // namespace
 
 template <uint32_t G, bool FULL, bool LIMBS>
-__global__ __launch_bounds__(256, 2) void gemv_stream8(Product a, uint32_t steps) {
+__global__ __launch_bounds__(256, 2) void gemv_stream8(Product a, uint32_t steps, uint32_t common) {
     constexpr uint32_t L = G / 8;              // lanes a row
     constexpr uint32_t kRows = 64 / L;         // rows a step
     constexpr uint32_t kRanges = 32 / L;       // ranges a lane
@@ -235,7 +235,15 @@ __global__ __launch_bounds__(256, 2) void gemv_stream8(Product a, uint32_t steps
         __asm__ __volatile__("" ::: "memory");
         StepRun8 run;
         take(run);
-        const uint32_t next = step + waves;
+        // Steps below `common` are dealt to every wave in turn; the rest to
+        // the first half of the grid alone (w < waves / 2), the CUs' first
+        // workgroups, which win the SIMDs' issue arbitration and finish
+        // sooner when dealt the same (as in gemv_stream.hip).
+        uint32_t next = step + waves;
+        if (next >= common) {
+            const uint32_t fast = waves / 2, w = blockIdx.x * kWaves8 + wave;
+            next = step < common ? (w < fast ? common + w : steps) : step + fast;
+        }
         if (next < steps) issue(next);
         if constexpr (LIMBS)
             decode_limbs(step, run);
@@ -260,16 +268,21 @@ template <uint32_t G>
 static void go8(const Product& a, uint32_t compute_units, bool limbs, hipStream_t stream) {
     const uint32_t steps = a.rows / (64 / (G / 8));
     const uint32_t blocks = std::min<uint32_t>(2 * compute_units, (steps + kWaves8 - 1) / kWaves8);
+    // The last round's worth of steps on the first half of the grid: Q6_K
+    // heads 151,936 x 1,024 32.5 -> 31.6 us, 128,256 x 2,048 47.5 -> 46.6,
+    // 262,144 x 1,024 48.1 -> 47.6 (two rounds A/B on one box).
+    const uint32_t waves = blocks * kWaves8;
+    const uint32_t common = steps >= 2 * waves ? steps - waves : steps;
     const bool plain = plain_epilogue(a);
     if (limbs) {
         if (plain)
-            hipLaunchKernelGGL((gemv_stream8<G, false, true>), dim3(blocks), dim3(256), 0, stream, a, steps);
+            hipLaunchKernelGGL((gemv_stream8<G, false, true>), dim3(blocks), dim3(256), 0, stream, a, steps, common);
         else
-            hipLaunchKernelGGL((gemv_stream8<G, true, true>), dim3(blocks), dim3(256), 0, stream, a, steps);
+            hipLaunchKernelGGL((gemv_stream8<G, true, true>), dim3(blocks), dim3(256), 0, stream, a, steps, common);
     } else if (plain) {
-        hipLaunchKernelGGL((gemv_stream8<G, false, false>), dim3(blocks), dim3(256), 0, stream, a, steps);
+        hipLaunchKernelGGL((gemv_stream8<G, false, false>), dim3(blocks), dim3(256), 0, stream, a, steps, common);
     } else {
-        hipLaunchKernelGGL((gemv_stream8<G, true, false>), dim3(blocks), dim3(256), 0, stream, a, steps);
+        hipLaunchKernelGGL((gemv_stream8<G, true, false>), dim3(blocks), dim3(256), 0, stream, a, steps, common);
     }
 }
 
