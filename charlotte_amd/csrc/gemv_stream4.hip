@@ -62,7 +62,7 @@ struct StepRun4 {
 }  // namespace
 
 template <uint32_t G, bool FULL, uint32_t W, bool LIMBS>
-__global__ __launch_bounds__(64 * W) void gemv_stream4(Product a, uint32_t steps) {
+__global__ __launch_bounds__(64 * W) void gemv_stream4(Product a, uint32_t steps, uint32_t common) {
     constexpr uint32_t L = G / 8;           // lanes a row
     constexpr uint32_t kRows = 64 / L;      // rows a step
     constexpr uint32_t kRanges = 32 / L;    // ranges a lane
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(64 * W) void gemv_stream4(Product a, uint32_t steps
     // orders the writes before the reads, and the reads before the next
     // batch's writes. `first` is the batch's first step; its steps are
     // `waves` apart.
-    auto flush = [&](uint32_t first, uint32_t count) {
+    auto flush = [&](uint32_t first, uint32_t count, uint32_t stride) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(64 * W) void gemv_stream4(Product a, uint32_t steps
             float total = 0.0f;
 #pragma unroll
             for (int k = 0; k < 32; ++k) total = total + sums_s[33 * lane + k];
-            const uint32_t p = (first + (lane / kRows) * waves) * kRows + lane % kRows;
+            const uint32_t p = (first + (lane / kRows) * stride) * kRows + lane % kRows;
             if (p < a.rows) emit<FULL>(a, p, 0, out_token, total, 0.0f);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -232,19 +232,30 @@ __global__ __launch_bounds__(64 * W) void gemv_stream4(Product a, uint32_t steps
         __syncthreads();
     }
     if (step >= steps) return;
-    uint32_t slot = 0, first = step;
+    uint32_t slot = 0, first = step, stride = waves;
     while (true) {
         __builtin_amdgcn_s_waitcnt(kVmcnt0);
         __asm__ __volatile__("" ::: "memory");
         StepRun4 run;
         take(run);
-        const uint32_t next = step + waves;
+        // Steps below `common` are dealt to every wave in turn; the rest to
+        // the first half of the grid alone (the CUs' first workgroups, which
+        // finish sooner when dealt the same). A batch's steps are `stride`
+        // apart, so a batch ends where the dealing changes.
+        uint32_t next = step + waves;
+        bool turn = false;
+        if (next >= common) {
+            const uint32_t fast = waves / 2, w = blockIdx.x * W + wave;
+            turn = step < common;
+            next = turn ? (w < fast ? common + w : steps) : step + fast;
+        }
         if (next < steps) issue(next);
         decode(slot, run);
-        if (++slot == kBatch || next >= steps) {
-            flush(first, slot);
+        if (++slot == kBatch || next >= steps || turn) {
+            flush(first, slot, stride);
             slot = 0;
             first = next;
+            if (turn) stride = waves / 2;
         }
         if (next >= steps) break;
         step = next;
@@ -277,10 +288,15 @@ static void go4(const Product& a, uint32_t compute_units, hipStream_t stream) {
     constexpr uint32_t W = kS4Waves[s4_index(G)];
     const uint32_t steps = a.rows / (64 / (G / 8));
     const uint32_t blocks = static_cast<uint32_t>(gemv_stream4_workgroups(G, compute_units, steps));
+    // The last round's worth of steps on the first half of the grid: Q4_0
+    // head 151,936 x 1,024 21.6 -> 20.3 us, 65,536 x 2,048 18.4 -> 17.9,
+    // 32,768 x 8,192 32.4 -> 32.1 (two rounds A/B on one box).
+    const uint32_t waves = blocks * W;
+    const uint32_t common = steps >= 2 * waves ? steps - waves : steps;
     if (plain_epilogue(a))
-        hipLaunchKernelGGL((gemv_stream4<G, false, W, LIMBS>), dim3(blocks), dim3(64 * W), 0, stream, a, steps);
+        hipLaunchKernelGGL((gemv_stream4<G, false, W, LIMBS>), dim3(blocks), dim3(64 * W), 0, stream, a, steps, common);
     else
-        hipLaunchKernelGGL((gemv_stream4<G, true, W, LIMBS>), dim3(blocks), dim3(64 * W), 0, stream, a, steps);
+        hipLaunchKernelGGL((gemv_stream4<G, true, W, LIMBS>), dim3(blocks), dim3(64 * W), 0, stream, a, steps, common);
 }
 
 template <bool LIMBS>
