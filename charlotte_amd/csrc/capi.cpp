@@ -148,7 +148,14 @@ Verdict describe(const charlotte_hip_matmul_desc* desc, uint32_t tokens, const c
     // The options are a Write's; a gated product may be clipped (matmul.h:229-255, 623-629).
     if ((d.bias || d.activated) && d.epilogue != CHARLOTTE_HIP_MATMUL_WRITE)
         return bad("bias and activated are a Write's options");
-    if (d.clip && d.epilogue != CHARLOTTE_HIP_MATMUL_WRITE && !gated)
+    // The four bounds come together (matmul.cpp:280-281 sets all four words
+    // or none), each a 4-byte word of its own.
+    const bool clip = d.clip[0] || d.clip[1] || d.clip[2] || d.clip[3];
+    if (clip && !(d.clip[0] && d.clip[1] && d.clip[2] && d.clip[3]))
+        return bad("clip takes its four bounds or none");
+    for (const float* bound : d.clip)
+        if (reinterpret_cast<uintptr_t>(bound) % 4 != 0) return bad("a clip bound not 4-byte aligned");
+    if (clip && d.epilogue != CHARLOTTE_HIP_MATMUL_WRITE && !gated)
         return bad("clip is a Write's or a gated product's option");
     if (gated && d.member_count != 2) return bad("a gated product takes two members, gate and up");
     if (gated && d.members[0].rows != d.members[1].rows) return bad("gate and up rows differ");
@@ -211,7 +218,7 @@ Verdict describe(const charlotte_hip_matmul_desc* desc, uint32_t tokens, const c
     a.gate_stride = d.gate_input_stride;
     a.gate_column = d.gate_input_column;
     a.gate_input = d.gate_input;
-    a.clip = d.clip;
+    for (int i = 0; i < 4; ++i) a.clip[i] = d.clip[i];
     a.bias = d.bias;
     a.activated = d.activated ? 1u : 0u;
     *out = a;
@@ -246,7 +253,7 @@ Verdict plan_product(const chm::Product& a, uint32_t format, const Target& t, ch
         return {};
     }
     bool split = false;
-    const bool options = a.clip || a.bias || a.activated;
+    const bool options = chm::clipped(a) || a.bias || a.activated;
     if (!options && a.epilogue != chm::kGated && range_sums_bytes && gate.denominator) {
         const uint64_t fits = range_sums_bytes / 4 / (uint64_t{a.rows} * 32);
         const uint64_t most = std::min<uint64_t>(split_tokens_of(a.epilogue, a.rows, uint64_t{a.groups} * 32, gate), fits);
@@ -552,18 +559,12 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch_static(charlotte_hip_mat
     uint32_t format = 0;
     Verdict v = describe(desc, tokens, ctx, &a, &format);
     chm::Plan plan;
-    // The plan with room for any split first: a step the gate splits whose
-    // range sums pass the static array is refused, not run another way.
-    if (v.ok()) v = plan_product(a, format, target_of(ctx), gate, ~uint64_t{0}, &plan);
+    // Planned as the ordinary launch plans with a buffer of the static
+    // array's size: a step whose range sums would not fit it runs the tiled
+    // form, whose bits are the split's (the same order of addition).
+    if (v.ok())
+        v = plan_product(a, format, target_of(ctx), gate, CHARLOTTE_HIP_MATMUL_STATIC_SCRATCH_BYTES, &plan);
     if (!v.ok()) return fail(ctx, v.status, v.message);
-    if (plan.kernel == chm::kGemmSplit) {
-        const uint64_t need = uint64_t{4} * 32 * a.tokens * a.rows;
-        if (need > CHARLOTTE_HIP_MATMUL_STATIC_SCRATCH_BYTES)
-            return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT,
-                        "launch_static: the split's range sums need " + std::to_string(need) +
-                            " bytes, past the static scratch's " +
-                            std::to_string(uint64_t{CHARLOTTE_HIP_MATMUL_STATIC_SCRATCH_BYTES}));
-    }
     return run_plan(ctx, a, format, plan, ctx->scratch, stream);
 }
 

@@ -134,8 +134,8 @@ __global__ __launch_bounds__(256, kRangesMinBlocks) void gemv_ranges(Product a, 
                 }
             }
         }
-        if (a.clip) {
-            const float lo = a.clip[0], hi = a.clip[1];
+        if (clipped(a)) {
+            const float lo = *a.clip[0], hi = *a.clip[1];
 #pragma unroll
             for (int k = 0; k < SPAN * 32; ++k) xr[k] = clamp_to(xr[k], lo, hi);
         }

@@ -142,6 +142,11 @@ int chx_event_elapsed_ms(float* ms, void* start, void* stop) {
 int chx_capture_begin(void* s) {
     return hipStreamBeginCapture(static_cast<hipStream_t>(s), hipStreamCaptureModeThreadLocal);
 }
+// Global mode: while it lasts, an unsafe call (an allocation, a free, a
+// synchronous copy) from any thread of the process fails the capture.
+int chx_capture_begin_global(void* s) {
+    return hipStreamBeginCapture(static_cast<hipStream_t>(s), hipStreamCaptureModeGlobal);
+}
 int chx_capture_end(void* s, void** exec) {
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(static_cast<hipStream_t>(s), &g);

@@ -38,9 +38,13 @@ struct Product {
     uint32_t gate_column;
     uint32_t activated;
     const float* gate_input;
-    const float* clip;     // device: in_min, in_max, out_min, out_max, or null
+    // device: the four bounds in_min, in_max, out_min, out_max, each its own
+    // word wherever the caller keeps it, or all four null
+    const float* clip[4];
     const float* bias;     // device, or null
 };
+
+__host__ __device__ __forceinline__ bool clipped(const Product& a) { return a.clip[0] != nullptr; }
 
 // Where product row p's weights lie: its member's piece and p's row within
 // it. Members are compared with constant indices only, so their fields stay
@@ -126,7 +130,7 @@ __device__ __forceinline__ float activate(uint32_t activation, float g) {
 
 // Whether a product's epilogue is a plain store (no FULL kernel needed).
 inline bool plain_epilogue(const Product& a) {
-    return a.epilogue == kQKV || (a.epilogue == kWrite && !a.clip && !a.bias && !a.activated);
+    return a.epilogue == kQKV || (a.epilogue == kWrite && !clipped(a) && !a.bias && !a.activated);
 }
 
 // WGSL's clamp(e, low, high): min(max(e, low), high). Exact.
@@ -135,8 +139,8 @@ __device__ __forceinline__ float clamp_to(float v, float lo, float hi) { return 
 // The input as a product reads it: clamped to its bounds where clipped
 // (matmul.wgsl:117-124). Applied as x is staged.
 __device__ __forceinline__ float4 clamp_input(const Product& a, float4 v) {
-    if (!a.clip) return v;
-    const float lo = a.clip[0], hi = a.clip[1];
+    if (!clipped(a)) return v;
+    const float lo = *a.clip[0], hi = *a.clip[1];
     return {clamp_to(v.x, lo, hi), clamp_to(v.y, lo, hi), clamp_to(v.z, lo, hi), clamp_to(v.w, lo, hi)};
 }
 
@@ -174,7 +178,10 @@ __device__ __forceinline__ void emit(const Product& a, uint32_t p, uint32_t toke
     if (a.epilogue == kGated) {
         if (p & 1u) return;
         float g = total, u = partner;
-        if (a.clip) g = clamp_to(g, a.clip[2], a.clip[3]), u = clamp_to(u, a.clip[2], a.clip[3]);
+        if (clipped(a)) {
+            const float lo = *a.clip[2], hi = *a.clip[3];
+            g = clamp_to(g, lo, hi), u = clamp_to(u, lo, hi);
+        }
         put<THROUGH>(activate(a.activation, g) * u, &a.m[0].out[static_cast<uint64_t>(token) * a.m[0].out_width + (p >> 1)]);
         return;
     }
@@ -184,7 +191,7 @@ __device__ __forceinline__ void emit(const Product& a, uint32_t p, uint32_t toke
         y = activate(a.activation, y) *
             a.gate_input[static_cast<uint64_t>(in_token) * a.gate_stride + a.gate_column + w.o];
     } else if (a.epilogue == kWrite) {
-        if (a.clip) y = clamp_to(y, a.clip[2], a.clip[3]);
+        if (clipped(a)) y = clamp_to(y, *a.clip[2], *a.clip[3]);
         if (a.bias) y = y + a.bias[w.o];
         if (a.activated) y = activate(a.activation, y);
     }

@@ -34,6 +34,7 @@ _SIGS = {
     "chx_event_sync": (_c.c_int, [_c.c_void_p]),
     "chx_event_elapsed_ms": (_c.c_int, [_c.POINTER(_c.c_float), _c.c_void_p, _c.c_void_p]),
     "chx_capture_begin": (_c.c_int, [_c.c_void_p]),
+    "chx_capture_begin_global": (_c.c_int, [_c.c_void_p]),
     "chx_capture_end": (_c.c_int, [_c.c_void_p, _c.POINTER(_c.c_void_p)]),
     "chx_graph_launch": (_c.c_int, [_c.c_void_p, _c.c_void_p]),
     "chx_graph_destroy": (_c.c_int, [_c.c_void_p]),
@@ -159,8 +160,11 @@ class Event:
 class Graph:
     """The launches a callable makes on `stream`, captured once, replayable."""
 
-    def __init__(self, stream: Stream, body):
-        check(lib.chx_capture_begin(stream.handle), "capture begin")
+    def __init__(self, stream: Stream, body, global_mode=False):
+        """global_mode: capture in hipStreamCaptureModeGlobal, under which any
+        allocation, free or synchronous copy the body makes fails the capture."""
+        begin = lib.chx_capture_begin_global if global_mode else lib.chx_capture_begin
+        check(begin(stream.handle), "capture begin")
         try:
             body()
         finally:

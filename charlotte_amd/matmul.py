@@ -156,7 +156,7 @@ class _Desc(ctypes.Structure):
         ("gate_input", ctypes.c_void_p),
         ("gate_input_stride", ctypes.c_uint32),
         ("gate_input_column", ctypes.c_uint32),
-        ("clip", ctypes.c_void_p),
+        ("clip", ctypes.c_void_p * 4),
         ("bias", ctypes.c_void_p),
         ("activated", ctypes.c_uint32),
         ("row_divisor", ctypes.c_uint32),
@@ -413,7 +413,7 @@ class MatmulLaunch:
     gate_input: int = 0
     gate_input_stride: int = 0
     gate_input_column: int = 0
-    clip: int = 0
+    clip: Sequence[int] = ()  # four device pointers: in_min, in_max, out_min, out_max (or none)
     bias: int = 0
     activated: bool = False
     row_divisor: int = 1
@@ -431,7 +431,9 @@ class MatmulLaunch:
             d.outputs[i] = o
         d.out_width = self.out_width
         d.gate_input, d.gate_input_stride, d.gate_input_column = self.gate_input, self.gate_input_stride, self.gate_input_column
-        d.clip, d.bias, d.activated = self.clip, self.bias, int(self.activated)
+        for i, bound in enumerate(self.clip):
+            d.clip[i] = bound
+        d.bias, d.activated = self.bias, int(self.activated)
         d.row_divisor = self.row_divisor
         return d
 

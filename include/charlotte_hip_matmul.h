@@ -249,10 +249,17 @@ typedef struct {
     const float* gate_input;
     uint32_t gate_input_stride;
     uint32_t gate_input_column;
-    /* Options (matmul.h:229-255): `clip` four device floats in_min, in_max,
-     * out_min, out_max, or NULL; `bias` device floats, one an output row, or
-     * NULL (WRITE); `activated` nonzero applies `activation` last (WRITE). */
-    const float* clip;
+    /* Options (matmul.h:229-255). `clip`: the four bounds in_min, in_max,
+     * out_min, out_max, each a device pointer to its own F32 word — the
+     * reference keeps them as four scalars beside the weight and reads each
+     * by its own word offset into the product's span (Constants.clip, a
+     * vec4<u32> of first words, matmul.h:275-277, matmul.cpp:280-281), so
+     * each pointer is that span's base plus 4 x its word; all four NULL for
+     * an unclipped product (any other mix is refused). Each bound is read on
+     * the device, never on the host. `bias` device floats, one an output
+     * row, or NULL (WRITE); `activated` nonzero applies `activation` last
+     * (WRITE). */
+    const float* clip[4];
     const float* bias;
     uint32_t activated;
     /* kernels::Launch::row_divisor (interface.h:270-279): the launch's rows

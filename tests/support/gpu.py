@@ -19,7 +19,9 @@ class Runner:
                 gate_input_stride=0, gate_input_column=0, clip=None, bias=None, activated=False):
         """Run one product over the first `tokens` rows of x; return each output as [rows_written, width].
 
-        gate_input, clip and bias are host arrays, copied to the device for the launch."""
+        gate_input, clip and bias are host arrays, copied to the device for the launch. The
+        four clip bounds go to words 32 bytes apart in one buffer, each bound its own
+        pointer, as the reference's file keeps them (matmul_rows.gguf's clip_* tensors)."""
         x = np.ascontiguousarray(x, np.float32)
         xb = hx.Buffer.of(x)
         out_rows = 1 if rows == mm.Rows.LastToken else tokens
@@ -28,11 +30,17 @@ class Runner:
             o.fill(0xFF)  # NaN: an output left unwritten shows
         extra = {}
         owned = [xb, *outs]
-        for name, value in (("gate_input", gate_input), ("clip", clip), ("bias", bias)):
+        for name, value in (("gate_input", gate_input), ("bias", bias)):
             if value is not None:
                 b = hx.Buffer.of(np.asarray(value, np.float32))
                 extra[name] = b.ptr
                 owned.append(b)
+        if clip is not None:
+            spaced = np.full((4, 8), np.nan, np.float32)  # padding words read as NaN if ever misread
+            spaced[:, 0] = np.asarray(clip, np.float32)
+            b = hx.Buffer.of(spaced)
+            extra["clip"] = [b.ptr + 32 * i for i in range(4)]
+            owned.append(b)
         sums = hx.Buffer(sums_bytes) if sums_bytes else None
         if sums:
             sums.fill(0xFF)

@@ -36,15 +36,18 @@ def run():
 
 def _edge_weight(gtype, rows, columns, seed=None):
     """The format's edge blocks (their codes and later scales from the LCG at
-    `seed`), and every fifth block's d set to one of the edge scales in turn."""
+    `seed`), and every fifth block's d set to one of the edge scales in turn.
+    Past 8,192 blocks the first 8,192 repeat (the LCG in Python is slow), the
+    edge scales still every fifth block over the whole weight."""
     count = rows * columns // WEIGHTS_A_BLOCK[gtype]
+    n = min(count, 8192)
     make = B.q4_0_edge_blocks if gtype == Q4_0 else B.q6_k_edge_blocks
-    stored = bytearray(make(count) if seed is None else make(count, seed=seed))
     size, at = BLOCK_BYTES[gtype], D_OFFSET[gtype]
-    for b in range(0, count, 5):
-        d = B.EDGE_SCALES[(b // 5) % len(B.EDGE_SCALES)]
-        stored[size * b + at : size * b + at + 2] = int(d).to_bytes(2, "little")
-    return bytes(stored)
+    base = np.frombuffer(make(n) if seed is None else make(n, seed=seed), np.uint8).reshape(n, size)
+    stored = np.tile(base, (-(-count // n), 1))[:count].copy()
+    scales = np.array(B.EDGE_SCALES, "<u2")[np.arange(-(-count // 5)) % len(B.EDGE_SCALES)]
+    stored[::5, at : at + 2] = scales.view(np.uint8).reshape(-1, 2)
+    return stored.tobytes()
 
 
 def _special_inputs(columns, seed):
@@ -73,19 +76,34 @@ def _check(got, want, what):
     assert bad.size == 0, f"{what}: {bad.size} differ; first got {got[~nan_w][bad[0]]!r} want {want[~nan_w][bad[0]]!r}"
 
 
-# (format, rows, K): the ranges kernel with x in registers and staged in LDS,
-# the L = 4 kernel (rows not whole 16-row steps), the streamed K = 1,152 and
-# K = 1,024 / 2,048 kernels.
-CASES = [(Q4_0, 256, 1024), (Q4_0, 96, 4096), (Q6_K, 70, 1152), (Q6_K, 64, 1152), (Q6_K, 64, 1024),
-         (Q6_K, 48, 2048)]
+# (format, rows, K, the decode kernel the plan names): the ranges kernel with
+# x in registers and staged in LDS, the L = 4 kernel (rows not whole 16-row
+# steps), the streamed K = 1,152 and K = 1,024 / 2,048 Q6_K kernels; the
+# streamed Q4_0 kernel at K = 1,024 with its dealing's turn (4,096 steps over
+# 2,048 waves: the last round's steps go to the first half of the grid) and
+# at K = 8,192; the wide Q4_0 kernel (K = 9,216, an odd number of two-row
+# steps' rows); the chunked kernel past K = 8,192.
+CASES = [(Q4_0, 256, 1024, "GEMV_RANGES"), (Q4_0, 96, 4096, "GEMV_RANGES"), (Q6_K, 70, 1152, "GEMV_QUARTERS"),
+         (Q6_K, 64, 1152, "GEMV_STREAM"), (Q6_K, 64, 1024, "GEMV_STREAM8"), (Q6_K, 48, 2048, "GEMV_STREAM8"),
+         (Q4_0, 65536, 1024, "GEMV_STREAM4"), (Q4_0, 4096, 8192, "GEMV_STREAM4"), (Q4_0, 66, 9216, "GEMV_WIDE"),
+         (Q6_K, 64, 9216, "GEMV_CHUNKED")]
 
 
-@pytest.mark.parametrize("gtype,rows,columns", CASES)
-def test_edges_decoded_and_prefilled(oracle, run, gtype, rows, columns):
+def _kernel_of(m, tokens=1):
+    from charlotte_amd import matmul as mm
+
+    return mm.plan_launch(m, tokens).kernel.name
+
+
+@pytest.mark.parametrize("gtype,rows,columns,kernel", CASES)
+def test_edges_decoded_and_prefilled(oracle, run, gtype, rows, columns, kernel):
+    from charlotte_amd import matmul as mm
+
     stored = _edge_weight(gtype, rows, columns)
     x = _special_inputs(columns, seed=rows + columns)
     w = run.weight(gtype, rows, columns, stored)
     try:
+        assert _kernel_of(mm.MatmulLaunch([mm.Member(w)], 0x10000, [0x20000])) == kernel
         want = oracle.matmul_f32(gtype, stored, rows, columns, x, threads=THREADS)
         assert np.isfinite(want[0]).mean() > 0.5 and np.isfinite(want[3]).mean() > 0.5 and np.isnan(want[2]).all()
         for t in range(5):
@@ -97,18 +115,24 @@ def test_edges_decoded_and_prefilled(oracle, run, gtype, rows, columns):
         w.free()
 
 
-@pytest.mark.parametrize("columns", [1024, 1152])
-def test_edges_through_the_epilogues(oracle, run, columns):
+@pytest.mark.parametrize("gtype,rows,columns,kernels", [
+    (Q4_0, 128, 1024, ("GEMV_RANGES", "GEMV_RANGES")), (Q6_K, 64, 1152, ("GEMV_QUARTERS", "GEMV_STREAM")),
+    (Q4_0, 66, 9216, ("GEMV_WIDE", "GEMV_WIDE")), (Q4_0, 32768, 1024, ("GEMV_RANGES", "GEMV_STREAM4"))])
+def test_edges_through_the_epilogues(oracle, run, gtype, rows, columns, kernels):
     """The same weights and inputs through GatedActivation (SiLU) and Write
     with bias and GELU-tanh: the activations of huge, infinite and NaN
-    totals, decoded and prefilled."""
+    totals, decoded and prefilled. `kernels`: the decodes of the gated
+    product and of the Write, by the plan."""
     from charlotte_amd import matmul as mm
 
-    gtype, rows = (Q4_0, 128) if columns == 1024 else (Q6_K, 64)
     stored = [_edge_weight(gtype, rows, columns), _edge_weight(gtype, rows, columns, seed=0x68E31DA4)]
     x = _special_inputs(columns, seed=7 * columns)
     ws = [run.weight(gtype, rows, columns, s) for s in stored]
     try:
+        gated = mm.MatmulLaunch([mm.Member(ws[0]), mm.Member(ws[1])], 0x10000, [0x20000],
+                                epilogue=mm.Epilogue.GatedActivation)
+        write = mm.MatmulLaunch([mm.Member(ws[0])], 0x10000, [0x20000], bias=0x30000, activated=True)
+        assert (_kernel_of(gated), _kernel_of(write)) == kernels
         gate = oracle.matmul_f32(gtype, stored[0], rows, columns, x, threads=THREADS)
         up = oracle.matmul_f32(gtype, stored[1], rows, columns, x, threads=THREADS)
         want_gated = oracle.gated(gate, up, activation=0)

@@ -286,7 +286,7 @@ def test_epilogue_argument_errors(run, fixture_tensors):
         (dict(members=[mm.Member(w, rows=8), mm.Member(w, rows=9)], epilogue=mm.Epilogue.GatedActivation), "rows differ"),
         (dict(members=[mm.Member(w)], epilogue=mm.Epilogue.GatedByInput), "without its input"),
         (dict(members=[mm.Member(w)], epilogue=mm.Epilogue.QKV, bias=xb.ptr), "Write's options"),
-        (dict(members=[mm.Member(w)], epilogue=mm.Epilogue.GatedByInput, gate_input=xb.ptr, clip=xb.ptr), "clip"),
+        (dict(members=[mm.Member(w)], epilogue=mm.Epilogue.GatedByInput, gate_input=xb.ptr, clip=[xb.ptr] * 4), "clip"),
     ]
     for kw, words in bad:
         m = mm.MatmulLaunch(input=xb.ptr, outputs=[out.ptr], **kw)

@@ -90,6 +90,25 @@ def test_descriptor_checks_match_the_launchs(shapes):
     _refused(mm.MatmulLaunch([mm.Member(w)], X, [Y0], epilogue=mm.Epilogue.GatedByInput), 1)
 
 
+def test_clip_takes_four_bound_words_or_none(shapes):
+    """The four bounds are four words of their own, wherever they lie (the
+    reference's Constants.clip, a first word each, matmul.cpp:280-281): four
+    pointers 32 bytes apart plan as a clipped product, in any order; some but
+    not all of them, or one not on a 4-byte word, are refused."""
+    w = shapes(Q4_0, 64, 1024)
+    span = 0x50000
+    apart = [span + 32 * i for i in range(4)]
+    assert mm.plan_launch(_write(w, clip=apart), 33).kernel == K.GEMM_TILED
+    assert mm.plan_launch(_write(w, clip=apart[::-1]), 1).kernel != K.NONE
+    assert mm.plan_launch(_write(w, clip=[span] * 4), 1).kernel != K.NONE
+    for partial in ([span, 0, 0, 0], [span, span + 4, span + 8, 0], [0, 0, 0, span]):
+        assert "four bounds or none" in _refused(_write(w, clip=partial), 1)
+    assert "4-byte" in _refused(_write(w, clip=[span, span + 2, span + 8, span + 12]), 1)
+    # An optioned product never splits (matmul.cpp:166-172), whatever the gate.
+    assert mm.plan_launch(_write(w, clip=apart), 32, gate=mm.kAlways, range_sums_bytes=1 << 24).kernel == K.GEMM_TILED
+    assert mm.plan_launch(_write(w), 32, gate=mm.kAlways, range_sums_bytes=1 << 24).kernel == K.GEMM_SPLIT
+
+
 # ---- the kernel each shape runs --------------------------------------------------
 
 
