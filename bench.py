@@ -79,6 +79,7 @@ class Setup:
         self.buffers = []
         self.weights = []
         self.settle_ms = SETTLE_MS
+        self.settle_replays = None  # a count of untimed replays in place of settle_ms (bounded under a tracer)
         self.last_first = None
 
     def buffer(self, array=None, nbytes=None):
@@ -128,11 +129,20 @@ class Setup:
         self.last_first = start.elapsed_ms(stop) / steps
         # replays in batches of ~10 ms, so the queue never drains while settling
         batch = max(1, int(10.0 / max(self.last_first * steps, 1e-3)))
-        t0 = time.time()
-        while time.time() - t0 < self.settle_ms / 1e3:
-            for _ in range(batch):
-                graph.launch()
-            self.stream.sync()
+        if self.settle_replays is not None:
+            # a fixed count (--settle-replays): a tracer records a bounded number of dispatches
+            left = self.settle_replays
+            while left > 0:
+                for _ in range(min(batch, left)):
+                    graph.launch()
+                left -= min(batch, left)
+                self.stream.sync()
+        else:
+            t0 = time.time()
+            while time.time() - t0 < self.settle_ms / 1e3:
+                for _ in range(batch):
+                    graph.launch()
+                self.stream.sync()
         times = []
         for _ in range(reps):
             start.record(self.stream)
@@ -345,7 +355,99 @@ def run_c3(S, steps, warmup, rng, fused=True):
                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
     if fused:
         out["floors"] = c3_floors(S, launches, steps, warmup)
+        out["breakdown"] = c3_breakdown(S, launches, ms, steps, warmup)
         out.update(decode_matches_prefill(S, launches, xs, rng))
+    return out
+
+
+C3_KINDS = ("qkv", "o", "gate_up", "down", "head")
+
+
+def prefix_breakdown(S, calls, kind_of, names, step_ms, steps, warmup, reads_of=None):
+    """Each kind of launch in a step timed in place, as the reference's
+    forward profile times a launch where timestamps inside a pass are not
+    granted (bench/forward_profile.cpp:44-68): a prefix's time T, and a
+    launch's time the difference of two prefixes' medians. Here the prefix
+    runs through kind k of every layer (the layers' launches of kinds < k, in
+    step order, each layer's weights its own, so the step's traffic through
+    the caches is kept), and the last kind (the head) is the whole step less
+    all layers:
+        launch of kind k = (T(kinds <= k) - T(kinds < k)) / its launches,
+    each T the median of 5 settled, timed replays of its graph, reported with
+    the spread (least and most) of the replays. Beside each kind: the same
+    launches alone back to back and, with `reads_of`, their reads-alone floor
+    in place (the products' bytes read in their launch shapes, nothing
+    decoded). calls: one launcher a launch, in step order; kind_of: each
+    launch's kind (an index into names)."""
+
+    def body_of(keep):
+        chosen = [c for c, k in zip(calls, kind_of) if k in keep]
+
+        def body():
+            for c in chosen:
+                c()
+        return body
+
+    def timed(body):
+        ms = S.time_graph(body, steps, warmup)
+        return ms * 1e3, [round(t * 1e3, 1) for t in (min(S.last_reps), max(S.last_reps))]
+
+    last = len(names) - 1
+    prefix = [(0.0, [0.0, 0.0])]
+    for k in range(1, last + 1):
+        prefix.append(timed(body_of(set(range(k)))))
+    prefix.append((step_ms * 1e3, None))
+    rows = {}
+    for k, name in enumerate(names):
+        count = sum(1 for kk in kind_of if kk == k)
+        in_place = (prefix[k + 1][0] - prefix[k][0]) / count
+        alone, alone_spread = timed(body_of({k}))
+        rows[name] = {"launches": count, "us_in_place": round(in_place, 2), "us_alone": round(alone / count, 2),
+                      "prefix_us": round(prefix[k + 1][0], 1), "prefix_spread_us": prefix[k + 1][1],
+                      "alone_spread_us": alone_spread}
+        line = (f"{name}: {count} launches, {in_place:.2f} us each in place (prefix {prefix[k][0]:.1f} -> "
+                f"{prefix[k + 1][0]:.1f} us), {alone / count:.2f} alone")
+        if reads_of is not None:
+            reads, _ = timed(reads_of({k}))
+            rows[name]["us_reads_alone"] = round(reads / count, 2)
+            line += f", reads alone {reads / count:.2f}"
+        log("  breakdown " + line)
+    return {"method": "prefix through kind k of every layer; median of 5 settled replays a prefix", "kinds": rows}
+
+
+def c3_breakdown(S, launches, step_ms, steps, warmup):
+    """The decode step's kinds (QKV, o, gate/up, down, head) timed in place
+    (prefix_breakdown), each beside its reads-alone floor."""
+    hx, mm = S.hx, S.mm
+    layers = (len(launches) - 1) // 4
+    kind_of = [i % 4 if i < 4 * layers else 4 for i in range(len(launches))]
+    calls = [lambda m=m: mm.launch(S.ctx, m, 1, stream=S.stream.handle) for m in launches]
+    # the reads-alone stand-ins, each at its place in the step's walk through memory
+    parts = floor_parts(mm, launches)
+    offsets, at = [], 0
+    for k, a, c in parts:
+        offsets.append(at)
+        at += a if k == "read" else a * c * 1024
+    buf = S.buffer(nbytes=max(at, 2 * MALL_BYTES) + (1 << 20))
+    sink_bytes = max(hx.read_sink_bytes(), 64 * 4 * max(a for k, a, c in parts if k == "touch"))
+    sink = S.buffer(nbytes=sink_bytes)
+
+    def reads_of(keep):
+        chosen = [(p, o) for p, o, k in zip(parts, offsets, kind_of) if k in keep]
+
+        def body():
+            for (k, a, c), o in chosen:
+                if k == "read":
+                    hx.read(buf.ptr + o, a, sink.ptr, sink_bytes, S.stream)
+                else:
+                    hx.touch(buf.ptr + o, a, c, sink.ptr, sink_bytes, S.stream)
+        return body
+
+    log("c3 breakdown (a launch of each kind in place, us):")
+    out = prefix_breakdown(S, calls, kind_of, C3_KINDS, step_ms, steps, warmup, reads_of)
+    for b in (buf, sink):
+        b.free()
+        S.buffers.remove(b)
     return out
 
 
@@ -446,9 +548,10 @@ def decode_matches_prefill(S, launches, xs, rng, tokens=4):
     return {"decode_prefill_outputs_compared": compared, "decode_prefill_bits_equal": differing == 0}
 
 
-def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=None):
+def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=None, breakdown=False):
     """plan: products (build_products) over `tokens` tokens, on prefill path `path`; with `gate`, the
-    split along K where the gate takes the step (range sums sized for the largest product)."""
+    split along K where the gate takes the step (range sums sized for the largest product). With
+    `breakdown`, a step of layers of four products and a head: each kind timed in place."""
     from charlotte_amd import synthetic
 
     mm = S.mm
@@ -478,10 +581,21 @@ def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=No
     ms = S.time_graph(body, steps, warmup)
     tflops = flops / (ms * 1e-3) / 1e12
     roof = gemm_roofline(tflops, path, name)
+    target = mm.Target(256, path, workspace_bytes=1 << 40)
+    kernels = sorted({mm.plan_launch(m, t, target, gate, sums_bytes).kernel.name for m, t in launches})
     log(f"{name}: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s ({100 * roof['frac']:.1f}% of its unit's peak, "
-        f"{roof['peak']} TFLOP/s {roof['bound']})")
-    return {"ms_per_step": ms, "ms_first_replay": S.last_first, "flops": flops, "TFLOP/s": tflops, "path": path.name, "roofline": roof,
-            "tokens_per_s": tokens / (ms * 1e-3), "launches": len(launches), "head_gemv_bytes": head_bytes}
+        f"{roof['peak']} TFLOP/s {roof['bound']}); kernels {','.join(kernels)}")
+    out = {"ms_per_step": ms, "ms_first_replay": S.last_first, "flops": flops, "TFLOP/s": tflops, "path": path.name,
+           "kernels": kernels, "roofline": roof, "tokens_per_s": tokens / (ms * 1e-3), "launches": len(launches),
+           "head_gemv_bytes": head_bytes}
+    if breakdown and head is not None:
+        layers = (len(launches) - 1) // 4
+        kind_of = [i % 4 if i < 4 * layers else 4 for i in range(len(launches))]
+        calls = [lambda m=m, t=t: mm.launch(S.ctx, m, t, gate, sums, sums_bytes, stream=S.stream.handle)
+                 for m, t in launches]
+        log(f"{name} breakdown (a launch of each kind in place, us):")
+        out["breakdown"] = prefix_breakdown(S, calls, kind_of, C3_KINDS, ms, steps, warmup)
+    return out
 
 
 def gemm_roofline(tflops, path, name):
@@ -687,7 +801,12 @@ def main():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--settle-ms", type=float, default=SETTLE_MS,
                    help="untimed replays of each config's graph, in ms of wall time, before its timed replays")
+    p.add_argument("--settle-replays", type=int, default=None,
+                   help="settle with this many untimed replays of each graph instead of --settle-ms of wall time "
+                        "(for runs under a tracer: the dispatches it records stay bounded)")
     p.add_argument("--only", default="c1,c2,c3,c4,c5,c6,c7,c8")
+    p.add_argument("--breakdown", action="store_true",
+                   help="also time each kind of c5's launches in place (prefixes of its graph)")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-table", action="store_true",
                    help="time the CPU baseline table (C1-C5, f32 and f64, 1 and all threads) and exit")
@@ -713,6 +832,7 @@ def main():
     log("device:", hx.device_name(0))
     S = Setup()
     S.settle_ms = args.settle_ms
+    S.settle_replays = args.settle_replays
     out = {}
     rng = np.random.default_rng(0xC4A7)
     c2 = None
@@ -771,18 +891,29 @@ def main():
         if "c5" in only:
             for tag, path in paths:
                 out["c5" + tag] = run_gemm(S, "c5" + tag, layer_plan(2048, 512, 2048, 8192, True) * 16, 2048,
-                                           max(args.steps // 4, 3), args.warmup, rng, path, head=(128256, 2048))
+                                           max(args.steps // 4, 3), args.warmup, rng, path, head=(128256, 2048),
+                                           breakdown=args.breakdown)
         if "c6" in only:
             # A short prefill step (32 tokens) through Llama 3.2 1B's down
-            # projection: one 64-token tile a 128-row block, 16 workgroups,
-            # unless split along K (the reference's measured gate, 2/1 up to
-            # 64 workgroups) or run on the matrix cores.
+            # projection: split along K (the reference's measured gate, 2/1 up
+            # to 64 workgroups); unsplit, as a product with options or without
+            # range sums runs, on the short-step tile AUTO takes (8 rows x 32
+            # tokens, K split among a workgroup's waves: 256 workgroups) and on
+            # the 128-row tile (16 workgroups); on the matrix cores. Then the
+            # same step's gated gate/up product, which never splits: the
+            # short-step tile and the 128-row tile.
             plan = [("write", [(2048, 8192)])]
             out["c6_split"] = run_gemm(S, "c6_split", plan, 32, args.steps, args.warmup, rng,
                                        S.mm.GemmPath.CANONICAL, gate=S.mm.kSplitGate)
-            out["c6_tiled"] = run_gemm(S, "c6_tiled", plan, 32, args.steps, args.warmup, rng, S.mm.GemmPath.CANONICAL)
+            out["c6_tiled"] = run_gemm(S, "c6_tiled", plan, 32, args.steps, args.warmup, rng, S.mm.GemmPath.AUTO)
+            out["c6_tiled128"] = run_gemm(S, "c6_tiled128", plan, 32, args.steps, args.warmup, rng,
+                                          S.mm.GemmPath.CANONICAL)
             out["c6_mfma"] = run_gemm(S, "c6_mfma", plan, 32, args.steps, args.warmup, rng,
                                       S.mm.GemmPath.SPLIT_F16_MFMA)
+            gated = [("gated", [(8192, 2048), (8192, 2048)])]
+            out["c6_gated"] = run_gemm(S, "c6_gated", gated, 32, args.steps, args.warmup, rng, S.mm.GemmPath.AUTO)
+            out["c6_gated128"] = run_gemm(S, "c6_gated128", gated, 32, args.steps, args.warmup, rng,
+                                          S.mm.GemmPath.CANONICAL)
         if "c7" in only:
             # The embedding gather of Qwen3 0.6B's tied Q6_K table: a
             # 512-token prefill step and a decode step.

@@ -260,6 +260,10 @@ Verdict plan_product(const chm::Product& a, uint32_t format, const Target& t, ch
         split = a.tokens <= most;
     }
     chm::plan_gemm_canonical(a, t.compute_units, split, plan);
+    // A step the 128-row tile leaves short of one workgroup a compute unit:
+    // the short-step tile, K split among its waves (the same bits).
+    if (!split && t.gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_AUTO && plan->tiles < t.compute_units)
+        chm::plan_gemm_short(a, t.compute_units, plan);
     return {};
 }
 
@@ -523,6 +527,7 @@ static Status run_plan(charlotte_hip_matmul_context* ctx, const chm::Product& a,
     switch (plan.kernel) {
         case chm::kGemmMfma: e = chm::launch_gemm_mfma(a, format, plan, ctx->workspace, s); break;
         case chm::kGemmTiled: e = chm::launch_gemm_canonical(a, format, plan, nullptr, s); break;
+        case chm::kGemmShort: e = chm::launch_gemm_short(a, format, plan, s); break;
         case chm::kGemmSplit: e = chm::launch_gemm_canonical(a, format, plan, range_sums, s); break;
         default: e = chm::launch_gemv(a, format, plan, ctx->compute_units, s); break;
     }

@@ -27,6 +27,7 @@ enum Kernel : uint32_t {
     kGemmTiled = 16,    // prefill, the VALU tile
     kGemmSplit = 17,    // prefill split along K, then the ordered combine
     kGemmMfma = 18,     // prefill on the matrix cores, x split into two f16 parts
+    kGemmShort = 19,    // prefill of a short step: 16 or 8 rows x 32 tokens, K split among the waves
 };
 
 struct Plan {
@@ -67,6 +68,11 @@ uint64_t gemv_wide_workgroups(uint32_t compute_units, uint64_t steps);
 void plan_gemm_canonical(const Product& a, uint32_t compute_units, bool split, Plan* plan);
 hipError_t launch_gemm_canonical(const Product& a, uint32_t format, const Plan& plan, float* range_sums,
                                  hipStream_t stream);
+
+// Prefill of a short step (gemm_short.hip): a step that does not split and
+// whose 128-row tiles would leave compute units idle.
+void plan_gemm_short(const Product& a, uint32_t compute_units, Plan* plan);
+hipError_t launch_gemm_short(const Product& a, uint32_t format, const Plan& plan, hipStream_t stream);
 
 // Prefill on the matrix cores.
 bool mfma_reads(uint32_t format);

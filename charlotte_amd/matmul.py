@@ -73,8 +73,11 @@ class Rows(enum.IntEnum):
 
 
 class GemmPath(enum.IntEnum):
-    """The prefill kernel: AUTO (the default) and CANONICAL run the bit-exact VALU
-    tile; SPLIT_F16_MFMA, only when asked for, the matrix cores within 1e-5."""
+    """The prefill kernel: AUTO (the default) and CANONICAL run bit-exact VALU
+    tiles — AUTO takes the short-step tile (GEMM_SHORT) where the 128-row tile
+    would leave compute units idle, CANONICAL always the 128-row tile, the same
+    bits either way; SPLIT_F16_MFMA, only when asked for, the matrix cores within
+    1e-5."""
 
     AUTO = 0
     CANONICAL = 1
@@ -95,6 +98,7 @@ class Kernel(enum.IntEnum):
     GEMM_TILED = 16
     GEMM_SPLIT = 17
     GEMM_MFMA = 18
+    GEMM_SHORT = 19
 
 
 class GemvPath(enum.IntEnum):
@@ -333,8 +337,11 @@ class Context:
         if status != 0:
             raise MatmulError(status, self.error())
 
+    gemm_path = GemmPath.AUTO
+
     def set_gemm_path(self, path: GemmPath):
         self.check(lib.charlotte_hip_matmul_set_gemm_path(self.handle, int(path)))
+        self.gemm_path = GemmPath(path)
 
     def set_gemv_path(self, path: GemvPath):
         self.check(lib.charlotte_hip_matmul_set_gemv_path(self.handle, int(path)))

@@ -114,10 +114,14 @@ typedef enum {
 } charlotte_hip_matmul_rows;
 
 /* Which prefill kernel runs (no counterpart: the reference has one, on WebGPU's
- * shader cores). AUTO, the default, and CANONICAL run the VALU tile in the
+ * shader cores). AUTO, the default, and CANONICAL run VALU tiles in the
  * order above (split along K where the gate and the caller's range sums
  * allow), bit-exact and batch-invariant: a drop-in caller keeps the
- * reference's decode = prefill guarantee whatever workspace it sets.
+ * reference's decode = prefill guarantee whatever workspace it sets. AUTO
+ * takes the short-step tile (GEMM_SHORT: 16 or 8 rows by 32 tokens, K split
+ * among a workgroup's waves) for a step that does not split and whose
+ * 128-row tiles would number fewer than the device's compute units;
+ * CANONICAL always takes the 128-row tile. Both give the same bits.
  * SPLIT_F16_MFMA, only when asked for, runs the products on the matrix cores
  * with x split into two f16 parts, within the tolerance max|err| / max|y| <=
  * 1e-5 but not bit-exact and not batch-invariant with decode; it needs a
@@ -301,7 +305,8 @@ typedef enum {
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMV_WIDE = 7,     /* decode, Q4_0 at K = 9,216 .. 16,384 (whole 1,024s) streamed through LDS */
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_TILED = 16,   /* prefill, the VALU tile */
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_SPLIT = 17,   /* prefill split along K, then the ordered combine */
-    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_MFMA = 18     /* prefill on the matrix cores (x split into two f16 parts) */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_MFMA = 18,    /* prefill on the matrix cores (x split into two f16 parts) */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_SHORT = 19    /* prefill of a short step: 16 or 8 rows x 32 tokens, K split in the workgroup */
 } charlotte_hip_matmul_kernel;
 
 /* What a plan is made for: the device's compute units (256 on MI355X) and
@@ -349,10 +354,11 @@ charlotte_hip_matmul_status charlotte_hip_matmul_plan_launch(const charlotte_hip
  * the split's range sums taken from the library's own static array, one a
  * device of CHARLOTTE_HIP_MATMUL_STATIC_SCRATCH_BYTES, held from the
  * library's load on the device until the process ends, in place of the
- * caller's buffer. It allocates nothing and frees nothing. A step the gate
- * splits whose range sums (4 x 32 x tokens x rows bytes) pass the array is
- * refused with INVALID_ARGUMENT; every other step runs as the ordinary
- * launch runs it, with the same bits. Every call on one GPU shares that
+ * caller's buffer. It allocates nothing and frees nothing. It plans as the
+ * ordinary launch plans with a range-sums buffer of the array's size: a step
+ * the gate would split whose range sums (4 x 32 x tokens x rows bytes) pass
+ * the array runs the tiled form, whose bits are the split's; every step runs
+ * with the ordinary launch's bits. Every call on one GPU shares that
  * GPU's array and leaves its contents behind (nothing in it must start at
  * zero): calls that overlap on one GPU — on two streams, or from two
  * threads — race. */

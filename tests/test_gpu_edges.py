@@ -23,13 +23,15 @@ D_OFFSET = {Q4_0: 0, Q6_K: 208}  # where a block's fp16 d lies
 WEIGHTS_A_BLOCK = {Q4_0: 32, Q6_K: 256}
 
 
-@pytest.fixture(scope="module")
-def run():
+@pytest.fixture(scope="module", params=["AUTO", "CANONICAL"])
+def run(request):
+    """The prefill under AUTO (the short-step tile for these small steps) and
+    CANONICAL (the 128-row tile)."""
     from charlotte_amd import matmul as mm
     from tests.support.gpu import Runner
 
     c = mm.Context(0)
-    c.set_gemm_path(mm.GemmPath.CANONICAL)
+    c.set_gemm_path(mm.GemmPath[request.param])
     yield Runner(c)
     c.close()
 

@@ -32,11 +32,14 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 SILU, GELU, SIGMOID = 0, 1, 2
 
 
-@pytest.fixture(scope="module")
-def ctx():
+@pytest.fixture(scope="module", params=["AUTO", "CANONICAL"])
+def ctx(request):
+    """Each test twice: under AUTO (the short-step tile where the 128-row tile
+    would leave compute units idle) and CANONICAL (always the 128-row tile)."""
     from charlotte_amd import matmul as mm
 
     c = mm.Context(0)
+    c.set_gemm_path(mm.GemmPath[request.param])
     yield c
     c.close()
 
@@ -239,17 +242,18 @@ def test_the_matrix_cores_take_the_fixture_within_tolerance(oracle, run, source,
     ws = hx.Buffer(mm.workspace_bytes(64, t.columns))
     run.ctx.set_workspace(ws.ptr, mm.workspace_bytes(64, t.columns))
     try:
+        path = run.ctx.gemm_path
         run.ctx.set_gemm_path(mm.GemmPath.SPLIT_F16_MFMA)
         for tokens in (16, 33, 64):
             got = run.write(w, x, tokens)
             err = np.abs(got.astype(np.float64) - y64[:tokens]).max()
             assert err <= 1e-5 * np.abs(y64[:tokens]).max(), f"{name} tokens={tokens}: {err}"
             assert (np.argmax(got, 1) == np.argmax(exact[:tokens], 1)).all()
-        run.ctx.set_gemm_path(mm.GemmPath.AUTO)
+        run.ctx.set_gemm_path(path)
         for tokens in (9, 16, 64):
-            _check(run.write(w, x, tokens), exact[:tokens], f"{name} AUTO {tokens} tokens")
+            _check(run.write(w, x, tokens), exact[:tokens], f"{name} {path.name} {tokens} tokens")
     finally:
-        run.ctx.set_gemm_path(mm.GemmPath.AUTO)
+        run.ctx.set_gemm_path(path)
         run.ctx.set_workspace(0, 0)
         ws.free()
         w.free()

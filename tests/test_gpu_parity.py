@@ -27,11 +27,14 @@ WIDEST = 3072
 THREADS = max(1, min(16, os.cpu_count() or 1))
 
 
-@pytest.fixture(scope="module")
-def ctx():
+@pytest.fixture(scope="module", params=["AUTO", "CANONICAL"])
+def ctx(request):
+    """Each test twice: under AUTO (the short-step tile where the 128-row tile
+    would leave compute units idle) and CANONICAL (always the 128-row tile)."""
     from charlotte_amd import matmul as mm
 
     c = mm.Context(0)
+    c.set_gemm_path(mm.GemmPath[request.param])
     yield c
     c.close()
 
