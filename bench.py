@@ -271,8 +271,65 @@ def run_read_floor(S, name, nbytes, copies, steps, warmup):
     for b in bufs + [sink]:
         b.free()
         S.buffers.remove(b)
-    return {"kernel": "harness read_kernel: global_load_lds_dwordx4, 9 KB a wave a step, no decode",
+    return {"kernel": "harness read_kernel: global_load_lds_dwordx4 nt, 9 KB a wave a step, no decode",
             "bytes": nbytes, "ms_per_step": ms, "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def read_sweep(steps, warmup, settle_ms):
+    """The ceiling of a pure read of C2's bytes on this part: every form of
+    chx_read_sweep (registers grid-strided or a chunk a workgroup, 4-16 loads
+    in flight a lane, plain or non-temporal, 8-32 waves a CU; the LDS copy at
+    4, 9 and 16 KB a wave step, one or two steps in flight, plain or
+    non-temporal) over the same
+    three rotated copies as c2, each timed as c2 is (graph replays, median of
+    5). One JSON object: each form's us and TB/s, fastest first."""
+    from charlotte_amd import synthetic
+
+    S = Setup()
+    S.settle_ms = settle_ms
+    hx = S.hx
+    cus = int(hx.device_name(0).split("cus=")[1].split("|")[0])
+    nbytes = synthetic.stored_bytes(14, 262144, 1152) // 1024 * 1024
+    bufs = [S.buffer(nbytes=nbytes) for _ in range(3)]
+    for b in bufs:
+        b.fill(0x5A)
+    forms = []
+    for per_cu in (2, 4, 8):
+        for u in (4, 8, 16):
+            for nt in (False, True):
+                forms.append((f"regs strided u{u}{' nt' if nt else ''} {per_cu * 4} waves/CU", 0, u, nt, 1,
+                              cus * per_cu, 256))
+    for per_cu, threads in ((4, 256), (8, 256), (2, 1024)):
+        for nt in (False, True):
+            forms.append((f"regs chunk u8{' nt' if nt else ''} {per_cu * threads // 64} waves/CU "
+                          f"({per_cu} x {threads} lanes)", 1, 8, nt, 1, cus * per_cu, threads))
+    for kb in (4, 9, 16):
+        for depth in (1, 2):
+            for nt in (False, True):
+                per_cu = 1 if kb * depth > 16 else 2
+                forms.append((f"lds {kb} KB x{depth}{' nt' if nt else ''} {per_cu * 4} waves/CU", 2, kb, nt, depth,
+                              cus * per_cu, 256))
+    sink_bytes = max(f[5] * f[6] for f in forms) * 4
+    sink = S.buffer(nbytes=sink_bytes)
+    rows = []
+    try:
+        for name, form, u, nt, depth, blocks, threads in forms:
+            state = {"i": 0}
+
+            def body():
+                b = bufs[state["i"] % len(bufs)]
+                state["i"] += 1
+                hx.read_sweep(form, u, nt, depth, blocks, threads, b.ptr, nbytes, sink.ptr, sink_bytes, S.stream)
+
+            ms = S.time_graph(body, steps, warmup)
+            tbs = nbytes / (ms * 1e-3) / 1e12
+            rows.append({"form": name, "us": round(ms * 1e3, 2), "TB/s": round(tbs, 3),
+                         "frac": round(tbs * 1e3 / HBM_PEAK_GBS, 4)})
+            log(f"read {name}: {ms * 1e3:.2f} us, {tbs:.3f} TB/s")
+    finally:
+        S.close()
+    rows.sort(key=lambda r: r["us"])
+    return {"bytes": nbytes, "copies": 3, "steps": steps, "forms": rows}
 
 
 def build_products(S, rng, plan, tokens, gtype=2):
@@ -814,9 +871,14 @@ def main():
                    help="time decode products of the given shapes and exit: a comma list of ROWSxCOLUMNS[:TYPE], "
                         "TYPE a GGUF type number (2 Q4_0, default; 3 Q4_1; 8 Q8_0; 14 Q6_K, repacked)")
     p.add_argument("--limbs", action="store_true", help="with --decode: the INT8_LIMBS decode path")
+    p.add_argument("--read-sweep", action="store_true",
+                   help="time every pure-read form over C2's bytes (the read ceiling) and exit")
     args = p.parse_args()
     if args.cpu_table:
         print(json.dumps(cpu_table(min(os.cpu_count() or 1, 16))), flush=True)
+        return
+    if args.read_sweep:
+        print(json.dumps(read_sweep(max(args.steps, 20), args.warmup, args.settle_ms)), flush=True)
         return
     if args.decode:
         print(json.dumps(time_decode_shapes(args.decode, args.steps, args.warmup, args.settle_ms, args.limbs)),

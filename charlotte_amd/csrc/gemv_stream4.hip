@@ -95,7 +95,8 @@ __global__ __launch_bounds__(64 * W) void gemv_stream4(Product a, uint32_t steps
         const uint8_t* from = w.piece + 16 * g0;
 #pragma unroll
         for (uint32_t i = 0; i < kCodeChunks / 64; ++i)
-            __builtin_amdgcn_global_load_lds(from + 16 * (64 * i + swizzled), (lds_void)(codes_s + 64 * i), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(from + 16 * (64 * i + swizzled), (lds_void)(codes_s + 64 * i), 16, 0,
+                                             kStreamPolicy);
         copy_stream<kScaleChunks>(w.piece + 16 * w.blocks + 2 * g0, scales_s, lane);
     };
     // The stage's reads are instructions the compiler does not look into (it

@@ -51,7 +51,7 @@ struct WideRun {
 // (A function of its own: written inline in the kernel template's lambda,
 // the builtin loses the kernel's host launch stub in this compiler.)
 __device__ __forceinline__ void copy16(const uint8_t* from, u32x4s_t* to) {
-    __builtin_amdgcn_global_load_lds(from, (lds_void)to, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(from, (lds_void)to, 16, 0, kStreamPolicy);
 }
 
 }  // namespace

@@ -8,12 +8,17 @@
 //   chx_copy — a plain copy of known size, the yardstick rocprofv3's
 //     FETCH_SIZE / WRITE_SIZE counters are scaled by;
 //   chx_read — a streaming read of known size and nothing else, copied a
-//     9 KB step a wave at a time into LDS by global_load_lds_dwordx4 as the
-//     LDS-streamed decodes copy their weights: the rate a decode of the same
-//     bytes could reach were its arithmetic free;
+//     9 KB step a wave at a time into LDS by global_load_lds_dwordx4,
+//     non-temporal, as the LDS-streamed decodes copy their weights: the rate
+//     a decode of the same bytes could reach were its arithmetic free;
 //   chx_touch — one-wave workgroups that each read a few KB and write a
 //     word: a small decode's dispatch and memory round trip with its
-//     arithmetic, reduction and epilogue taken away.
+//     arithmetic, reduction and epilogue taken away;
+//   chx_read_sweep — the same read in other forms, for the ceiling of a
+//     pure read on this part: 16-byte loads into registers (grid-strided or
+//     a contiguous chunk a workgroup, U loads in flight a lane, plain or
+//     non-temporal) and the LDS copy at 4, 9 or 16 KB a wave step with one
+//     or two steps in flight.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -63,7 +68,7 @@ __global__ __launch_bounds__(64 * kReadWaves) void read_kernel(const uint8_t* sr
             const uint64_t c = s * kReadChunks + i;
             if (c < chunks)
                 __builtin_amdgcn_global_load_lds(src + 1024 * c + 16 * lane, (lds_void_t)(stage[wave] + 64 * i), 16, 0,
-                                                 0);
+                                                 2);
         }
         __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));  // vmcnt(0)
     }
@@ -87,6 +92,70 @@ __global__ __launch_bounds__(64) void touch_kernel(const u32x4_t* src, uint32_t 
             if (i + j < kib) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
     }
     sink[static_cast<uint64_t>(blockIdx.x) * 64 + threadIdx.x] = acc;
+}
+
+// vmcnt(n) for s_waitcnt (expcnt and lgkmcnt left at their maxima).
+constexpr int vmcnt(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
+
+// A lane's sink word is written only when its fold of every loaded word
+// meets a value no data here makes, so the loads cannot be dropped and
+// nothing is stored.
+constexpr uint32_t kNever = 0x9E3779B9u;
+
+// 16-byte loads into registers, U a lane in flight: grid-strided over the
+// buffer (CHUNK false) or over one contiguous chunk a workgroup.
+template <int U, bool NT, bool CHUNK>
+__global__ __launch_bounds__(1024) void sweep_regs(const u32x4_t* src, uint64_t n16, uint32_t* sink) {
+    uint64_t i, stride, end;
+    if constexpr (CHUNK) {
+        const uint64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+        i = blockIdx.x * per + threadIdx.x;
+        end = min(n16, (blockIdx.x + 1) * per);
+        stride = blockDim.x;
+    } else {
+        i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+        end = n16;
+        stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    }
+    uint32_t acc = 0;
+    for (; i + (U - 1) * stride < end; i += U * stride) {
+        u32x4_t v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = NT ? __builtin_nontemporal_load(src + i + u * stride) : src[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < end; i += stride) {
+        const u32x4_t v = src[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == kNever) sink[static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = acc;
+}
+
+// The LDS copy: each of a workgroup's four waves copies steps of CH 1 KB
+// chunks (grid-strided) into its own stage, DEPTH steps in flight; POLICY
+// the copies' cache policy bits (0, or 2: non-temporal).
+template <int CH, int DEPTH, int POLICY>
+__global__ __launch_bounds__(256) void sweep_lds(const uint8_t* src, uint64_t chunks, uint32_t* sink) {
+    __shared__ u32x4_t stage[4][DEPTH][CH * 64];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
+    const uint64_t steps = (chunks + CH - 1) / CH;
+    uint32_t k = 0;
+    for (uint64_t s = static_cast<uint64_t>(blockIdx.x) * 4 + wave; s < steps;
+         s += static_cast<uint64_t>(gridDim.x) * 4, ++k) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const uint64_t c = s * CH + i;
+            if (c < chunks)
+                __builtin_amdgcn_global_load_lds(src + 1024 * c + 16 * lane,
+                                                 (lds_void_t)(stage[wave][k % DEPTH] + 64 * i), 16, 0, POLICY);
+        }
+        __builtin_amdgcn_s_waitcnt(vmcnt(CH * (DEPTH - 1)));
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt(0));
+    __syncthreads();
+    const uint32_t v = stage[wave][0][lane].x;
+    if (v == kNever) sink[static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = v;
 }
 
 }  // namespace
@@ -222,6 +291,72 @@ int chx_read(const void* src, uint64_t bytes, void* sink, uint64_t sink_bytes, v
     const uint32_t blocks = static_cast<uint32_t>(need / (64 * kReadWaves * 4));
     hipLaunchKernelGGL(read_kernel, dim3(blocks), dim3(64 * kReadWaves), 0, static_cast<hipStream_t>(s),
                        static_cast<const uint8_t*>(src), bytes / 1024, static_cast<uint32_t*>(sink));
+    return hipGetLastError();
+}
+
+// One form of the read sweep over `bytes` (whole KB, 16-byte aligned) at
+// `src`: form 0 registers grid-strided, 1 registers a chunk a workgroup
+// (u loads in flight a lane: 4, 8 or 16; nt: non-temporal loads), both with
+// `blocks` workgroups of `threads` lanes (64..1024, whole waves); form 2 the
+// LDS copy (u KB a step: 4, 9 or 16; depth steps in flight: 1 or 2; nt:
+// non-temporal copies), `blocks` four-wave workgroups. `sink` must hold a
+// word a lane of the grid.
+int chx_read_sweep(int form, int u, int nt, int depth, uint32_t blocks, uint32_t threads, const void* src,
+                   uint64_t bytes, void* sink, uint64_t sink_bytes, void* s) {
+    const auto stream = static_cast<hipStream_t>(s);
+    if (form == 2) threads = 256;
+    if (blocks == 0 || threads == 0 || threads > 1024 || threads % 64 != 0 || bytes % 1024 != 0 ||
+        reinterpret_cast<uintptr_t>(src) % 16 != 0 || sink_bytes < static_cast<uint64_t>(blocks) * threads * 4)
+        return hipErrorInvalidValue;
+    const auto* v = static_cast<const u32x4_t*>(src);
+    auto* out = static_cast<uint32_t*>(sink);
+    const uint64_t n16 = bytes / 16;
+#define CHX_REGS(U, NT, CHUNK) \
+    hipLaunchKernelGGL((sweep_regs<U, NT, CHUNK>), dim3(blocks), dim3(threads), 0, stream, v, n16, out)
+    if (form == 0 || form == 1) {
+        const bool chunk = form == 1;
+        const int key = u * 4 + (nt ? 2 : 0) + (chunk ? 1 : 0);
+        switch (key) {
+            case 16: CHX_REGS(4, false, false); break;
+            case 17: CHX_REGS(4, false, true); break;
+            case 18: CHX_REGS(4, true, false); break;
+            case 19: CHX_REGS(4, true, true); break;
+            case 32: CHX_REGS(8, false, false); break;
+            case 33: CHX_REGS(8, false, true); break;
+            case 34: CHX_REGS(8, true, false); break;
+            case 35: CHX_REGS(8, true, true); break;
+            case 64: CHX_REGS(16, false, false); break;
+            case 65: CHX_REGS(16, false, true); break;
+            case 66: CHX_REGS(16, true, false); break;
+            case 67: CHX_REGS(16, true, true); break;
+            default: return hipErrorInvalidValue;
+        }
+    } else if (form == 2) {
+        const auto* b = static_cast<const uint8_t*>(src);
+        const uint64_t chunks = bytes / 1024;
+        const int key = u * 4 + depth + (nt ? 1000 : 0);
+#define CHX_LDS(CH, D, P) \
+    hipLaunchKernelGGL((sweep_lds<CH, D, P>), dim3(blocks), dim3(256), 0, stream, b, chunks, out)
+        switch (key) {
+            case 17: CHX_LDS(4, 1, 0); break;
+            case 18: CHX_LDS(4, 2, 0); break;
+            case 37: CHX_LDS(9, 1, 0); break;
+            case 38: CHX_LDS(9, 2, 0); break;
+            case 65: CHX_LDS(16, 1, 0); break;
+            case 66: CHX_LDS(16, 2, 0); break;
+            case 1017: CHX_LDS(4, 1, 2); break;
+            case 1018: CHX_LDS(4, 2, 2); break;
+            case 1037: CHX_LDS(9, 1, 2); break;
+            case 1038: CHX_LDS(9, 2, 2); break;
+            case 1065: CHX_LDS(16, 1, 2); break;
+            case 1066: CHX_LDS(16, 2, 2); break;
+            default: return hipErrorInvalidValue;
+        }
+#undef CHX_LDS
+    } else {
+        return hipErrorInvalidValue;
+    }
+#undef CHX_REGS
     return hipGetLastError();
 }
 

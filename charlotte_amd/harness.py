@@ -44,6 +44,8 @@ _SIGS = {
     "chx_read_sink_bytes": (_c.c_int, [_c.POINTER(_c.c_uint64)]),
     "chx_read": (_c.c_int, [_c.c_void_p, _c.c_uint64, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
     "chx_touch": (_c.c_int, [_c.c_void_p, _c.c_uint32, _c.c_uint32, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
+    "chx_read_sweep": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_uint32, _c.c_uint32, _c.c_void_p,
+                                  _c.c_uint64, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
 }
 
 
@@ -203,6 +205,13 @@ def read(src_ptr, nbytes, sink_ptr, sink_bytes, stream=None):
     pattern of the LDS-streamed decodes with their arithmetic taken away."""
     check(lib.chx_read(src_ptr, nbytes, sink_ptr, sink_bytes, stream.handle if isinstance(stream, Stream) else stream),
           "read")
+
+
+def read_sweep(form, u, nt, depth, blocks, threads, src_ptr, nbytes, sink_ptr, sink_bytes, stream=None):
+    """One form of the pure-read sweep (chx_read_sweep): 0 registers grid-strided, 1 registers a chunk a
+    workgroup (u loads in flight a lane, nt non-temporal), 2 the LDS copy (u KB a wave step, depth steps)."""
+    check(lib.chx_read_sweep(form, u, int(nt), depth, blocks, threads, src_ptr, nbytes, sink_ptr, sink_bytes,
+                             stream.handle if isinstance(stream, Stream) else stream), "read sweep")
 
 
 def touch(src_ptr, waves, kib, sink_ptr, sink_bytes, stream=None):
