@@ -332,6 +332,46 @@ def read_sweep(steps, warmup, settle_ms):
     return {"bytes": nbytes, "copies": 3, "steps": steps, "forms": rows}
 
 
+MFMA_SHAPES = ((0, "f16 16x16x32", 2 * 16 * 16 * 32), (1, "f16 32x32x16", 2 * 32 * 32 * 16),
+               (2, "bf16 16x16x32", 2 * 16 * 16 * 32), (3, "i8 16x16x64", 2 * 16 * 16 * 64),
+               (4, "i8 32x32x32", 2 * 32 * 32 * 32))
+
+
+def mfma_rate(iters=2000):
+    """Each matrix-core shape the prefill could use, issued back to back by
+    every wave of the GPU (chx_mfma_rate), 1 or 8 independent accumulators a
+    wave, 1, 2 or 4 waves a SIMD: the sustained rate against the part's dense
+    peak, and the time a SIMD spends on one instruction (ns; x the clock for
+    cycles). Single launches between HIP events, median of 5."""
+    S = Setup()
+    hx = S.hx
+    cus = int(hx.device_name(0).split("cus=")[1].split("|")[0])
+    sink = S.buffer(nbytes=cus * 4 * 256 * 4)
+    rows = []
+    try:
+        for shape, name, ops in MFMA_SHAPES:
+            for chains in (1, 8):
+                for per_simd in (1, 2, 4):
+                    blocks = cus * per_simd
+
+                    def body():
+                        hx.mfma_rate(shape, chains, blocks, iters, sink.ptr, sink.nbytes, S.stream)
+
+                    ms = S.time_single(body, reps=5)
+                    count = blocks * 4 * iters * chains
+                    rate = count * ops / (ms * 1e-3) / 1e12
+                    ns = ms * 1e6 / (count / (cus * 4))
+                    peak = F16_PEAK_TFLOPS * (2 if shape >= 3 else 1)
+                    rows.append({"shape": name, "chains": chains, "waves_a_simd": per_simd,
+                                 "TOP/s": round(rate, 1), "frac_of_dense_peak": round(rate / peak, 3),
+                                 "ns_an_instruction_a_simd": round(ns, 2)})
+                    log(f"mfma {name} chains {chains} waves/SIMD {per_simd}: {rate:.0f} TOP/s "
+                        f"({100 * rate / peak:.0f}% of {peak:.0f}), {ns:.2f} ns an instruction a SIMD")
+    finally:
+        S.close()
+    return {"iters": iters, "rows": rows}
+
+
 def build_products(S, rng, plan, tokens, gtype=2):
     """Weights, inputs and outputs for a list of products. plan: (kind, [(rows, columns), ...]) with kind
     "write" (one member), "qkv" (three members, three outputs) or "gated" (gate, up; one output of their rows).
@@ -871,11 +911,16 @@ def main():
                    help="time decode products of the given shapes and exit: a comma list of ROWSxCOLUMNS[:TYPE], "
                         "TYPE a GGUF type number (2 Q4_0, default; 3 Q4_1; 8 Q8_0; 14 Q6_K, repacked)")
     p.add_argument("--limbs", action="store_true", help="with --decode: the INT8_LIMBS decode path")
+    p.add_argument("--mfma-rate", action="store_true",
+                   help="time each matrix-core instruction shape's sustained rate (a probe) and exit")
     p.add_argument("--read-sweep", action="store_true",
                    help="time every pure-read form over C2's bytes (the read ceiling) and exit")
     args = p.parse_args()
     if args.cpu_table:
         print(json.dumps(cpu_table(min(os.cpu_count() or 1, 16))), flush=True)
+        return
+    if args.mfma_rate:
+        print(json.dumps(mfma_rate()), flush=True)
         return
     if args.read_sweep:
         print(json.dumps(read_sweep(max(args.steps, 20), args.warmup, args.settle_ms)), flush=True)

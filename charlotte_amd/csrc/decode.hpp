@@ -31,6 +31,14 @@ __device__ __forceinline__ half2_t lift(uint32_t codes, uint32_t selector) {
     return __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(kHalf1024, codes, selector));
 }
 
+// Two code bytes as binary16 codes less their bias: (1024 + q) - (1024 +
+// bias) = q - bias, exact (the matrix-core prefill's operands).
+__device__ __forceinline__ half2_t lift_less(uint32_t codes, uint32_t selector, _Float16 bias) {
+    const half2_t v = lift(codes, selector);
+    const half2_t b = {bias, bias};
+    return v - b;
+}
+
 // Four weights from four code bytes, continuing the chain over x[0..3].
 __device__ __forceinline__ float chain4(uint32_t codes, float scale, float offset, const float* x, float s) {
     const half2_t a = lift(codes, kLowPair), b = lift(codes, kHighPair);

@@ -235,12 +235,6 @@ struct Batch<kQ4_0, R> {
     }
 };
 
-__device__ __forceinline__ half2_t lift_less(uint32_t codes, uint32_t selector, _Float16 bias) {
-    half2_t v = lift(codes, selector);
-    const half2_t b = {bias, bias};
-    return v - b;  // (1024 + q) - (1024 + bias) = q - bias, exact in binary16
-}
-
 // One group's products for a wave: the codes of its R row blocks (decoded
 // here to binary16) against the T token blocks' split input, each block's
 // P = codes . hi + codes . lo scaled into its totals.

@@ -14,6 +14,9 @@
 //   chx_touch — one-wave workgroups that each read a few KB and write a
 //     word: a small decode's dispatch and memory round trip with its
 //     arithmetic, reduction and epilogue taken away;
+//   chx_mfma_rate — a matrix-core instruction shape issued back to back by
+//     every wave, C independent accumulators a wave: the shape's sustained
+//     rate, and with one accumulator its dependent-chain rate;
 //   chx_read_sweep — the same read in other forms, for the ceiling of a
 //     pure read on this part: 16-byte loads into registers (grid-strided or
 //     a contiguous chunk a workgroup, U loads in flight a lane, plain or
@@ -24,6 +27,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <type_traits>
 
 #include "formats.hpp"
 
@@ -156,6 +160,52 @@ __global__ __launch_bounds__(256) void sweep_lds(const uint8_t* src, uint64_t ch
     __syncthreads();
     const uint32_t v = stage[wave][0][lane].x;
     if (v == kNever) sink[static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = v;
+}
+
+typedef _Float16 mh8 __attribute__((ext_vector_type(8)));
+typedef __bf16 mb8 __attribute__((ext_vector_type(8)));
+typedef float mf4 __attribute__((ext_vector_type(4)));
+typedef float mf16 __attribute__((ext_vector_type(16)));
+typedef int mi4 __attribute__((ext_vector_type(4)));
+typedef int mi16 __attribute__((ext_vector_type(16)));
+
+// Shape S (0 f16 16x16x32, 1 f16 32x32x16, 2 bf16 16x16x32, 3 i8 16x16x64,
+// 4 i8 32x32x32), C chains, `iters` rounds of C instructions a wave.
+template <int S, int C>
+__global__ __launch_bounds__(256) void mfma_rate_kernel(uint32_t iters, uint32_t* sink) {
+    const float f = static_cast<float>(threadIdx.x & 7u) * 0.125f;
+    const mh8 h = {(_Float16)f, (_Float16)0.5f, (_Float16)f, (_Float16)1.0f,
+                   (_Float16)f, (_Float16)0.25f, (_Float16)f, (_Float16)2.0f};
+    const mb8 bb = {(__bf16)f, (__bf16)0.5f, (__bf16)f, (__bf16)1.0f, (__bf16)f, (__bf16)0.25f, (__bf16)f, (__bf16)2.0f};
+    const mi4 iv = {static_cast<int>(threadIdx.x), 0x01020304, 0x7F00FF01, 3};
+    uint32_t fold = 0;
+    if constexpr (S == 0 || S == 2 || S == 3) {
+        using Acc = std::conditional_t<S == 3, mi4, mf4>;
+        Acc acc[C] = {};
+        for (uint32_t i = 0; i < iters; ++i) {
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                if constexpr (S == 0) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, h, acc[c], 0, 0, 0);
+                else if constexpr (S == 2) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bb, bb, acc[c], 0, 0, 0);
+                else acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(iv, iv, acc[c], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < C; ++c) fold ^= __builtin_bit_cast(uint32_t, acc[c][0]);
+    } else {
+        using Acc = std::conditional_t<S == 4, mi16, mf16>;
+        Acc acc[C] = {};
+        for (uint32_t i = 0; i < iters; ++i) {
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                if constexpr (S == 1) acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h, h, acc[c], 0, 0, 0);
+                else acc[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(iv, iv, acc[c], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < C; ++c) fold ^= __builtin_bit_cast(uint32_t, acc[c][0]);
+    }
+    if (fold == kNever) sink[static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = fold;
 }
 
 }  // namespace
@@ -357,6 +407,36 @@ int chx_read_sweep(int form, int u, int nt, int depth, uint32_t blocks, uint32_t
         return hipErrorInvalidValue;
     }
 #undef CHX_REGS
+    return hipGetLastError();
+}
+
+// The matrix-core rate probe: `blocks` four-wave workgroups each issuing
+// `iters` rounds of `chains` independent instructions of `shape` (see
+// mfma_rate_kernel) a wave. The operations a launch does: blocks x 4 x
+// iters x chains x the shape's 2 M N K. `sink` holds a word a lane.
+int chx_mfma_rate(int shape, int chains, uint32_t blocks, uint32_t iters, void* sink, uint64_t sink_bytes, void* s) {
+    if (blocks == 0 || sink_bytes < static_cast<uint64_t>(blocks) * 256 * 4) return hipErrorInvalidValue;
+    const auto stream = static_cast<hipStream_t>(s);
+    auto* out = static_cast<uint32_t*>(sink);
+#define CHX_MFMA(S, C) hipLaunchKernelGGL((mfma_rate_kernel<S, C>), dim3(blocks), dim3(256), 0, stream, iters, out)
+#define CHX_SHAPE(S)                  \
+    switch (chains) {                 \
+        case 1: CHX_MFMA(S, 1); break; \
+        case 2: CHX_MFMA(S, 2); break; \
+        case 4: CHX_MFMA(S, 4); break; \
+        case 8: CHX_MFMA(S, 8); break; \
+        default: return hipErrorInvalidValue; \
+    }
+    switch (shape) {
+        case 0: CHX_SHAPE(0); break;
+        case 1: CHX_SHAPE(1); break;
+        case 2: CHX_SHAPE(2); break;
+        case 3: CHX_SHAPE(3); break;
+        case 4: CHX_SHAPE(4); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef CHX_SHAPE
+#undef CHX_MFMA
     return hipGetLastError();
 }
 

@@ -44,6 +44,7 @@ _SIGS = {
     "chx_read_sink_bytes": (_c.c_int, [_c.POINTER(_c.c_uint64)]),
     "chx_read": (_c.c_int, [_c.c_void_p, _c.c_uint64, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
     "chx_touch": (_c.c_int, [_c.c_void_p, _c.c_uint32, _c.c_uint32, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
+    "chx_mfma_rate": (_c.c_int, [_c.c_int, _c.c_int, _c.c_uint32, _c.c_uint32, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
     "chx_read_sweep": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_uint32, _c.c_uint32, _c.c_void_p,
                                   _c.c_uint64, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
 }
@@ -212,6 +213,13 @@ def read_sweep(form, u, nt, depth, blocks, threads, src_ptr, nbytes, sink_ptr, s
     workgroup (u loads in flight a lane, nt non-temporal), 2 the LDS copy (u KB a wave step, depth steps)."""
     check(lib.chx_read_sweep(form, u, int(nt), depth, blocks, threads, src_ptr, nbytes, sink_ptr, sink_bytes,
                              stream.handle if isinstance(stream, Stream) else stream), "read sweep")
+
+
+def mfma_rate(shape, chains, blocks, iters, sink_ptr, sink_bytes, stream=None):
+    """The matrix-core rate probe (chx_mfma_rate): shape 0 f16 16x16x32, 1 f16 32x32x16, 2 bf16 16x16x32,
+    3 i8 16x16x64, 4 i8 32x32x32; `chains` independent accumulators a wave."""
+    check(lib.chx_mfma_rate(shape, chains, blocks, iters, sink_ptr, sink_bytes,
+                            stream.handle if isinstance(stream, Stream) else stream), "mfma rate")
 
 
 def touch(src_ptr, waves, kib, sink_ptr, sink_bytes, stream=None):
