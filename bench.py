@@ -545,6 +545,48 @@ def c3_breakdown(S, launches, step_ms, steps, warmup):
     for b in (buf, sink):
         b.free()
         S.buffers.remove(b)
+    out["head_placement"] = c3_head_placement(S, launches, steps, warmup)
+    return out
+
+
+def c3_head_placement(S, launches, steps, warmup):
+    """What the head adds where it stands, each a graph of settled replays timed
+    one after another: the layers; the step (the layers, then the head); the
+    step with a second head after the first (its own copy of the weights, so
+    none of the first head's bytes come from a cache); the layers, 20 empty
+    launches, then the head; and the head and the 20 empty launches alone.
+    A prefix difference holds a launch's own time only if the launches around
+    it run as they do alone."""
+    from charlotte_amd import synthetic
+
+    mm, hx = S.mm, S.hx
+    head = launches[-1]
+    w = head.members[0].weight
+    twin_w = mm.Weight(S.ctx, int(w.type), w.rows, w.columns,
+                       synthetic.q6_k(np.random.default_rng(0x4EAD), w.rows, w.columns))
+    S.weights.append(twin_w)
+    twin = mm.MatmulLaunch([mm.Member(twin_w)], head.input, list(head.outputs))
+
+    def run(ms):
+        for m in ms:
+            mm.launch(S.ctx, m, 1, stream=S.stream.handle)
+
+    def empties():
+        for _ in range(20):
+            hx.null(S.stream)
+
+    layers = launches[:-1]
+    cases = (("layers", lambda: run(layers)),
+             ("step", lambda: run(launches)),
+             ("step, head twice", lambda: run(launches + [twin])),
+             ("layers, 20 empty, head", lambda: (run(layers), empties(), run([head]))),
+             ("head alone", lambda: run([head])),
+             ("20 empty alone", empties))
+    out = {}
+    for name, body in cases:
+        ms = S.time_graph(body, steps, warmup)
+        out[name] = round(ms * 1e3, 1)
+    log("c3 head in place (us a step): " + ", ".join(f"{k} {v:.1f}" for k, v in out.items()))
     return out
 
 
@@ -732,10 +774,11 @@ def gemm_traffic(name, path):
 
 
 def gemv_traffic(name):
-    """HBM bytes a launch of a c8 decode from the counter runs in
-    profiles/traffic_c8.json (FETCH_SIZE and WRITE_SIZE, KiB a dispatch,
-    scaled as traffic_c2.json's); None for other configs or when absent."""
-    file = os.path.join(ROOT, "profiles", "traffic_c8.json")
+    """HBM bytes a launch of a c1 or c8 decode from the counter runs in
+    profiles/traffic_c1.json and traffic_c8.json (FETCH_SIZE and WRITE_SIZE,
+    KiB a dispatch, scaled as traffic_c2.json's); None for other configs or
+    when absent."""
+    file = os.path.join(ROOT, "profiles", "traffic_c1.json" if name == "c1" else "traffic_c8.json")
     if not os.path.exists(file):
         return None
     t = json.load(open(file))
