@@ -698,8 +698,8 @@ bool plan_gemv(const Product& a, uint32_t format, uint32_t compute_units, bool l
         plan->kernel = kGemvStream4;
         // the limbs form at K = 1,024 and 2,048 only: at 4,096 and 8,192 it
         // measured slower than the canonical decode (21.4 against 20.4 us,
-        // 37.9 against 33.7); at 1,024 and 2,048 it runs within noise of the
-        // canonical decode (Q4_0 head 20.3 against 20.2 us)
+        // 37.9 against 33.7, plain copies); at 1,024 it is ~10% faster with
+        // non-temporal copies (Q4_0 head 19.6 against 21.7 us)
         plan->limbs = limbs && G <= 64;
         plan->canonical = !plan->limbs;
         plan->lanes = G / 8;

@@ -25,10 +25,11 @@
 //
 // The LIMBS form (the GEMV path INT8_LIMBS at K = 1,024 and 2,048,
 // limbs.hpp) stages x as int8 limb records in the places of its float4 and
-// decodes a group with 24 v_dot4_i32_i8: about half the VALU work a step,
-// but no faster than the canonical form with its skewed dealing (Q4_0 head
-// 20.2-21.1 us either way). At K = 4,096 and 8,192 it measured slower than
-// the canonical decode and is not used there. Not the canonical bits:
+// decodes a group with 24 v_dot4_i32_i8: about half the VALU work a step.
+// With plain weight copies it ran within noise of the canonical form (Q4_0
+// head 20.2-21.1 us either way); with non-temporal copies it is ~10% faster
+// there (19.6 against 21.7 us). At K = 4,096 and 8,192 it measured slower
+// than the canonical decode and is not used there. Not the canonical bits:
 // within 1e-5 of them.
 #include <algorithm>
 
