@@ -13,8 +13,11 @@ A step is one pass of the hot path over one batch of synthetic input:
   c4  Q4_0 prefill GEMM M=512, N=8192, K=2048 (Llama-3.2-1B gate/up)
   c5  Llama-3.2-1B prefill, M=2048, 16 layers x 7 Q4_0 GEMMs (fused as c3) + Q6_K
       head on the last row
-  c4, c5 run on the matrix cores (split-f16, within tolerance) and again on the
-  canonical VALU tile (bit-exact), reported as c4_canonical, c5_canonical.
+  c4, c5 run on the matrix cores (split-f16, within tolerance), again in the
+  canonical order as a drop-in caller gets it (AUTO, bit-exact: the matrix
+  cores' f32 fused multiply-add tile at these sizes), reported as c4_canonical,
+  c5_canonical, and on the 128-row VALU tile (the same bits) as c4_tile128,
+  c5_tile128.
   c6  a short prefill step, 32 tokens through Llama-3.2-1B's down projection
       (2048x8192 Q4_0): split along K (c6_split), tiled (c6_tiled), matrix cores
   c7  the embedding gather from Qwen3-0.6B's Q6_K table (151936x1024): a
@@ -25,8 +28,9 @@ copy (global_load_lds_dwordx4, 9 KB a wave a step) with nothing decoded, the
 practical ceiling under the 8 TB/s peak; frac_of_read_floor is the decode's
 rate over it.
 Every row carries a roofline in the unit its kernel runs on: HBM GB/s for the
-decodes; TFLOP/s for the prefills, the VALU tile against the FP32 peak, the
-matrix cores against the dense FP16 peak and this design's useful half of it.
+decodes; TFLOP/s for the prefills, the VALU tiles and the f32 fused
+multiply-add tile against the FP32 peak, the split-f16 matrix cores against
+the dense FP16 peak and that design's useful half of it.
 Inputs are seeded synthetic data (BASELINE's distributions) resident in HBM
 before timing; a GEMV's weights rotate over copies totalling > 2x the 256 MB
 MALL so every step reads HBM. Each config's launches are captured once in a
@@ -248,6 +252,30 @@ def time_decode_shapes(spec, steps, warmup, settle_ms, limbs=False):
     return out
 
 
+def time_prefill_shapes(spec, steps, warmup, settle_ms):
+    """One Q4_0 prefill product a shape ROWSxKxTOKENS, timed as the configs
+    are, on each bit-exact path (CANONICAL: the 128-row tile; AUTO; EXACT_MFMA:
+    the matrix cores' fused multiply-add): {"ROWSxKxTOKENS": {path: {us,
+    TFLOP/s, kernel}}}. The figures that choose AUTO's kernel."""
+    S = Setup()
+    S.settle_ms = settle_ms
+    rng = np.random.default_rng(2)
+    out = {}
+    try:
+        for item in spec.split(","):
+            rows, columns, tokens = (int(v) for v in item.lower().split("x"))
+            row = {}
+            for path in (S.mm.GemmPath.CANONICAL, S.mm.GemmPath.AUTO, S.mm.GemmPath.EXACT_MFMA):
+                r = run_gemm(S, f"{item} {path.name}", [("write", [(rows, columns)])], tokens, steps, warmup, rng,
+                             path)
+                row[path.name] = {"us": round(r["ms_per_step"] * 1e3, 2), "TFLOP/s": round(r["TFLOP/s"], 1),
+                                  "kernel": r["kernels"][0]}
+            out[item] = row
+    finally:
+        S.close()
+    return out
+
+
 def run_read_floor(S, name, nbytes, copies, steps, warmup):
     """The same bytes read and nothing else (harness chx_read: the LDS-streamed
     decodes' copy, 9 KB a wave a step, with no decode), over `copies` buffers
@@ -332,25 +360,35 @@ def read_sweep(steps, warmup, settle_ms):
     return {"bytes": nbytes, "copies": 3, "steps": steps, "forms": rows}
 
 
-MFMA_SHAPES = ((0, "f16 16x16x32", 2 * 16 * 16 * 32), (1, "f16 32x32x16", 2 * 32 * 32 * 16),
-               (2, "bf16 16x16x32", 2 * 16 * 16 * 32), (3, "i8 16x16x64", 2 * 16 * 16 * 64),
-               (4, "i8 32x32x32", 2 * 32 * 32 * 32))
+# (probe shape, name, operations an instruction, the shape's dense peak TOP/s, chain counts timed)
+MFMA_SHAPES = ((0, "f16 16x16x32", 2 * 16 * 16 * 32, F16_PEAK_TFLOPS, (1, 8)),
+               (1, "f16 32x32x16", 2 * 32 * 32 * 16, F16_PEAK_TFLOPS, (1, 8)),
+               (2, "bf16 16x16x32", 2 * 16 * 16 * 32, F16_PEAK_TFLOPS, (1, 8)),
+               (3, "i8 16x16x64", 2 * 16 * 16 * 64, 2 * F16_PEAK_TFLOPS, (1, 8)),
+               (4, "i8 32x32x32", 2 * 32 * 32 * 32, 2 * F16_PEAK_TFLOPS, (1, 8)),
+               (5, "f32 32x32x1 (2 blocks)", 2 * 32 * 32 * 2, FP32_PEAK_TFLOPS, (1, 4)),
+               (6, "f32 16x16x1 (4 blocks)", 2 * 16 * 16 * 4, FP32_PEAK_TFLOPS, (1, 8)),
+               (7, "f32 32x32x2", 2 * 32 * 32 * 2, FP32_PEAK_TFLOPS, (1, 8)),
+               (8, "f32 16x16x4", 2 * 16 * 16 * 4, FP32_PEAK_TFLOPS, (1, 8)))
 
 
-def mfma_rate(iters=2000):
-    """Each matrix-core shape the prefill could use, issued back to back by
-    every wave of the GPU (chx_mfma_rate), 1 or 8 independent accumulators a
-    wave, 1, 2 or 4 waves a SIMD: the sustained rate against the part's dense
-    peak, and the time a SIMD spends on one instruction (ns; x the clock for
-    cycles). Single launches between HIP events, median of 5."""
+def mfma_rate(iters=2000, shapes=None):
+    """Each matrix-core shape the prefill could use (`shapes`: probe numbers,
+    default all), issued back to back by every wave of the GPU
+    (chx_mfma_rate), a few independent accumulators a wave, 1, 2 or 4 waves a
+    SIMD: the sustained rate against the shape's dense peak, and the time a
+    SIMD spends on one instruction (ns; x the clock for cycles). Single
+    launches between HIP events, median of 5."""
     S = Setup()
     hx = S.hx
     cus = int(hx.device_name(0).split("cus=")[1].split("|")[0])
     sink = S.buffer(nbytes=cus * 4 * 256 * 4)
     rows = []
     try:
-        for shape, name, ops in MFMA_SHAPES:
-            for chains in (1, 8):
+        for shape, name, ops, peak, chain_counts in MFMA_SHAPES:
+            if shapes is not None and shape not in shapes:
+                continue
+            for chains in chain_counts:
                 for per_simd in (1, 2, 4):
                     blocks = cus * per_simd
 
@@ -361,7 +399,6 @@ def mfma_rate(iters=2000):
                     count = blocks * 4 * iters * chains
                     rate = count * ops / (ms * 1e-3) / 1e12
                     ns = ms * 1e6 / (count / (cus * 4))
-                    peak = F16_PEAK_TFLOPS * (2 if shape >= 3 else 1)
                     rows.append({"shape": name, "chains": chains, "waves_a_simd": per_simd,
                                  "TOP/s": round(rate, 1), "frac_of_dense_peak": round(rate / peak, 3),
                                  "ns_an_instruction_a_simd": round(ns, 2)})
@@ -719,9 +756,9 @@ def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=No
 
     ms = S.time_graph(body, steps, warmup)
     tflops = flops / (ms * 1e-3) / 1e12
-    roof = gemm_roofline(tflops, path, name)
     target = mm.Target(256, path, workspace_bytes=1 << 40)
     kernels = sorted({mm.plan_launch(m, t, target, gate, sums_bytes).kernel.name for m, t in launches})
+    roof = gemm_roofline(tflops, path, name, kernels)
     log(f"{name}: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s ({100 * roof['frac']:.1f}% of its unit's peak, "
         f"{roof['peak']} TFLOP/s {roof['bound']}); kernels {','.join(kernels)}")
     out = {"ms_per_step": ms, "ms_first_replay": S.last_first, "flops": flops, "TFLOP/s": tflops, "path": path.name,
@@ -737,28 +774,35 @@ def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=No
     return out
 
 
-def gemm_roofline(tflops, path, name):
-    """The roofline of a prefill row in the unit its path runs on: the VALU
-    tile against the FP32 peak; the matrix cores against the dense FP16 peak,
-    and against the useful ceiling of this design (two f16 products an output
-    product: half the peak). Counter traffic where profiles/traffic_c4.json
-    holds it (c4)."""
-    mm_path = path.name
-    if mm_path == "SPLIT_F16_MFMA":
+def gemm_roofline(tflops, path, name, kernels):
+    """The roofline of a prefill row in the unit its kernel runs on: the
+    canonical order on the matrix cores' f32 fused multiply-add (GEMM_EXACT)
+    against their FP32 peak; the VALU tiles against the FP32 peak; the
+    split-f16 matrix cores against the dense FP16 peak, and against the useful
+    ceiling of that design (two f16 products an output product: half the
+    peak). Counter traffic where profiles/traffic_c4.json holds it (c4)."""
+    if path.name == "SPLIT_F16_MFMA":
         roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(tflops / F16_PEAK_TFLOPS, 4), "useful_peak": F16_PEAK_TFLOPS / 2,
                 "frac_of_useful": round(tflops / (F16_PEAK_TFLOPS / 2), 4)}
+        kind = "mfma"
+    elif "GEMM_EXACT" in kernels:
+        roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / FP32_PEAK_TFLOPS, 4)}
+        kind = "exact"
     else:
         roof = {"bound": "valu", "achieved": round(tflops, 1), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(tflops / FP32_PEAK_TFLOPS, 4)}
-    roof["traffic"] = gemm_traffic(name, mm_path)
+        kind = "canonical"
+    roof["traffic"] = gemm_traffic(name, kind)
     return roof
 
 
-def gemm_traffic(name, path):
+def gemm_traffic(name, kind):
     """HBM bytes a step of c4 from the counter runs in profiles/traffic_c4.json
-    (FETCH_SIZE and WRITE_SIZE, KiB a dispatch, scaled as traffic_c2.json's);
-    the matrix-core step adds prepare_x's. None for other configs."""
+    (FETCH_SIZE and WRITE_SIZE, KiB a dispatch, scaled as traffic_c2.json's)
+    for its kernel kind (mfma: the split-f16 step, with prepare_x's; exact;
+    canonical: the 128-row tile). None for other configs or kinds absent."""
     file = os.path.join(ROOT, "profiles", "traffic_c4.json")
     if not name.startswith("c4") or not os.path.exists(file):
         return None
@@ -768,9 +812,9 @@ def gemm_traffic(name, path):
     def b(e):
         return (e["fetch_kib"] * t["fetch_scale"] + e["write_kib"] * t["write_scale"]) * 1024
 
-    if path == "SPLIT_F16_MFMA":
+    if kind == "mfma":
         return int(round(b(k["mfma"]) + b(k["prepare_x"])))
-    return int(round(b(k["canonical"])))
+    return int(round(b(k[kind]))) if kind in k else None
 
 
 def gemv_traffic(name):
@@ -954,8 +998,11 @@ def main():
                    help="time decode products of the given shapes and exit: a comma list of ROWSxCOLUMNS[:TYPE], "
                         "TYPE a GGUF type number (2 Q4_0, default; 3 Q4_1; 8 Q8_0; 14 Q6_K, repacked)")
     p.add_argument("--limbs", action="store_true", help="with --decode: the INT8_LIMBS decode path")
-    p.add_argument("--mfma-rate", action="store_true",
-                   help="time each matrix-core instruction shape's sustained rate (a probe) and exit")
+    p.add_argument("--prefill", metavar="SHAPES",
+                   help="time Q4_0 prefill products ROWSxKxTOKENS (a comma list) on each bit-exact path and exit")
+    p.add_argument("--mfma-rate", nargs="?", const="all", default=None,
+                   help="time each matrix-core instruction shape's sustained rate (a probe) and exit; "
+                        "optionally a comma list of probe shape numbers (0-8)")
     p.add_argument("--read-sweep", action="store_true",
                    help="time every pure-read form over C2's bytes (the read ceiling) and exit")
     args = p.parse_args()
@@ -963,7 +1010,8 @@ def main():
         print(json.dumps(cpu_table(min(os.cpu_count() or 1, 16))), flush=True)
         return
     if args.mfma_rate:
-        print(json.dumps(mfma_rate()), flush=True)
+        shapes = None if args.mfma_rate == "all" else {int(x) for x in args.mfma_rate.split(",")}
+        print(json.dumps(mfma_rate(shapes=shapes)), flush=True)
         return
     if args.read_sweep:
         print(json.dumps(read_sweep(max(args.steps, 20), args.warmup, args.settle_ms)), flush=True)
@@ -971,6 +1019,9 @@ def main():
     if args.decode:
         print(json.dumps(time_decode_shapes(args.decode, args.steps, args.warmup, args.settle_ms, args.limbs)),
               flush=True)
+        return
+    if args.prefill:
+        print(json.dumps(time_prefill_shapes(args.prefill, args.steps, args.warmup, args.settle_ms)), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this path is measured on one MI355X); got --gpus {args.gpus}",
@@ -1033,7 +1084,11 @@ def main():
         # canonical VALU tile (bit-exact), each on the same shapes.
         ws = S.buffer(nbytes=S.mm.workspace_bytes(2048, 8192))
         S.ctx.set_workspace(ws.ptr, ws.nbytes)
-        paths = [("", S.mm.GemmPath.SPLIT_F16_MFMA), ("_canonical", S.mm.GemmPath.CANONICAL)]
+        # The split-f16 matrix cores (within 1e-5, opt-in); the bit-exact
+        # default (AUTO: the matrix cores' fused multiply-add tile at these
+        # sizes); the 128-row VALU tile (CANONICAL), the same bits.
+        paths = [("", S.mm.GemmPath.SPLIT_F16_MFMA), ("_canonical", S.mm.GemmPath.AUTO),
+                 ("_tile128", S.mm.GemmPath.CANONICAL)]
         if "c4" in only:
             for tag, path in paths:
                 out["c4" + tag] = run_gemm(S, "c4" + tag, [("write", [(8192, 2048)])], 512, args.steps, args.warmup,

@@ -227,10 +227,12 @@ Verdict describe(const charlotte_hip_matmul_desc* desc, uint32_t tokens, const c
 }
 
 // The kernel a described product runs on `t`, and its shape: decode for one
-// token or the head's last; else the VALU tile, split along K when the gate
-// allows the step and its range sums fit `range_sums_bytes` (a product with
-// options, or gated, never splits: matmul.cpp:166-172, 233-241), or the
-// matrix cores when the target asks for them.
+// token or the head's last; else the split along K when the gate allows the
+// step and its range sums fit `range_sums_bytes` (a product with options, or
+// gated, never splits: matmul.cpp:166-172, 233-241); else a tile in the
+// canonical order (the matrix cores' fused multiply-add, the short-step tile
+// or the 128-row VALU tile), or the split-f16 matrix cores when the target
+// asks for them.
 Verdict plan_product(const chm::Product& a, uint32_t format, const Target& t, charlotte_hip_matmul_split_gate gate,
                      uint64_t range_sums_bytes, chm::Plan* plan) {
     *plan = chm::Plan{};
@@ -260,9 +262,19 @@ Verdict plan_product(const chm::Product& a, uint32_t format, const Target& t, ch
         split = a.tokens <= most;
     }
     chm::plan_gemm_canonical(a, t.compute_units, split, plan);
-    // A step the 128-row tile leaves short of one workgroup a compute unit:
-    // the short-step tile, K split among its waves (the same bits).
-    if (!split && t.gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_AUTO && plan->tiles < t.compute_units)
+    if (split || t.gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_CANONICAL) return {};
+    chm::Plan exact;
+    chm::plan_gemm_exact(a, format, t.compute_units, &exact);
+    // AUTO: the matrix cores' fused multiply-add tile where the step gives it
+    // at least two waves a compute unit (below that each of its waves' walk
+    // through K is the step's time: measured slower than the short-step tile
+    // at 256 waves, faster at 512); else, a step the 128-row tile leaves short
+    // of one workgroup a compute unit: the short-step tile, K split among its
+    // waves. The same bits whichever runs.
+    const uint64_t exact_waves = uint64_t{(a.rows + 63) / 64} * exact.token_tiles;
+    if (t.gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_EXACT_MFMA || exact_waves >= 2ull * t.compute_units)
+        *plan = exact;
+    else if (plan->tiles < t.compute_units)
         chm::plan_gemm_short(a, t.compute_units, plan);
     return {};
 }
@@ -326,7 +338,7 @@ charlotte_hip_matmul_status charlotte_hip_matmul_set_gemm_path(charlotte_hip_mat
                                                                charlotte_hip_matmul_gemm_path path) {
     if (!ctx) return CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT;
     if (path != CHARLOTTE_HIP_MATMUL_GEMM_AUTO && path != CHARLOTTE_HIP_MATMUL_GEMM_CANONICAL &&
-        path != CHARLOTTE_HIP_MATMUL_GEMM_SPLIT_F16_MFMA)
+        path != CHARLOTTE_HIP_MATMUL_GEMM_SPLIT_F16_MFMA && path != CHARLOTTE_HIP_MATMUL_GEMM_EXACT_MFMA)
         return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "gemm path: " + std::to_string(path));
     ctx->gemm_path = path;
     return ok(ctx);
@@ -528,6 +540,7 @@ static Status run_plan(charlotte_hip_matmul_context* ctx, const chm::Product& a,
         case chm::kGemmMfma: e = chm::launch_gemm_mfma(a, format, plan, ctx->workspace, s); break;
         case chm::kGemmTiled: e = chm::launch_gemm_canonical(a, format, plan, nullptr, s); break;
         case chm::kGemmShort: e = chm::launch_gemm_short(a, format, plan, s); break;
+        case chm::kGemmExact: e = chm::launch_gemm_exact(a, format, plan, s); break;
         case chm::kGemmSplit: e = chm::launch_gemm_canonical(a, format, plan, range_sums, s); break;
         default: e = chm::launch_gemv(a, format, plan, ctx->compute_units, s); break;
     }

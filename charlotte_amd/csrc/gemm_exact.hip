@@ -1,0 +1,274 @@
+// Prefill on the matrix cores in the canonical order: bit-exact.
+//
+// gemm_exact — v_mfma_f32_32x32x1_2b_f32 (K = 1, two 32 x 32 blocks) rounds
+// each element once, as a fused multiply-add: d = c + a b is fmaf(a, b, c)
+// bit for bit (checked on the GPU by harness.hip's mfma_fma_check over
+// random, cancelling, halfway, denormal, overflowing, infinite and NaN
+// operands). So a range's chain s = fma(w_k, x_k, s), in k order from +0
+// (matmul.wgsl:121-126, 224-230), runs as a chain of these instructions, one
+// k at a time, for 2,048 outputs at once; a range's sums then add into the
+// totals in order on the VALU (matmul.wgsl:134-137), as gemm_canonical adds
+// them. Every output is gemm_canonical's bits, and decode's.
+//
+// A wave takes 64 rows x TT tokens. At each k lane l supplies row R + l's
+// weight as the A operand (lanes 0-31 block 0's rows, 32-63 block 1's).
+// TT = 64: lane l supplies token T + l's input as B (lanes 0-31 block 0's
+// columns, 32-63 block 1's), and two instructions a k, each broadcasting one
+// block's A to both blocks (CBSZ 1, ABID 0 and 1), give rows R .. R + 31 and
+// R + 32 .. R + 63 against tokens T .. T + 63. TT = 32 (for steps too small
+// to give every SIMD two waves of 64 x 64): lanes l and l + 32 both supply
+// token T + l % 32, and one instruction a k gives rows R .. R + 63 against
+// tokens T .. T + 31. Each lane decodes its row's group (32 exact f32 weights) and
+// loads its token's 32 inputs into registers, a group ahead; nothing goes
+// through LDS and the waves of a workgroup never wait for one another. The
+// VALU's share — a group's decode, a range's adds — is small beside the 64
+// matrix instructions a group, and runs while they do.
+//
+// Result layout of one instruction (register v of 32, lane l): block v / 16,
+// in it column l % 32 and row 8 ((v % 16) / 4) + 4 (l / 32) + v % 4 — rows
+// p, p + 1 (p even) in one lane, so a gated product's gate and up totals
+// (rows 2r, 2r + 1) meet there.
+#include "decode.hpp"
+#include "plan.hpp"
+#include "product.hpp"
+
+namespace chm {
+
+namespace {
+
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+
+constexpr uint32_t kWaveRows = 64;   // rows a wave
+constexpr uint32_t kWaves = 4;       // waves a workgroup, each its own 64 rows
+
+// The 32 exact weights of a group as loaded (the arithmetic of formats.hpp's
+// weight(), which the VALU tile stages: the same values).
+template <uint32_t F>
+__device__ __forceinline__ void weights_of(const Raw<F>& r, float* w) {
+    if constexpr (F == kQ4_0) {
+        const Q4_0Group g = group_of(Q4_0Bytes{make_uint4(r.w[0], r.w[1], r.w[2], r.w[3]), r.d});
+#pragma unroll
+        for (int l = 0; l < 32; ++l) w[l] = weight(g, l);
+    } else if constexpr (F == kQ4_1) {
+        const Q4_1Group g = group_of(Q4_1Bytes{make_uint4(r.w[0], r.w[1], r.w[2], r.w[3]), r.dm});
+#pragma unroll
+        for (int l = 0; l < 32; ++l) w[l] = weight(g, l);
+    } else if constexpr (F == kQ8_0) {
+        const Q8_0Group g = group_of(Q8_0Bytes{make_uint4(r.w[0], r.w[1], r.w[2], r.w[3]),
+                                               make_uint4(r.w[4], r.w[5], r.w[6], r.w[7]), r.d});
+#pragma unroll
+        for (int l = 0; l < 32; ++l) w[l] = weight(g, l);
+    } else if constexpr (F == kQ6_K) {
+        const Q6_KGroup g = group_of(
+            Q6_KBytes{make_uint4(r.lo[0], r.lo[1], r.lo[2], r.lo[3]), make_uint2(r.hi[0], r.hi[1]), r.sc, r.d});
+#pragma unroll
+        for (int l = 0; l < 32; ++l) w[l] = weight(g, l);
+    } else if constexpr (F == kF32) {
+#pragma unroll
+        for (int l = 0; l < 32; ++l) w[l] = __uint_as_float(r.w[l]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            w[2 * i] = F == kF16 ? half_to_float(r.w[i] & 0xFFFFu) : bf16_low(r.w[i]);
+            w[2 * i + 1] = F == kF16 ? half_to_float(r.w[i] >> 16) : bf16_high(r.w[i]);
+        }
+    }
+}
+
+template <uint32_t F, uint32_t TT, bool FULL, bool CLIP>
+__global__ __launch_bounds__(256, 2) void gemm_exact(Product a, uint32_t token_tiles) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t tile_t = blockIdx.x % token_tiles, tile_r = blockIdx.x / token_tiles;
+    const uint32_t T = tile_t * TT, R = (tile_r * kWaves + wave) * kWaveRows;
+    if (R >= a.rows) return;  // the whole wave: no barrier follows
+    const uint32_t G = a.groups;
+    const uint64_t K = static_cast<uint64_t>(G) * 32;
+
+    // Rows and tokens past the product read its last row or token; their
+    // outputs are never stored.
+    const Piece pc = piece_of(a, min(R + lane, a.rows - 1));
+    const uint64_t row0 = static_cast<uint64_t>(pc.row) * G;
+    const uint32_t my_token = T + (TT == 64 ? lane : lane & 31u);
+    const float4* xrow = reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(min(my_token, a.tokens - 1)) * K);
+    float lo = 0.0f, hi = 0.0f;
+    if constexpr (CLIP) lo = *a.clip[0], hi = *a.clip[1];
+
+    // Range sums (TT = 64: rows R .. R + 31 and R + 32 .. R + 63 against 64
+    // tokens; TT = 32: s0 alone, rows R .. R + 63 against 32) and totals.
+    constexpr int S = TT == 64 ? 2 : 1;
+    f32x32 s0 = {}, s1 = {};
+    float t[S][32];
+#pragma unroll
+    for (int v = 0; v < 32; ++v)
+#pragma unroll
+        for (int i = 0; i < S; ++i) t[i][v] = 0.0f;
+
+    // The range that ends after group g is the one before `next_r`'s first
+    // group; ranges with no groups (G < 32) hold zero and add nothing.
+    uint32_t next_r = 1;
+    while (next_r < 32 && range_lo(next_r, G) == 0) ++next_r;
+
+    // A group's bytes and inputs are loaded a whole group ahead, into one of
+    // two buffers (the loop takes groups in pairs, so each buffer keeps its
+    // registers): at the top of group g every load of group g has been
+    // waited for, and the loads of group g + 1 go out before its products,
+    // so no wait inside them depends on a load issued in the same group.
+    struct Buffer {
+        Raw<F> raw;
+        float4 xq[8];
+    };
+    auto fetch = [&](Buffer& b, uint32_t g) {
+        b.raw.load(pc.piece, pc.blocks, row0 + g);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) b.xq[v] = xrow[8 * g + v];
+    };
+    bool fresh = true;  // the next product starts a range: its chain from +0
+    auto group = [&](const Buffer& b, uint32_t g) {
+        float w[32], x[32];
+        weights_of(b.raw, w);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            float4 q = b.xq[v];
+            if constexpr (CLIP) {
+                q.x = clamp_to(q.x, lo, hi);
+                q.y = clamp_to(q.y, lo, hi);
+                q.z = clamp_to(q.z, lo, hi);
+                q.w = clamp_to(q.w, lo, hi);
+            }
+            x[4 * v] = q.x;
+            x[4 * v + 1] = q.y;
+            x[4 * v + 2] = q.z;
+            x[4 * v + 3] = q.w;
+        }
+        // A range's first product takes +0 as its accumulator, so the chain
+        // starts from +0 as fma(w, x, +0) does (the sums are never cleared).
+        if (fresh) {
+            const f32x32 zero = {};
+            if constexpr (TT == 64) {
+                s0 = __builtin_amdgcn_mfma_f32_32x32x1f32(w[0], x[0], zero, 1, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x1f32(w[0], x[0], zero, 1, 1, 0);
+            } else {
+                s0 = __builtin_amdgcn_mfma_f32_32x32x1f32(w[0], x[0], zero, 0, 0, 0);
+            }
+        } else {
+            if constexpr (TT == 64) {
+                s0 = __builtin_amdgcn_mfma_f32_32x32x1f32(w[0], x[0], s0, 1, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x1f32(w[0], x[0], s1, 1, 1, 0);
+            } else {
+                s0 = __builtin_amdgcn_mfma_f32_32x32x1f32(w[0], x[0], s0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int k = 1; k < 32; ++k) {
+            if constexpr (TT == 64) {
+                s0 = __builtin_amdgcn_mfma_f32_32x32x1f32(w[k], x[k], s0, 1, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x1f32(w[k], x[k], s1, 1, 1, 0);
+            } else {
+                s0 = __builtin_amdgcn_mfma_f32_32x32x1f32(w[k], x[k], s0, 0, 0, 0);
+            }
+        }
+        fresh = g + 1 == range_lo(next_r, G);
+        if (fresh) {  // range next_r - 1 ends
+#pragma unroll
+            for (int v = 0; v < 32; ++v) {
+                const float a0 = s0[v];
+                t[0][v] = t[0][v] + a0;
+                if constexpr (S == 2) {
+                    const float a1 = s1[v];
+                    t[S - 1][v] = t[S - 1][v] + a1;
+                }
+            }
+            while (next_r < 32 && range_lo(next_r, G) <= g + 1) ++next_r;
+        }
+    };
+
+    // Every fetch is issued on every path (past the last group it reads the
+    // last group again, unused), so the count of loads in flight at each wait
+    // is the same on every path: a wait for one buffer never waits for the
+    // other's loads.
+    Buffer A, B;
+    fetch(A, 0);
+    for (uint32_t g = 0; g < G; g += 2) {
+        fetch(B, min(g + 1, G - 1));
+        group(A, g);
+        if (g + 1 >= G) break;
+        fetch(A, min(g + 2, G - 1));
+        group(B, g + 1);
+    }
+
+#pragma unroll
+    for (int v = 0; v < 32; ++v) {
+        const uint32_t in_block = 8 * ((v & 15) / 4) + 4 * (lane >> 5) + (v & 3);
+        if constexpr (TT == 64) {
+            const uint32_t token = T + 32 * (v / 16) + (lane & 31u), p = R + in_block;
+            if (token < a.tokens) {
+                if (p < a.rows) emit<FULL>(a, p, token, token, t[0][v], (v & 1) ? 0.0f : t[0][v ^ 1]);
+                if (p + 32 < a.rows) emit<FULL>(a, p + 32, token, token, t[S - 1][v], (v & 1) ? 0.0f : t[S - 1][v ^ 1]);
+            }
+        } else {
+            const uint32_t token = T + (lane & 31u), p = R + 32 * (v / 16) + in_block;
+            if (token < a.tokens && p < a.rows) emit<FULL>(a, p, token, token, t[0][v], (v & 1) ? 0.0f : t[0][v ^ 1]);
+        }
+    }
+}
+
+template <uint32_t F, uint32_t TT>
+void go_exact_tile(const Product& a, const Plan& plan, hipStream_t stream) {
+    const dim3 grid(static_cast<uint32_t>(plan.workgroups));
+    if (plain_epilogue(a))
+        hipLaunchKernelGGL((gemm_exact<F, TT, false, false>), grid, dim3(64 * kWaves), 0, stream, a, plan.token_tiles);
+    else if (!clipped(a))
+        hipLaunchKernelGGL((gemm_exact<F, TT, true, false>), grid, dim3(64 * kWaves), 0, stream, a, plan.token_tiles);
+    else
+        hipLaunchKernelGGL((gemm_exact<F, TT, true, true>), grid, dim3(64 * kWaves), 0, stream, a, plan.token_tiles);
+}
+
+template <uint32_t F>
+void go_exact(const Product& a, const Plan& plan, hipStream_t stream) {
+    if constexpr (F != kF32) {
+        if (plan.tile_tokens == 64) return go_exact_tile<F, 64>(a, plan, stream);
+    }
+    go_exact_tile<F, 32>(a, plan, stream);
+}
+
+}  // namespace
+
+// Tiles of 256 rows (four waves of 64) by 64 tokens where that gives every
+// SIMD (4 a compute unit) a wave, else by 32 (F32 always by 32: its 32 dwords
+// a group beside 64 tokens' sums would not fit two waves' registers); token
+// tile first, so the tiles reading one row tile's weights run together. One
+// wave of 64 x 64 a SIMD (two chains of products) measured faster than two
+// of 64 x 32 (one chain each): C4 98.6 against 93.4 TFLOP/s.
+void plan_gemm_exact(const Product& a, uint32_t format, uint32_t compute_units, Plan* plan) {
+    *plan = Plan{};
+    const uint64_t wave_rows = (a.rows + kWaveRows - 1) / kWaveRows;
+    const uint32_t tt =
+        format != kF32 && wave_rows * ((a.tokens + 63) / 64) >= 4ull * compute_units ? 64 : 32;
+    plan->kernel = kGemmExact;
+    plan->launches = 1;
+    plan->tile_tokens = tt;
+    plan->tile_rows = kWaves * kWaveRows;
+    plan->token_tiles = (a.tokens + tt - 1) / tt;
+    plan->row_tiles = (a.rows + plan->tile_rows - 1) / plan->tile_rows;
+    plan->chunks = 1;
+    plan->wave_rows = kWaveRows / 32;
+    plan->wave_tokens = tt / 32;
+    plan->tiles = static_cast<uint64_t>(plan->token_tiles) * plan->row_tiles;
+    plan->workgroups = plan->tiles;
+}
+
+hipError_t launch_gemm_exact(const Product& a, uint32_t format, const Plan& plan, hipStream_t stream) {
+    switch (format) {
+        case kQ4_0: go_exact<kQ4_0>(a, plan, stream); break;
+        case kQ4_1: go_exact<kQ4_1>(a, plan, stream); break;
+        case kQ8_0: go_exact<kQ8_0>(a, plan, stream); break;
+        case kQ6_K: go_exact<kQ6_K>(a, plan, stream); break;
+        case kF32: go_exact<kF32>(a, plan, stream); break;
+        case kF16: go_exact<kF16>(a, plan, stream); break;
+        case kBF16: go_exact<kBF16>(a, plan, stream); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace chm

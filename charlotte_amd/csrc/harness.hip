@@ -169,11 +169,35 @@ typedef float mf16 __attribute__((ext_vector_type(16)));
 typedef int mi4 __attribute__((ext_vector_type(4)));
 typedef int mi16 __attribute__((ext_vector_type(16)));
 
+typedef float mf32 __attribute__((ext_vector_type(32)));
+
 // Shape S (0 f16 16x16x32, 1 f16 32x32x16, 2 bf16 16x16x32, 3 i8 16x16x64,
-// 4 i8 32x32x32), C chains, `iters` rounds of C instructions a wave.
+// 4 i8 32x32x32, 5 f32 32x32x1 two blocks, 6 f32 16x16x1 four blocks, 7 f32
+// 32x32x2, 8 f32 16x16x4), C chains, `iters` rounds of C instructions a wave.
 template <int S, int C>
 __global__ __launch_bounds__(256) void mfma_rate_kernel(uint32_t iters, uint32_t* sink) {
     const float f = static_cast<float>(threadIdx.x & 7u) * 0.125f;
+    if constexpr (S >= 5) {
+        using Acc = std::conditional_t<S == 5, mf32, std::conditional_t<S == 8, mf4, mf16>>;
+        // 32x32x1's 32 accumulators a chain: at most 4 chains (never launched with 8)
+        constexpr int CC = S == 5 && C > 4 ? 4 : C;
+        const float g = 1.0f + f;
+        Acc acc[CC] = {};
+        for (uint32_t i = 0; i < iters; ++i) {
+#pragma unroll
+            for (int c = 0; c < CC; ++c) {
+                if constexpr (S == 5) acc[c] = __builtin_amdgcn_mfma_f32_32x32x1f32(f, g, acc[c], 0, 0, 0);
+                else if constexpr (S == 6) acc[c] = __builtin_amdgcn_mfma_f32_16x16x1f32(f, g, acc[c], 0, 0, 0);
+                else if constexpr (S == 7) acc[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(f, g, acc[c], 0, 0, 0);
+                else acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(f, g, acc[c], 0, 0, 0);
+            }
+        }
+        uint32_t fold = 0;
+#pragma unroll
+        for (int c = 0; c < CC; ++c) fold ^= __builtin_bit_cast(uint32_t, acc[c][0]);
+        if (fold == kNever) sink[static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = fold;
+        return;
+    }
     const mh8 h = {(_Float16)f, (_Float16)0.5f, (_Float16)f, (_Float16)1.0f,
                    (_Float16)f, (_Float16)0.25f, (_Float16)f, (_Float16)2.0f};
     const mb8 bb = {(__bf16)f, (__bf16)0.5f, (__bf16)f, (__bf16)1.0f, (__bf16)f, (__bf16)0.25f, (__bf16)f, (__bf16)2.0f};
@@ -206,6 +230,92 @@ __global__ __launch_bounds__(256) void mfma_rate_kernel(uint32_t iters, uint32_t
         for (int c = 0; c < C; ++c) fold ^= __builtin_bit_cast(uint32_t, acc[c][0]);
     }
     if (fold == kNever) sink[static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = fold;
+}
+
+// Whether the K = 1 f32 matrix instruction (32x32x1, two blocks) rounds as
+// one fused multiply-add. Pair p gives a and b to every lane, and the wave's
+// 2,048 accumulator values c[p][64 v + lane] (v < 32); every element of the
+// result is then c + a b whatever its place in the blocks, so no layout is
+// assumed: lane l compares its result v with fmaf(a, b, c) bit for bit (two
+// NaNs agree). out: [0] elements differing, [1] elements compared, then for
+// the first 64 differing: pair, element, the instruction's bits, fmaf's bits.
+__global__ __launch_bounds__(64) void mfma_fma_check_kernel(const float* ab, const float* c, uint32_t pairs,
+                                                            uint32_t* out) {
+    const uint32_t lane = threadIdx.x;
+    uint32_t differing = 0, compared = 0;
+    for (uint32_t p = blockIdx.x; p < pairs; p += gridDim.x) {
+        const float a = ab[2 * p], b = ab[2 * p + 1];
+        const float* cp = c + static_cast<uint64_t>(p) * 2048;
+        mf32 acc;
+#pragma unroll
+        for (int v = 0; v < 32; ++v) acc[v] = cp[64 * v + lane];
+        const mf32 d = __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, acc, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 32; ++v) {
+            // the element copied out first: this compiler lowers a bit cast of
+            // a vector's element d[v] to element 0 whatever v is
+            const float dv = d[v];
+            const float r = __builtin_fmaf(a, b, acc[v]);
+            const uint32_t rb = __builtin_bit_cast(uint32_t, r), db = __builtin_bit_cast(uint32_t, dv);
+            const bool same = rb == db || (r != r && dv != dv);
+            ++compared;
+            if (!same) {
+                const uint32_t at = atomicAdd(out, 1u);
+                if (at < 64) {
+                    out[2 + 4 * at] = p;
+                    out[3 + 4 * at] = 64 * v + lane;
+                    out[4 + 4 * at] = db;
+                    out[5 + 4 * at] = rb;
+                }
+                ++differing;
+            }
+        }
+    }
+    (void)differing;
+    atomicAdd(out + 1, compared);
+}
+
+// Where a shape puts each accumulator it is given: a = b = 0 and C read from
+// c[64 v + lane] (v < the shape's registers), D written to out at the same
+// places, so out = c where the instruction adds C element by element in its
+// own layout. S: 5 f32 32x32x1 two blocks, 6 f32 16x16x1 four blocks, 7 f32
+// 32x32x2, 8 f32 16x16x4, 9 f32 4x4x1 sixteen blocks, 1 f16 32x32x16.
+template <int S>
+__global__ __launch_bounds__(64) void mfma_c_probe_kernel(const float* c, float* out) {
+    const uint32_t lane = threadIdx.x;
+    constexpr int R = S == 5 ? 32 : S == 8 || S == 9 ? 4 : 16;
+    using Acc = std::conditional_t<R == 32, mf32, std::conditional_t<R == 4, mf4, mf16>>;
+    Acc acc;
+#pragma unroll
+    for (int v = 0; v < R; ++v) acc[v] = c[64 * v + lane];
+    Acc d;
+    if constexpr (S == 5) d = __builtin_amdgcn_mfma_f32_32x32x1f32(0.0f, 0.0f, acc, 0, 0, 0);
+    else if constexpr (S == 6) d = __builtin_amdgcn_mfma_f32_16x16x1f32(0.0f, 0.0f, acc, 0, 0, 0);
+    else if constexpr (S == 7) d = __builtin_amdgcn_mfma_f32_32x32x2f32(0.0f, 0.0f, acc, 0, 0, 0);
+    else if constexpr (S == 8) d = __builtin_amdgcn_mfma_f32_16x16x4f32(0.0f, 0.0f, acc, 0, 0, 0);
+    else if constexpr (S == 9) d = __builtin_amdgcn_mfma_f32_4x4x1f32(0.0f, 0.0f, acc, 0, 0, 0);
+    else {
+        const mh8 z = {};
+        d = __builtin_amdgcn_mfma_f32_32x32x16_f16(z, z, acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int v = 0; v < R; ++v) out[64 * v + lane] = d[v];
+}
+
+// The K = 1 f32 instruction's lane layout: with C = 0, a = lane + 1 and b = 1
+// each result names the lane whose a it took (its row); with a = 1 and b =
+// lane + 1, the lane whose b it took (its column). out: 2 x 64 lanes x 32.
+__global__ __launch_bounds__(64) void mfma_layout_kernel(float* out) {
+    const uint32_t lane = threadIdx.x;
+    const mf32 zero = {};
+    const float id = static_cast<float>(lane + 1);
+    const mf32 rows = __builtin_amdgcn_mfma_f32_32x32x1f32(id, 1.0f, zero, 0, 0, 0);
+    const mf32 cols = __builtin_amdgcn_mfma_f32_32x32x1f32(1.0f, id, zero, 0, 0, 0);
+#pragma unroll
+    for (int v = 0; v < 32; ++v) {
+        out[64 * v + lane] = rows[v];
+        out[2048 + 64 * v + lane] = cols[v];
+    }
 }
 
 }  // namespace
@@ -424,7 +534,7 @@ int chx_mfma_rate(int shape, int chains, uint32_t blocks, uint32_t iters, void* 
         case 1: CHX_MFMA(S, 1); break; \
         case 2: CHX_MFMA(S, 2); break; \
         case 4: CHX_MFMA(S, 4); break; \
-        case 8: CHX_MFMA(S, 8); break; \
+        case 8: if (S == 5) return hipErrorInvalidValue; CHX_MFMA(S, 8); break; \
         default: return hipErrorInvalidValue; \
     }
     switch (shape) {
@@ -433,10 +543,50 @@ int chx_mfma_rate(int shape, int chains, uint32_t blocks, uint32_t iters, void* 
         case 2: CHX_SHAPE(2); break;
         case 3: CHX_SHAPE(3); break;
         case 4: CHX_SHAPE(4); break;
+        case 5: CHX_SHAPE(5); break;
+        case 6: CHX_SHAPE(6); break;
+        case 7: CHX_SHAPE(7); break;
+        case 8: CHX_SHAPE(8); break;
         default: return hipErrorInvalidValue;
     }
 #undef CHX_SHAPE
 #undef CHX_MFMA
+    return hipGetLastError();
+}
+
+// mfma_fma_check_kernel over `pairs` pairs (ab: 2 floats a pair; c: 2,048
+// floats a pair), `blocks` one-wave workgroups; out: 2 + 4 x 64 words,
+// cleared here.
+int chx_mfma_fma_check(const void* ab, const void* c, uint32_t pairs, uint32_t blocks, void* out, void* s) {
+    if (pairs == 0 || blocks == 0) return hipErrorInvalidValue;
+    const auto stream = static_cast<hipStream_t>(s);
+    hipError_t e = hipMemsetAsync(out, 0, (2 + 4 * 64) * 4, stream);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(mfma_fma_check_kernel, dim3(blocks), dim3(64), 0, stream, static_cast<const float*>(ab),
+                       static_cast<const float*>(c), pairs, static_cast<uint32_t*>(out));
+    return hipGetLastError();
+}
+
+// mfma_c_probe_kernel<shape>: c and out hold 2,048 floats.
+int chx_mfma_c_probe(int shape, const void* c, void* out, void* s) {
+    const auto stream = static_cast<hipStream_t>(s);
+    const auto* ci = static_cast<const float*>(c);
+    auto* o = static_cast<float*>(out);
+    switch (shape) {
+        case 1: hipLaunchKernelGGL(mfma_c_probe_kernel<1>, dim3(1), dim3(64), 0, stream, ci, o); break;
+        case 5: hipLaunchKernelGGL(mfma_c_probe_kernel<5>, dim3(1), dim3(64), 0, stream, ci, o); break;
+        case 6: hipLaunchKernelGGL(mfma_c_probe_kernel<6>, dim3(1), dim3(64), 0, stream, ci, o); break;
+        case 7: hipLaunchKernelGGL(mfma_c_probe_kernel<7>, dim3(1), dim3(64), 0, stream, ci, o); break;
+        case 8: hipLaunchKernelGGL(mfma_c_probe_kernel<8>, dim3(1), dim3(64), 0, stream, ci, o); break;
+        case 9: hipLaunchKernelGGL(mfma_c_probe_kernel<9>, dim3(1), dim3(64), 0, stream, ci, o); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// mfma_layout_kernel: out holds 2 x 2,048 floats.
+int chx_mfma_layout(void* out, void* s) {
+    hipLaunchKernelGGL(mfma_layout_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(s), static_cast<float*>(out));
     return hipGetLastError();
 }
 

@@ -28,6 +28,7 @@ enum Kernel : uint32_t {
     kGemmSplit = 17,    // prefill split along K, then the ordered combine
     kGemmMfma = 18,     // prefill on the matrix cores, x split into two f16 parts
     kGemmShort = 19,    // prefill of a short step: 16 or 8 rows x 32 tokens, K split among the waves
+    kGemmExact = 20,    // prefill on the matrix cores' K = 1 f32 instruction, the canonical order
 };
 
 struct Plan {
@@ -74,7 +75,12 @@ hipError_t launch_gemm_canonical(const Product& a, uint32_t format, const Plan& 
 void plan_gemm_short(const Product& a, uint32_t compute_units, Plan* plan);
 hipError_t launch_gemm_short(const Product& a, uint32_t format, const Plan& plan, hipStream_t stream);
 
-// Prefill on the matrix cores.
+// Prefill on the matrix cores in the canonical order (gemm_exact.hip):
+// every format, every epilogue, the VALU tile's bits.
+void plan_gemm_exact(const Product& a, uint32_t format, uint32_t compute_units, Plan* plan);
+hipError_t launch_gemm_exact(const Product& a, uint32_t format, const Plan& plan, hipStream_t stream);
+
+// Prefill on the matrix cores, x split into two f16 parts.
 bool mfma_reads(uint32_t format);
 uint64_t mfma_workspace_bytes(uint32_t tokens, uint32_t groups);
 void plan_gemm_mfma(const Product& a, uint32_t format, uint32_t compute_units, Plan* plan);

@@ -47,6 +47,9 @@ _SIGS = {
     "chx_mfma_rate": (_c.c_int, [_c.c_int, _c.c_int, _c.c_uint32, _c.c_uint32, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
     "chx_read_sweep": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_uint32, _c.c_uint32, _c.c_void_p,
                                   _c.c_uint64, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
+    "chx_mfma_fma_check": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_uint32, _c.c_uint32, _c.c_void_p, _c.c_void_p]),
+    "chx_mfma_layout": (_c.c_int, [_c.c_void_p, _c.c_void_p]),
+    "chx_mfma_c_probe": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_void_p, _c.c_void_p]),
 }
 
 
@@ -217,9 +220,28 @@ def read_sweep(form, u, nt, depth, blocks, threads, src_ptr, nbytes, sink_ptr, s
 
 def mfma_rate(shape, chains, blocks, iters, sink_ptr, sink_bytes, stream=None):
     """The matrix-core rate probe (chx_mfma_rate): shape 0 f16 16x16x32, 1 f16 32x32x16, 2 bf16 16x16x32,
-    3 i8 16x16x64, 4 i8 32x32x32; `chains` independent accumulators a wave."""
+    3 i8 16x16x64, 4 i8 32x32x32, 5 f32 32x32x1 (two blocks), 6 f32 16x16x1 (four blocks), 7 f32 32x32x2,
+    8 f32 16x16x4; `chains` independent accumulators a wave (at most 4 for shape 5)."""
     check(lib.chx_mfma_rate(shape, chains, blocks, iters, sink_ptr, sink_bytes,
                             stream.handle if isinstance(stream, Stream) else stream), "mfma rate")
+
+
+def mfma_fma_check(ab_ptr, c_ptr, pairs, blocks, out_ptr, stream=None):
+    """chx_mfma_fma_check: the K = 1 f32 matrix instruction against fmaf, bit for bit; out (2 + 256 words):
+    differing, compared, then (pair, element, instruction bits, fmaf bits) for the first 64 differing."""
+    check(lib.chx_mfma_fma_check(ab_ptr, c_ptr, pairs, blocks, out_ptr,
+                                 stream.handle if isinstance(stream, Stream) else stream), "mfma fma check")
+
+
+def mfma_layout(out_ptr, stream=None):
+    """chx_mfma_layout: 2 x 2,048 floats, the lane (+1) each 32x32x1 result took its a from, then its b."""
+    check(lib.chx_mfma_layout(out_ptr, stream.handle if isinstance(stream, Stream) else stream), "mfma layout")
+
+
+def mfma_c_probe(shape, c_ptr, out_ptr, stream=None):
+    """chx_mfma_c_probe: D of a = b = 0 and C = c (2,048 floats, c[64 v + lane]) written at C's places."""
+    check(lib.chx_mfma_c_probe(shape, c_ptr, out_ptr, stream.handle if isinstance(stream, Stream) else stream),
+          "mfma c probe")
 
 
 def touch(src_ptr, waves, kib, sink_ptr, sink_bytes, stream=None):

@@ -73,15 +73,17 @@ class Rows(enum.IntEnum):
 
 
 class GemmPath(enum.IntEnum):
-    """The prefill kernel: AUTO (the default) and CANONICAL run bit-exact VALU
-    tiles — AUTO takes the short-step tile (GEMM_SHORT) where the 128-row tile
-    would leave compute units idle, CANONICAL always the 128-row tile, the same
-    bits either way; SPLIT_F16_MFMA, only when asked for, the matrix cores within
-    1e-5."""
+    """The prefill kernel: AUTO (the default) and CANONICAL are bit-exact —
+    AUTO takes the short-step tile (GEMM_SHORT) where the 128-row tile would
+    leave compute units idle, CANONICAL always the 128-row tile; EXACT_MFMA runs
+    every step that does not split on the matrix cores' f32 fused multiply-add
+    (GEMM_EXACT), the same bits; SPLIT_F16_MFMA, only when asked for, the matrix
+    cores within 1e-5."""
 
     AUTO = 0
     CANONICAL = 1
     SPLIT_F16_MFMA = 2
+    EXACT_MFMA = 3
 
 
 class Kernel(enum.IntEnum):
@@ -99,6 +101,7 @@ class Kernel(enum.IntEnum):
     GEMM_SPLIT = 17
     GEMM_MFMA = 18
     GEMM_SHORT = 19
+    GEMM_EXACT = 20
 
 
 class GemvPath(enum.IntEnum):

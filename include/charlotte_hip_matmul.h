@@ -114,14 +114,18 @@ typedef enum {
 } charlotte_hip_matmul_rows;
 
 /* Which prefill kernel runs (no counterpart: the reference has one, on WebGPU's
- * shader cores). AUTO, the default, and CANONICAL run VALU tiles in the
+ * shader cores). AUTO, the default, CANONICAL and EXACT_MFMA add in the
  * order above (split along K where the gate and the caller's range sums
  * allow), bit-exact and batch-invariant: a drop-in caller keeps the
- * reference's decode = prefill guarantee whatever workspace it sets. AUTO
- * takes the short-step tile (GEMM_SHORT: 16 or 8 rows by 32 tokens, K split
- * among a workgroup's waves) for a step that does not split and whose
- * 128-row tiles would number fewer than the device's compute units;
- * CANONICAL always takes the 128-row tile. Both give the same bits.
+ * reference's decode = prefill guarantee whatever workspace it sets. For a
+ * step that does not split, AUTO takes the matrix cores' K = 1 f32
+ * instruction (GEMM_EXACT: each range's chain one fused multiply-add a k, as
+ * the VALU tile adds it, on 64-row waves) where the step gives it at least
+ * two waves a compute unit; else the short-step tile (GEMM_SHORT: 16 or 8
+ * rows by 32 tokens, K split among a workgroup's waves) where the 128-row
+ * tiles would number fewer than the compute units; else the 128-row VALU
+ * tile. CANONICAL always takes the 128-row tile; EXACT_MFMA always
+ * GEMM_EXACT. All three give the same bits.
  * SPLIT_F16_MFMA, only when asked for, runs the products on the matrix cores
  * with x split into two f16 parts, within the tolerance max|err| / max|y| <=
  * 1e-5 but not bit-exact and not batch-invariant with decode; it needs a
@@ -129,7 +133,8 @@ typedef enum {
 typedef enum {
     CHARLOTTE_HIP_MATMUL_GEMM_AUTO = 0,
     CHARLOTTE_HIP_MATMUL_GEMM_CANONICAL = 1,
-    CHARLOTTE_HIP_MATMUL_GEMM_SPLIT_F16_MFMA = 2
+    CHARLOTTE_HIP_MATMUL_GEMM_SPLIT_F16_MFMA = 2,
+    CHARLOTTE_HIP_MATMUL_GEMM_EXACT_MFMA = 3
 } charlotte_hip_matmul_gemm_path;
 
 /* Which decode kernel runs (no counterpart: the reference decodes in its one
@@ -306,7 +311,8 @@ typedef enum {
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_TILED = 16,   /* prefill, the VALU tile */
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_SPLIT = 17,   /* prefill split along K, then the ordered combine */
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_MFMA = 18,    /* prefill on the matrix cores (x split into two f16 parts) */
-    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_SHORT = 19    /* prefill of a short step: 16 or 8 rows x 32 tokens, K split in the workgroup */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_SHORT = 19,   /* prefill of a short step: 16 or 8 rows x 32 tokens, K split in the workgroup */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_EXACT = 20    /* prefill on the matrix cores' f32 fused multiply-add, the canonical order */
 } charlotte_hip_matmul_kernel;
 
 /* What a plan is made for: the device's compute units (256 on MI355X) and

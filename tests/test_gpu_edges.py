@@ -23,10 +23,11 @@ D_OFFSET = {Q4_0: 0, Q6_K: 208}  # where a block's fp16 d lies
 WEIGHTS_A_BLOCK = {Q4_0: 32, Q6_K: 256}
 
 
-@pytest.fixture(scope="module", params=["AUTO", "CANONICAL"])
+@pytest.fixture(scope="module", params=["AUTO", "CANONICAL", "EXACT_MFMA"])
 def run(request):
-    """The prefill under AUTO (the short-step tile for these small steps) and
-    CANONICAL (the 128-row tile)."""
+    """The prefill under AUTO (the short-step tile for these small steps),
+    CANONICAL (the 128-row tile) and EXACT_MFMA (the matrix cores' f32 fused
+    multiply-add)."""
     from charlotte_amd import matmul as mm
     from tests.support.gpu import Runner
 

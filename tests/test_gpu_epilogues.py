@@ -21,10 +21,12 @@ pytestmark = pytest.mark.gpu
 SILU, GELU, SIGMOID = 0, 1, 2
 
 
-@pytest.fixture(scope="module", params=["AUTO", "CANONICAL"])
+@pytest.fixture(scope="module", params=["AUTO", "CANONICAL", "EXACT_MFMA"])
 def ctx(request):
-    """Each test twice: under AUTO (the short-step tile where the 128-row tile
-    would leave compute units idle) and CANONICAL (always the 128-row tile)."""
+    """Each test three times: under AUTO (the short-step tile where the 128-row
+    tile would leave compute units idle), CANONICAL (always the 128-row tile)
+    and EXACT_MFMA (every unsplit step on the matrix cores' f32 fused
+    multiply-add)."""
     from charlotte_amd import matmul as mm
 
     c = mm.Context(0)

@@ -1,0 +1,166 @@
+"""The matrix-core prefill in the canonical order (GEMM_EXACT) against the
+128-row VALU tile, bit for bit, at full size.
+
+GEMM_EXACT runs each range's chain on v_mfma_f32_32x32x1_2b_f32, one fused
+multiply-add a k, so its outputs are the VALU tile's bits whatever the
+inputs. The oracle holds both tiles to the reference order at small sizes
+(test_gpu_parity, _formats, _float_formats, _epilogues and _edges run under
+EXACT_MFMA too); here the two tiles meet where the oracle would take too long:
+the BASELINE prefill shapes in full (C4; C5's QKV, gated gate/up and down at
+2,048 tokens), Q6_K products, K past the ranges' count (K = 14,336) and
+below it (K = 64: 30 empty ranges), ragged rows and tokens, every epilogue,
+on both of its tiles (64 tokens a wave for large steps, 32 for the rest).
+The reference's own check of the same property: a token's outputs the same
+whatever the step (tests/gpu/matmul_test.cpp:257-267).
+"""
+
+import numpy as np
+import pytest
+
+from tests.support.oracle_lib import Q4_0, Q6_K
+
+pytestmark = pytest.mark.gpu
+
+Q8_0, Q4_1 = 8, 3
+
+
+@pytest.fixture(scope="module")
+def ctxs():
+    from charlotte_amd import matmul as mm
+
+    exact, tile = mm.Context(0), mm.Context(0)
+    exact.set_gemm_path(mm.GemmPath.EXACT_MFMA)
+    tile.set_gemm_path(mm.GemmPath.CANONICAL)
+    yield exact, tile
+    exact.close()
+    tile.close()
+
+
+def _weight(ctx, gtype, rows, columns, stored):
+    from charlotte_amd import matmul as mm
+
+    return mm.Weight(ctx, gtype, rows, columns, stored)
+
+
+def _both(ctxs, members_of, x, tokens, widths, **kw):
+    """Run the product on both tiles (members_of(ctx) builds its members)."""
+    from tests.support.gpu import Runner
+
+    outs = []
+    for ctx in ctxs:
+        members, weights = members_of(ctx)
+        try:
+            outs.append(Runner(ctx).product(members, x, tokens, widths, **kw))
+        finally:
+            for w in weights:
+                w.free()
+    return outs
+
+
+def _same(got, want, what):
+    from tests.support.gpu import bits_equal, first_difference
+
+    for g, w in zip(got, want):
+        assert not np.isnan(w).all(), f"{what}: nothing written"
+        assert bits_equal(g, w), f"{what}: {first_difference(g, w)}"
+
+
+def _plans(ctx_path, members, tokens):
+    from charlotte_amd import matmul as mm
+
+    return mm.plan_launch(mm.MatmulLaunch(members, 16, [16]), tokens, mm.Target(gemm_path=ctx_path)).kernel
+
+
+@pytest.mark.parametrize("gtype,rows,columns,tokens", [
+    (Q4_0, 8192, 2048, 512),     # C4 in full
+    (Q4_0, 2048, 8192, 2048),    # C5's down projection
+    (Q6_K, 3072, 1152, 300),
+    (Q4_0, 1000, 14336, 65),     # 448 groups: 14 a range
+    (Q4_0, 333, 64, 129),        # 2 groups: 30 empty ranges
+    (Q8_0, 700, 2048, 97),
+    (Q4_1, 520, 1024, 70),
+    (Q6_K, 16384, 1152, 1024),   # 64-token tiles (4,096 waves of 64 x 64)
+    (Q4_0, 16001, 1024, 1001),   # 64-token tiles, ragged rows and tokens
+])
+def test_write_same_bits_as_the_tile(ctxs, gtype, rows, columns, tokens):
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+
+    rng = np.random.default_rng(rows + columns + tokens)
+    stored = synthetic.weight(rng, gtype, rows, columns)
+    x = synthetic.activations(rng, tokens, columns)
+    assert _plans(mm.GemmPath.EXACT_MFMA, [mm.Member(mm.Weight.shape(gtype, rows, columns))], tokens) == \
+        mm.Kernel.GEMM_EXACT
+
+    def members(ctx):
+        w = _weight(ctx, gtype, rows, columns, stored)
+        return [mm.Member(w)], [w]
+
+    got, want = _both(ctxs, members, x, tokens, [rows])
+    _same(got, want, f"type {gtype} {rows}x{columns} tokens={tokens}")
+
+
+def test_c5_qkv_and_gated_gate_up_same_bits(ctxs):
+    """Llama 3.2 1B's fused QKV (2,048 + 512 + 512 rows) and gated gate/up
+    (2 x 8,192 rows, SiLU) at 2,048 tokens."""
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+
+    rng = np.random.default_rng(5)
+    tokens, columns = 2048, 2048
+    x = synthetic.activations(rng, tokens, columns)
+    qkv = [synthetic.weight(rng, Q4_0, r, columns) for r in (2048, 512, 512)]
+
+    def qkv_members(ctx):
+        ws = [_weight(ctx, Q4_0, r, columns, s) for r, s in zip((2048, 512, 512), qkv)]
+        return [mm.Member(w) for w in ws], ws
+
+    got, want = _both(ctxs, qkv_members, x, tokens, [2048, 512, 512], epilogue=mm.Epilogue.QKV)
+    _same(got, want, "qkv")
+    gate, up = (synthetic.weight(rng, Q4_0, 8192, columns) for _ in range(2))
+
+    def gated_members(ctx):
+        ws = [_weight(ctx, Q4_0, 8192, columns, s) for s in (gate, up)]
+        return [mm.Member(w) for w in ws], ws
+
+    got, want = _both(ctxs, gated_members, x, tokens, [8192], epilogue=mm.Epilogue.GatedActivation)
+    _same(got, want, "gated gate/up")
+
+
+@pytest.mark.parametrize("activation", [0, 1, 2])
+def test_every_epilogue_and_option_same_bits(ctxs, activation):
+    """Ragged rows and tokens through GatedActivation (clipped), GatedByInput,
+    a Write with clip, bias and activation, and members placed past row 0."""
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+
+    rng = np.random.default_rng(40 + activation)
+    tokens, columns = 77, 1024
+    x = synthetic.activations(rng, tokens, columns)
+    a_s, b_s = synthetic.weight(rng, Q4_0, 300, columns), synthetic.weight(rng, Q4_0, 300, columns)
+    clip = [-1.5, 1.25, -3.0, 2.5]
+
+    def pair(ctx):
+        ws = [_weight(ctx, Q4_0, 300, columns, s) for s in (a_s, b_s)]
+        return [mm.Member(w) for w in ws], ws
+
+    got, want = _both(ctxs, pair, x, tokens, [300], epilogue=mm.Epilogue.GatedActivation, activation=activation,
+                      clip=clip)
+    _same(got, want, f"gated clipped act={activation}")
+    u = rng.standard_normal((tokens, 500)).astype(np.float32)
+
+    def one(ctx):
+        w = _weight(ctx, Q4_0, 300, columns, a_s)
+        return [mm.Member(w, output_row=100)], [w]
+
+    got, want = _both(ctxs, one, x, tokens, [500], epilogue=mm.Epilogue.GatedByInput, activation=activation,
+                      out_width=500, gate_input=u, gate_input_stride=500, gate_input_column=50)
+    _same(got, want, f"gated by input act={activation}")
+    bias = rng.standard_normal(300).astype(np.float32)
+
+    def opts(ctx):
+        w = _weight(ctx, Q4_0, 300, columns, b_s)
+        return [mm.Member(w)], [w]
+
+    got, want = _both(ctxs, opts, x, tokens, [300], clip=clip, bias=bias, activated=True, activation=activation)
+    _same(got, want, f"write with options act={activation}")

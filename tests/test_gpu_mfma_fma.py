@@ -1,0 +1,118 @@
+"""The matrix-core instruction the canonical-order prefill tile (GEMM_EXACT)
+is built on: v_mfma_f32_32x32x1_2b_f32 is, element by element, one fused
+multiply-add, d = fmaf(a, b, c), bit for bit.
+
+GEMM_EXACT's outputs are the reference order's bits only because of that, so
+the property itself is held here, on the harness's probes (harness.hip):
+mfma_fma_check gives every lane of a wave one a and one b and 2,048
+accumulators c, so every element of the result is c + a b whatever its place,
+and compares each with fmaf on the VALU; mfma_c_probe checks that each
+accumulator comes back in its own place (a = b = 0). Operands: random
+magnitudes over 2^+-20, products cancelling their accumulator, sums on and
+next to halfway points of the accumulator's ulp, denormal operands and
+results, infinities, NaNs and signed zeros, and overflow.
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+PAIRS = 2048
+F32 = np.float32
+
+
+def _classes(rng):
+    n = PAIRS
+
+    def random():
+        a = (rng.standard_normal(n) * 2.0 ** rng.integers(-20, 20, n)).astype(F32)
+        b = (rng.standard_normal(n) * 2.0 ** rng.integers(-20, 20, n)).astype(F32)
+        ab = np.abs(a.astype(np.float64) * b)
+        c = rng.standard_normal((n, 2048)) * ab[:, None] * 2.0 ** rng.integers(-30, 30, (n, 2048))
+        return a, b, c.astype(F32)
+
+    def cancel():
+        a, b = rng.standard_normal(n).astype(F32), rng.standard_normal(n).astype(F32)
+        ab = a.astype(np.float64) * b
+        rel = rng.standard_normal((n, 2048)) * 2.0 ** rng.integers(-30, -1, (n, 2048))
+        return a, b, (-(ab[:, None]) * (1 + rel)).astype(F32)
+
+    def halfway():
+        # a b = (2j + 1) 2^(e - 24 - k), c a 24-bit integer times 2^(e - 23):
+        # the sum on (k = 0) or near a halfway point of c's ulp
+        e = rng.integers(-20, 20, n)
+        j, k = rng.integers(0, 1 << 10, n), rng.integers(0, 3, n)
+        a = ((2 * j + 1) * 2.0 ** (e - 34 - k)).astype(F32)
+        b = np.full(n, 2.0 ** 10, F32)
+        m = rng.integers(1 << 23, 1 << 24, (n, 2048)) * rng.choice([-1.0, 1.0], (n, 2048))
+        return a, b, (m * 2.0 ** (e[:, None] - 23)).astype(F32)
+
+    def denormal():
+        a = (rng.standard_normal(n) * 2.0 ** rng.integers(-80, -60, n)).astype(F32)
+        b = (rng.standard_normal(n) * 2.0 ** rng.integers(-80, -60, n)).astype(F32)
+        c = rng.standard_normal((n, 2048)) * 2.0 ** rng.integers(-150, -120, (n, 2048))
+        return a, b, c.astype(F32)
+
+    def denormal_operand():
+        a = (rng.standard_normal(n) * 2.0 ** rng.integers(-140, -127, n)).astype(F32)
+        b = (rng.standard_normal(n) * 2.0 ** rng.integers(0, 40, n)).astype(F32)
+        ab = np.abs(a.astype(np.float64) * b)
+        c = rng.standard_normal((n, 2048)) * ab[:, None] * 2.0 ** rng.integers(-10, 10, (n, 2048))
+        return a, b, c.astype(F32)
+
+    def special():
+        vals = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1.0, -1.0, 3.4e38, -3.4e38, 1e-45, -1e-45,
+                         1.17549435e-38], F32)
+        return rng.choice(vals, n).astype(F32), rng.choice(vals, n).astype(F32), rng.choice(vals, (n, 2048))
+
+    def overflow():
+        a = (rng.standard_normal(n) * 2.0 ** rng.integers(60, 64, n)).astype(F32)
+        b = (rng.standard_normal(n) * 2.0 ** rng.integers(60, 64, n)).astype(F32)
+        c = rng.standard_normal((n, 2048)) * 2.0 ** rng.integers(110, 125, (n, 2048))
+        return a, b, c.astype(F32)
+
+    return {"random": random, "cancel": cancel, "halfway": halfway, "denormal": denormal,
+            "denormal_operand": denormal_operand, "special": special, "overflow": overflow}
+
+
+@pytest.mark.parametrize("name", ["random", "cancel", "halfway", "denormal", "denormal_operand", "special",
+                                  "overflow"])
+def test_k1_f32_instruction_is_fmaf_bit_for_bit(name):
+    from charlotte_amd import harness as hx
+
+    a, b, c = _classes(np.random.default_rng(sum(map(ord, name))))[name]()
+    ab = hx.Buffer.of(np.stack([a, b], 1).astype(F32).ravel())
+    cb = hx.Buffer.of(np.ascontiguousarray(c, F32).ravel())
+    out = hx.Buffer(nbytes=(2 + 256) * 4)
+    s = hx.Stream()
+    try:
+        hx.mfma_fma_check(ab.ptr, cb.ptr, PAIRS, 1024, out.ptr, s)
+        s.sync()
+        o = out.read(np.uint32)
+        assert o[1] == PAIRS * 2048, "every element compared"
+        assert o[0] == 0, f"{name}: {o[0]} of {o[1]} differ; first (pair, element, mfma, fmaf): {o[2:6].tolist()}"
+    finally:
+        for buf in (ab, cb, out):
+            buf.free()
+        s.destroy()
+
+
+@pytest.mark.parametrize("shape,registers", [(5, 32), (6, 16), (7, 16), (8, 4), (9, 4), (1, 16)])
+def test_accumulators_come_back_in_their_places(shape, registers):
+    """a = b = 0: D = C, each accumulator in its own register and lane (the
+    f32 K = 1, 2 and 4 shapes, and the f16 32 x 32 x 16 one)."""
+    from charlotte_amd import harness as hx
+
+    ids = (np.arange(2048) + 1).astype(F32)
+    cb, ob = hx.Buffer.of(ids), hx.Buffer(nbytes=2048 * 4)
+    s = hx.Stream()
+    try:
+        hx.mfma_c_probe(shape, cb.ptr, ob.ptr, s)
+        s.sync()
+        got = ob.read(np.float32)[: 64 * registers]
+        assert (got == ids[: 64 * registers]).all()
+    finally:
+        cb.free()
+        ob.free()
+        s.destroy()

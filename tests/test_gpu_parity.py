@@ -27,10 +27,12 @@ WIDEST = 3072
 THREADS = max(1, min(16, os.cpu_count() or 1))
 
 
-@pytest.fixture(scope="module", params=["AUTO", "CANONICAL"])
+@pytest.fixture(scope="module", params=["AUTO", "CANONICAL", "EXACT_MFMA"])
 def ctx(request):
-    """Each test twice: under AUTO (the short-step tile where the 128-row tile
-    would leave compute units idle) and CANONICAL (always the 128-row tile)."""
+    """Each test three times: under AUTO (the short-step tile where the 128-row
+    tile would leave compute units idle), CANONICAL (always the 128-row tile)
+    and EXACT_MFMA (every unsplit step on the matrix cores' f32 fused
+    multiply-add)."""
     from charlotte_amd import matmul as mm
 
     c = mm.Context(0)

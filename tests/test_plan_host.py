@@ -241,13 +241,19 @@ def test_last_token_decodes_whatever_the_step(shapes):
     assert p.kernel == K.GEMV_STREAM8 and p.rows == 1
 
 
-def test_c4_prefill_is_the_bit_exact_tile_under_auto_with_or_without_a_workspace(shapes):
+def test_c4_prefill_is_a_bit_exact_tile_under_auto_with_or_without_a_workspace(shapes):
+    """C4 under AUTO: the matrix cores' fused multiply-add tile (1,024 waves of
+    64 x 64, the canonical order) whatever workspace is set; CANONICAL: the
+    128-row VALU tile."""
     w = shapes(Q4_0, 8192, 2048)
     room = mm.workspace_bytes(512, 2048)
-    for target in (MI355X, mm.Target(256, workspace_bytes=room), mm.Target(256, mm.GemmPath.CANONICAL, workspace_bytes=room)):
+    for target in (MI355X, mm.Target(256, workspace_bytes=room)):
         p = mm.plan_launch(_write(w), 512, target)
-        assert (p.kernel, p.canonical, p.tile_tokens, p.tile_rows) == (K.GEMM_TILED, True, 64, 128), target
-        assert p.tiles == 8 * 64
+        assert (p.kernel, p.canonical, p.tile_tokens, p.tile_rows) == (K.GEMM_EXACT, True, 64, 256), target
+        assert p.tiles == 8 * 32
+    p = mm.plan_launch(_write(w), 512, mm.Target(256, mm.GemmPath.CANONICAL, workspace_bytes=room))
+    assert (p.kernel, p.canonical, p.tile_tokens, p.tile_rows) == (K.GEMM_TILED, True, 64, 128)
+    assert p.tiles == 8 * 64
     mfma = mm.plan_launch(_write(w), 512, mm.Target(256, mm.GemmPath.SPLIT_F16_MFMA, workspace_bytes=room))
     assert mfma.kernel == K.GEMM_MFMA and not mfma.canonical and mfma.launches == 2
     assert "workspace" in _refused(_write(w), 512, target=mm.Target(256, mm.GemmPath.SPLIT_F16_MFMA, workspace_bytes=room - 1))
@@ -289,10 +295,48 @@ def test_short_steps_that_do_not_split_take_the_short_tile_while_the_128_row_til
     p = mm.plan_launch(g, 32)
     assert (p.kernel, p.tile_rows, p.workgroups) == (K.GEMM_SHORT, 16, 1024)
     assert mm.plan_launch(g, 32, mm.Target(256, mm.GemmPath.CANONICAL)).kernel == K.GEMM_TILED
-    assert mm.plan_launch(_write(gate), 512).kernel == K.GEMM_TILED
+    assert mm.plan_launch(_write(gate), 512).kernel == K.GEMM_EXACT
     # 100 tokens over 2,048 rows: 32 tiles of 128 rows; short tiles of 16 rows, 4 x 128 workgroups.
     p = mm.plan_launch(_write(down), 100)
     assert (p.kernel, p.tiles, p.tile_rows) == (K.GEMM_SHORT, 4 * 128, 16)
+
+
+def test_auto_takes_the_exact_matrix_core_tile_from_two_waves_a_compute_unit(shapes):
+    """AUTO: GEMM_EXACT where its waves (64 rows by 64 or 32 tokens) number at
+    least 2 x the compute units, else the short-step tile: 2,048 x 2,048 at
+    512 tokens is 512 waves of 64 x 32, at 256 tokens 256 (the measured
+    crossing: 98 against 130 us at 512, 97 against 67 at 256)."""
+    w = shapes(Q4_0, 2048, 2048)
+    assert mm.plan_launch(_write(w), 512).kernel == K.GEMM_EXACT
+    assert mm.plan_launch(_write(w), 256).kernel == K.GEMM_SHORT
+    assert mm.plan_launch(_write(w), 1024).kernel == K.GEMM_EXACT
+    assert mm.plan_launch(_write(w), 512, mm.Target(128)).kernel == K.GEMM_EXACT  # 2 x 128 CUs: 256 waves
+    assert mm.plan_launch(_write(w), 256, mm.Target(128)).kernel == K.GEMM_EXACT
+
+
+def test_exact_mfma_path_takes_every_unsplit_prefill_step(shapes):
+    """EXACT_MFMA: every prefill step the gate does not split runs on the matrix
+    cores' f32 fused multiply-add (GEMM_EXACT, the canonical order): tiles of
+    256 rows by 64 tokens where waves of 64 x 64 give each of the 1,024 SIMDs
+    one, else by 32 tokens; decode and the split are unchanged."""
+    w = shapes(Q4_0, 2048, 8192)
+    exact = mm.Target(256, mm.GemmPath.EXACT_MFMA)
+    for tokens in (2, 31, 32, 64, 511, 2048, 4096):
+        p = mm.plan_launch(_write(w), tokens, exact)
+        tt = 64 if 32 * -(-tokens // 64) >= 1024 else 32
+        assert (p.kernel, p.canonical, p.launches, p.tile_rows, p.tile_tokens) == (K.GEMM_EXACT, True, 1, 256, tt)
+        assert p.workgroups == 8 * -(-tokens // tt)
+    big = shapes(Q4_0, 16384, 2048)
+    assert mm.plan_launch(_write(big), 2048, exact).tile_tokens == 64  # C5's gate/up: 8,192 waves of 64 x 64
+    assert mm.plan_launch(_write(shapes(Q4_0, 8192, 2048)), 512, exact).tile_tokens == 64  # C4: 1,024 of them
+    assert mm.plan_launch(_write(shapes(Q4_0, 4096, 2048)), 512, exact).tile_tokens == 32  # 512 of them
+    assert mm.plan_launch(_write(w), 1, exact).kernel == mm.plan_launch(_write(w), 1).kernel == K.GEMV_RANGES
+    sums = 4 * mm.range_sum_floats(mm.Epilogue.Write, 2048, 8192, mm.kSplitGate)
+    assert mm.plan_launch(_write(w), 32, exact, gate=mm.kSplitGate, range_sums_bytes=sums).kernel == K.GEMM_SPLIT
+    g = mm.MatmulLaunch([mm.Member(w), mm.Member(w)], X, [Y0], epilogue=mm.Epilogue.GatedActivation)
+    assert mm.plan_launch(g, 32, exact).kernel == K.GEMM_EXACT
+    f = shapes(F16, 300, 1024)
+    assert mm.plan_launch(_write(f), 70, exact).kernel == K.GEMM_EXACT
 
 
 # ---- row_divisor (interface.h:270-279, 292; program.cpp:382-387) -------------------
