@@ -275,6 +275,51 @@ __global__ __launch_bounds__(64) void mfma_fma_check_kernel(const float* ab, con
     atomicAdd(out + 1, compared);
 }
 
+// The K = 2 and K = 4 f32 shapes (32x32x2: lane l supplies k = l / 32; 16x16x4:
+// k = l / 16) against fmaf in k order: pair p gives a[k] and b[k] to the
+// lanes of its k, so every element is c + a0 b0 + a1 b1 (+ ...) whatever its
+// place; each lane compares its results with fmaf(a1, b1, fmaf(a0, b0, c))
+// (and so on) bit for bit. ab: 2 K floats a pair (a0 b0 a1 b1 ...); c: 64 R
+// floats a pair. out as mfma_fma_check's.
+template <int K>
+__global__ __launch_bounds__(64) void mfma_chain_check_kernel(const float* ab, const float* c, uint32_t pairs,
+                                                              uint32_t* out) {
+    constexpr int R = K == 2 ? 16 : 4;
+    using Acc = std::conditional_t<R == 16, mf16, mf4>;
+    const uint32_t lane = threadIdx.x;
+    uint32_t compared = 0;
+    for (uint32_t p = blockIdx.x; p < pairs; p += gridDim.x) {
+        const float* q = ab + static_cast<uint64_t>(p) * 2 * K;
+        const uint32_t my_k = K == 2 ? lane / 32 : lane / 16;
+        const float a = q[2 * my_k], b = q[2 * my_k + 1];
+        Acc acc;
+#pragma unroll
+        for (int v = 0; v < R; ++v) acc[v] = c[static_cast<uint64_t>(p) * 64 * R + 64 * v + lane];
+        Acc d;
+        if constexpr (K == 2) d = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
+        else d = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < R; ++v) {
+            const float dv = d[v];
+            float r = acc[v];
+#pragma unroll
+            for (int k = 0; k < K; ++k) r = __builtin_fmaf(q[2 * k], q[2 * k + 1], r);
+            const uint32_t rb = __builtin_bit_cast(uint32_t, r), db = __builtin_bit_cast(uint32_t, dv);
+            ++compared;
+            if (!(rb == db || (r != r && dv != dv))) {
+                const uint32_t at = atomicAdd(out, 1u);
+                if (at < 64) {
+                    out[2 + 4 * at] = p;
+                    out[3 + 4 * at] = 64 * v + lane;
+                    out[4 + 4 * at] = db;
+                    out[5 + 4 * at] = rb;
+                }
+            }
+        }
+    }
+    atomicAdd(out + 1, compared);
+}
+
 // Where a shape puts each accumulator it is given: a = b = 0 and C read from
 // c[64 v + lane] (v < the shape's registers), D written to out at the same
 // places, so out = c where the instruction adds C element by element in its
@@ -581,6 +626,24 @@ int chx_mfma_c_probe(int shape, const void* c, void* out, void* s) {
         case 9: hipLaunchKernelGGL(mfma_c_probe_kernel<9>, dim3(1), dim3(64), 0, stream, ci, o); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+// mfma_chain_check_kernel<k> (k = 2 or 4) over `pairs`: ab 2 k floats a
+// pair, c 1,024 (k = 2) or 256 (k = 4) floats a pair; out as
+// chx_mfma_fma_check's, cleared here.
+int chx_mfma_chain_check(int k, const void* ab, const void* c, uint32_t pairs, uint32_t blocks, void* out, void* s) {
+    if (pairs == 0 || blocks == 0 || (k != 2 && k != 4)) return hipErrorInvalidValue;
+    const auto stream = static_cast<hipStream_t>(s);
+    hipError_t e = hipMemsetAsync(out, 0, (2 + 4 * 64) * 4, stream);
+    if (e != hipSuccess) return e;
+    const auto* abf = static_cast<const float*>(ab);
+    const auto* cf = static_cast<const float*>(c);
+    auto* o = static_cast<uint32_t*>(out);
+    if (k == 2)
+        hipLaunchKernelGGL(mfma_chain_check_kernel<2>, dim3(blocks), dim3(64), 0, stream, abf, cf, pairs, o);
+    else
+        hipLaunchKernelGGL(mfma_chain_check_kernel<4>, dim3(blocks), dim3(64), 0, stream, abf, cf, pairs, o);
     return hipGetLastError();
 }
 

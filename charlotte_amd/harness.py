@@ -50,6 +50,8 @@ _SIGS = {
     "chx_mfma_fma_check": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_uint32, _c.c_uint32, _c.c_void_p, _c.c_void_p]),
     "chx_mfma_layout": (_c.c_int, [_c.c_void_p, _c.c_void_p]),
     "chx_mfma_c_probe": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_void_p, _c.c_void_p]),
+    "chx_mfma_chain_check": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_void_p, _c.c_uint32, _c.c_uint32, _c.c_void_p,
+                                        _c.c_void_p]),
 }
 
 
@@ -231,6 +233,13 @@ def mfma_fma_check(ab_ptr, c_ptr, pairs, blocks, out_ptr, stream=None):
     differing, compared, then (pair, element, instruction bits, fmaf bits) for the first 64 differing."""
     check(lib.chx_mfma_fma_check(ab_ptr, c_ptr, pairs, blocks, out_ptr,
                                  stream.handle if isinstance(stream, Stream) else stream), "mfma fma check")
+
+
+def mfma_chain_check(k, ab_ptr, c_ptr, pairs, blocks, out_ptr, stream=None):
+    """chx_mfma_chain_check: the K = 2 (32x32x2) or K = 4 (16x16x4) f32 shape against fmaf in k order;
+    ab 2 k floats a pair, c 1,024 (k = 2) or 256 (k = 4) a pair; out as mfma_fma_check's."""
+    check(lib.chx_mfma_chain_check(k, ab_ptr, c_ptr, pairs, blocks, out_ptr,
+                                   stream.handle if isinstance(stream, Stream) else stream), "mfma chain check")
 
 
 def mfma_layout(out_ptr, stream=None):

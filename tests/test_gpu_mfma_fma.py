@@ -11,12 +11,16 @@ accumulator comes back in its own place (a = b = 0). Operands: random
 magnitudes over 2^+-20, products cancelling their accumulator, sums on and
 next to halfway points of the accumulator's ulp, denormal operands and
 results, infinities, NaNs and signed zeros, and overflow.
+
+The K = 2 and K = 4 f32 shapes (32x32x2, 16x16x4) against fmaf applied in k
+order (mfma_chain_check), on operands whose two products nearly cancel with a
+small accumulator: there the sequential sum and a once-rounded one differ for
+most elements (counted exactly on the CPU below), so agreement shows the
+instruction rounds after each product.
 """
 
 import numpy as np
 import pytest
-
-pytestmark = pytest.mark.gpu
 
 PAIRS = 2048
 F32 = np.float32
@@ -76,6 +80,7 @@ def _classes(rng):
             "denormal_operand": denormal_operand, "special": special, "overflow": overflow}
 
 
+@pytest.mark.gpu
 @pytest.mark.parametrize("name", ["random", "cancel", "halfway", "denormal", "denormal_operand", "special",
                                   "overflow"])
 def test_k1_f32_instruction_is_fmaf_bit_for_bit(name):
@@ -98,6 +103,7 @@ def test_k1_f32_instruction_is_fmaf_bit_for_bit(name):
         s.destroy()
 
 
+@pytest.mark.gpu
 @pytest.mark.parametrize("shape,registers", [(5, 32), (6, 16), (7, 16), (8, 4), (9, 4), (1, 16)])
 def test_accumulators_come_back_in_their_places(shape, registers):
     """a = b = 0: D = C, each accumulator in its own register and lane (the
@@ -115,4 +121,77 @@ def test_accumulators_come_back_in_their_places(shape, registers):
     finally:
         cb.free()
         ob.free()
+        s.destroy()
+
+
+def _mixed(rng, n, k, registers):
+    """k products a pair, the second cancelling the first to its rounding, and
+    small accumulators: c + a0 b0 rounded, then + a1 b1, is far from the once-
+    rounded sum for most elements."""
+    a = (rng.standard_normal((n, k)) * 2.0 ** rng.integers(-10, 10, (n, k))).astype(F32)
+    b = (rng.standard_normal((n, k)) * 2.0 ** rng.integers(-10, 10, (n, k))).astype(F32)
+    b[:, 1] = (-(a[:, 0].astype(np.float64) * b[:, 0]) / a[:, 1]).astype(F32)
+    c = (rng.standard_normal((n, 64 * registers)) * 2.0 ** rng.integers(-30, 0, (n, 64 * registers))).astype(F32)
+    return a, b, c
+
+
+def _round_f32(x):
+    """A Fraction to the nearest binary32, ties to even (finite, normal range)."""
+    from fractions import Fraction
+
+    f = np.float32(float(x))
+    cands = [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+    return min(cands, key=lambda v: (abs(Fraction(float(v)) - x), int(np.array([v]).view(np.uint32)[0]) & 1))
+
+
+def test_mixed_operands_tell_sequential_from_once_rounded_sums():
+    """On the CPU, exactly: the mixed operands separate the two semantics, so
+    the GPU check below can tell them apart."""
+    from fractions import Fraction as Fr
+
+    a, b, c = _mixed(np.random.default_rng(3), 200, 2, 1)
+    differ = total = 0
+    for p in range(200):
+        for e in range(4):
+            p0, p1 = Fr(float(a[p, 0])) * Fr(float(b[p, 0])), Fr(float(a[p, 1])) * Fr(float(b[p, 1]))
+            seq = _round_f32(p1 + Fr(float(_round_f32(p0 + Fr(float(c[p, e]))))))
+            once = _round_f32(p0 + p1 + Fr(float(c[p, e])))
+            differ += int(seq != once)
+            total += 1
+    assert differ > total // 2, f"{differ} of {total}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k,registers", [(2, 16), (4, 4)])
+@pytest.mark.parametrize("kind", ["random", "cancel", "mixed"])
+def test_k2_and_k4_f32_instructions_are_fmaf_in_k_order(k, registers, kind):
+    from charlotte_amd import harness as hx
+
+    rng = np.random.default_rng(10 * k + len(kind))
+    n = PAIRS
+    if kind == "mixed":
+        a, b, c = _mixed(rng, n, k, registers)
+    else:
+        a = (rng.standard_normal((n, k)) * 2.0 ** rng.integers(-10, 10, (n, k))).astype(F32)
+        b = (rng.standard_normal((n, k)) * 2.0 ** rng.integers(-10, 10, (n, k))).astype(F32)
+        if kind == "random":
+            c = rng.standard_normal((n, 64 * registers)) * 2.0 ** rng.integers(-20, 20, (n, 64 * registers))
+        else:
+            ab = (a.astype(np.float64) * b).sum(1)
+            rel = rng.standard_normal((n, 64 * registers)) * 2.0 ** rng.integers(-30, -1, (n, 64 * registers))
+            c = -(ab[:, None]) * (1 + rel)
+        c = c.astype(F32)
+    abuf = hx.Buffer.of(np.stack([a, b], 2).astype(F32).ravel())
+    cbuf = hx.Buffer.of(np.ascontiguousarray(c, F32).ravel())
+    out = hx.Buffer(nbytes=(2 + 256) * 4)
+    s = hx.Stream()
+    try:
+        hx.mfma_chain_check(k, abuf.ptr, cbuf.ptr, n, 1024, out.ptr, s)
+        s.sync()
+        o = out.read(np.uint32)
+        assert o[1] == n * 64 * registers
+        assert o[0] == 0, f"K={k} {kind}: {o[0]} of {o[1]} differ; first: {o[2:6].tolist()}"
+    finally:
+        for buf in (abuf, cbuf, out):
+            buf.free()
         s.destroy()
