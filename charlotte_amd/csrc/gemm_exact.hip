@@ -41,28 +41,59 @@ typedef float f32x32 __attribute__((ext_vector_type(32)));
 constexpr uint32_t kWaveRows = 64;   // rows a wave
 constexpr uint32_t kWaves = 4;       // waves a workgroup, each its own 64 rows
 
-// The 32 exact weights of a group as loaded (the arithmetic of formats.hpp's
-// weight(), which the VALU tile stages: the same values).
+// Four weights from four code bytes as the decodes' chain4 makes them: two
+// codes a v_perm_b32 as binary16 1024 + b, then one v_fma_mix_f32 a weight,
+// fma(1024 + b, scale, offset) — one rounding of a value f32 holds exactly.
+__device__ __forceinline__ void weights4(uint32_t codes, float scale, float offset, float* w) {
+    const half2_t a = lift(codes, kLowPair), b = lift(codes, kHighPair);
+    w[0] = __builtin_fmaf(static_cast<float>(a.x), scale, offset);
+    w[1] = __builtin_fmaf(static_cast<float>(a.y), scale, offset);
+    w[2] = __builtin_fmaf(static_cast<float>(b.x), scale, offset);
+    w[3] = __builtin_fmaf(static_cast<float>(b.y), scale, offset);
+}
+
+// The 32 exact weights of a group as loaded: the values of formats.hpp's
+// weight(), which the VALU tile stages. Q4_0, Q8_0 and Q6_K by the lift of
+// decode.hpp's chain_q4_0, chain_q8_0 and chain_q6_k (1.75 instructions a
+// weight against weight()'s 3: C4 105 -> 111 TFLOP/s), the others by weight().
 template <uint32_t F>
 __device__ __forceinline__ void weights_of(const Raw<F>& r, float* w) {
     if constexpr (F == kQ4_0) {
-        const Q4_0Group g = group_of(Q4_0Bytes{make_uint4(r.w[0], r.w[1], r.w[2], r.w[3]), r.d});
+        // (1024 + q) d - 1032 d; high nibbles as bytes 16 q: (1024 + 16 q) (d / 16) - 72 d
+        const float d = half_to_float(r.d);
+        const float low_offset = -1032.0f * d, d16 = d * 0.0625f, high_offset = -72.0f * d;
 #pragma unroll
-        for (int l = 0; l < 32; ++l) w[l] = weight(g, l);
+        for (int c = 0; c < 4; ++c) {
+            weights4(r.w[c] & 0x0F0F0F0Fu, d, low_offset, w + 4 * c);
+            weights4(r.w[c] & 0xF0F0F0F0u, d16, high_offset, w + 16 + 4 * c);
+        }
     } else if constexpr (F == kQ4_1) {
         const Q4_1Group g = group_of(Q4_1Bytes{make_uint4(r.w[0], r.w[1], r.w[2], r.w[3]), r.dm});
 #pragma unroll
         for (int l = 0; l < 32; ++l) w[l] = weight(g, l);
     } else if constexpr (F == kQ8_0) {
-        const Q8_0Group g = group_of(Q8_0Bytes{make_uint4(r.w[0], r.w[1], r.w[2], r.w[3]),
-                                               make_uint4(r.w[4], r.w[5], r.w[6], r.w[7]), r.d});
+        // q + 128 (the sign bit flipped) lifted: fma(1152 + q, d, -1152 d) = q d
+        const float d = half_to_float(r.d), offset = -1152.0f * d;
 #pragma unroll
-        for (int l = 0; l < 32; ++l) w[l] = weight(g, l);
+        for (int c = 0; c < 8; ++c) weights4(r.w[c] ^ 0x80808080u, d, offset, w + 4 * c);
     } else if constexpr (F == kQ6_K) {
-        const Q6_KGroup g = group_of(
-            Q6_KBytes{make_uint4(r.lo[0], r.lo[1], r.lo[2], r.lo[3]), make_uint2(r.hi[0], r.hi[1]), r.sc, r.d});
-#pragma unroll
-        for (int l = 0; l < 32; ++l) w[l] = weight(g, l);
+        // the 6-bit codes assembled as chain_q6_k assembles them, then
+        // fma(1024 + q, scale, -1056 scale) = (q - 32) scale
+        const float d = half_to_float(r.d);
+        const float first = d * static_cast<float>(static_cast<int8_t>(r.sc & 0xFFu));
+        const float second = d * static_cast<float>(static_cast<int8_t>((r.sc >> 8) & 0xFFu));
+        const float first_offset = -1056.0f * first, second_offset = -1056.0f * second;
+        const uint32_t a0 = r.hi[0] & 0x33333333u, a1 = r.hi[1] & 0x33333333u;
+        const uint32_t b0 = (r.hi[0] >> 2) & 0x33333333u, b1 = (r.hi[1] >> 2) & 0x33333333u;
+        constexpr uint32_t kNib = 0x0F0F0F0Fu;
+        weights4(bitfield_insert(kNib, r.lo[0], a0 << 4), first, first_offset, w + 0);
+        weights4(bitfield_insert(kNib, r.lo[1], a1 << 4), first, first_offset, w + 4);
+        weights4(bitfield_insert(kNib, r.lo[2], b0 << 4), first, first_offset, w + 8);
+        weights4(bitfield_insert(kNib, r.lo[3], b1 << 4), first, first_offset, w + 12);
+        weights4(bitfield_insert(kNib, r.lo[0] >> 4, a0), second, second_offset, w + 16);
+        weights4(bitfield_insert(kNib, r.lo[1] >> 4, a1), second, second_offset, w + 20);
+        weights4(bitfield_insert(kNib, r.lo[2] >> 4, b0), second, second_offset, w + 24);
+        weights4(bitfield_insert(kNib, r.lo[3] >> 4, b1), second, second_offset, w + 28);
     } else if constexpr (F == kF32) {
 #pragma unroll
         for (int l = 0; l < 32; ++l) w[l] = __uint_as_float(r.w[l]);
