@@ -264,17 +264,23 @@ void go_exact(const Product& a, const Plan& plan, hipStream_t stream) {
 
 }  // namespace
 
-// Tiles of 256 rows (four waves of 64) by 64 tokens where that gives every
-// SIMD (4 a compute unit) a wave, else by 32 (F32 always by 32: its 32 dwords
-// a group beside 64 tokens' sums would not fit two waves' registers); token
-// tile first, so the tiles reading one row tile's weights run together. One
-// wave of 64 x 64 a SIMD (two chains of products) measured faster than two
-// of 64 x 32 (one chain each): C4 98.6 against 93.4 TFLOP/s.
+// Tiles of 256 rows (four waves of 64) by 64 or 32 tokens, token tile first,
+// so the tiles reading one row tile's weights run together. A wave's time is
+// its walk through K, and a SIMD's waves share its matrix core, so a step
+// takes as many rounds as its most loaded SIMD holds waves: 64 x 64 waves
+// where they give no more rounds than 64 x 32 waves give half-length ones
+// (one wave of 64 x 64 a SIMD, two chains of products, measured faster than
+// two of 64 x 32, one chain each: C4 98.6 against 93.4 TFLOP/s), else 64 x
+// 32 — Llama 3.2 1B's QKV at 2,048 tokens: 1,536 waves of 64 x 64 on 1,024
+// SIMDs are two rounds, 3,072 of 64 x 32 one and a half. F32 always by 32 (its
+// 32 dwords a group beside 64 tokens' sums would not fit two waves' registers).
 void plan_gemm_exact(const Product& a, uint32_t format, uint32_t compute_units, Plan* plan) {
     *plan = Plan{};
     const uint64_t wave_rows = (a.rows + kWaveRows - 1) / kWaveRows;
-    const uint32_t tt =
-        format != kF32 && wave_rows * ((a.tokens + 63) / 64) >= 4ull * compute_units ? 64 : 32;
+    const uint64_t simds = 4ull * compute_units;
+    const uint64_t rounds64 = (wave_rows * ((a.tokens + 63) / 64) + simds - 1) / simds;
+    const uint64_t rounds32 = (wave_rows * ((a.tokens + 31) / 32) + simds - 1) / simds;  // half-length rounds
+    const uint32_t tt = format != kF32 && rounds32 >= 2 * rounds64 ? 64 : 32;
     plan->kernel = kGemmExact;
     plan->launches = 1;
     plan->tile_tokens = tt;

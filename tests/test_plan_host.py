@@ -317,19 +317,24 @@ def test_auto_takes_the_exact_matrix_core_tile_from_two_waves_a_compute_unit(sha
 def test_exact_mfma_path_takes_every_unsplit_prefill_step(shapes):
     """EXACT_MFMA: every prefill step the gate does not split runs on the matrix
     cores' f32 fused multiply-add (GEMM_EXACT, the canonical order): tiles of
-    256 rows by 64 tokens where waves of 64 x 64 give each of the 1,024 SIMDs
-    one, else by 32 tokens; decode and the split are unchanged."""
+    256 rows by 64 tokens where 64 x 64 waves take no more rounds of the 1,024
+    SIMDs than 64 x 32 waves take half-length rounds, else by 32 tokens; decode
+    and the split are unchanged."""
     w = shapes(Q4_0, 2048, 8192)
     exact = mm.Target(256, mm.GemmPath.EXACT_MFMA)
     for tokens in (2, 31, 32, 64, 511, 2048, 4096):
         p = mm.plan_launch(_write(w), tokens, exact)
-        tt = 64 if 32 * -(-tokens // 64) >= 1024 else 32
+        rounds64, rounds32 = -(-32 * -(-tokens // 64) // 1024), -(-32 * -(-tokens // 32) // 1024)
+        tt = 64 if rounds32 >= 2 * rounds64 else 32
         assert (p.kernel, p.canonical, p.launches, p.tile_rows, p.tile_tokens) == (K.GEMM_EXACT, True, 1, 256, tt)
         assert p.workgroups == 8 * -(-tokens // tt)
     big = shapes(Q4_0, 16384, 2048)
     assert mm.plan_launch(_write(big), 2048, exact).tile_tokens == 64  # C5's gate/up: 8,192 waves of 64 x 64
     assert mm.plan_launch(_write(shapes(Q4_0, 8192, 2048)), 512, exact).tile_tokens == 64  # C4: 1,024 of them
     assert mm.plan_launch(_write(shapes(Q4_0, 4096, 2048)), 512, exact).tile_tokens == 32  # 512 of them
+    # Llama 3.2 1B's QKV (3,072 rows) at 2,048 tokens: 1,536 waves of 64 x 64 are two rounds, 3,072 of 64 x 32 three
+    # half-length ones
+    assert mm.plan_launch(_write(shapes(Q4_0, 3072, 2048)), 2048, exact).tile_tokens == 32
     assert mm.plan_launch(_write(w), 1, exact).kernel == mm.plan_launch(_write(w), 1).kernel == K.GEMV_RANGES
     sums = 4 * mm.range_sum_floats(mm.Epilogue.Write, 2048, 8192, mm.kSplitGate)
     assert mm.plan_launch(_write(w), 32, exact, gate=mm.kSplitGate, range_sums_bytes=sums).kernel == K.GEMM_SPLIT
