@@ -262,9 +262,15 @@ Verdict plan_product(const chm::Product& a, uint32_t format, const Target& t, ch
         split = a.tokens <= most;
     }
     chm::plan_gemm_canonical(a, t.compute_units, split, plan);
-    if (split || t.gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_CANONICAL) return {};
+    if (t.gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_CANONICAL) return {};
+    if (split) {
+        // the split on the matrix cores' fused multiply-add: the same range
+        // sums, the same combine
+        chm::plan_gemm_exact(a, format, t.compute_units, true, plan);
+        return {};
+    }
     chm::Plan exact;
-    chm::plan_gemm_exact(a, format, t.compute_units, &exact);
+    chm::plan_gemm_exact(a, format, t.compute_units, false, &exact);
     // AUTO: the matrix cores' fused multiply-add tile where the step gives it
     // at least two waves a compute unit (below that each of its waves' walk
     // through K is the step's time: measured slower than the short-step tile
@@ -540,7 +546,8 @@ static Status run_plan(charlotte_hip_matmul_context* ctx, const chm::Product& a,
         case chm::kGemmMfma: e = chm::launch_gemm_mfma(a, format, plan, ctx->workspace, s); break;
         case chm::kGemmTiled: e = chm::launch_gemm_canonical(a, format, plan, nullptr, s); break;
         case chm::kGemmShort: e = chm::launch_gemm_short(a, format, plan, s); break;
-        case chm::kGemmExact: e = chm::launch_gemm_exact(a, format, plan, s); break;
+        case chm::kGemmExact: e = chm::launch_gemm_exact(a, format, plan, nullptr, s); break;
+        case chm::kGemmExactSplit: e = chm::launch_gemm_exact(a, format, plan, range_sums, s); break;
         case chm::kGemmSplit: e = chm::launch_gemm_canonical(a, format, plan, range_sums, s); break;
         default: e = chm::launch_gemv(a, format, plan, ctx->compute_units, s); break;
     }
@@ -563,7 +570,8 @@ charlotte_hip_matmul_status charlotte_hip_matmul_launch(charlotte_hip_matmul_con
     chm::Plan plan;
     if (v.ok()) v = plan_product(a, format, target_of(ctx), gate, range_sums ? range_sums_bytes : 0, &plan);
     if (!v.ok()) return fail(ctx, v.status, v.message);
-    if (plan.kernel == chm::kGemmSplit && reinterpret_cast<uintptr_t>(range_sums) % 4 != 0)
+    if ((plan.kernel == chm::kGemmSplit || plan.kernel == chm::kGemmExactSplit) &&
+        reinterpret_cast<uintptr_t>(range_sums) % 4 != 0)
         return fail(ctx, CHARLOTTE_HIP_MATMUL_INVALID_ARGUMENT, "launch: range_sums not 4-byte aligned");
     return run_plan(ctx, a, format, plan, static_cast<float*>(range_sums), stream);
 }

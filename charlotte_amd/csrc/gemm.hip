@@ -287,6 +287,14 @@ void plan_gemm_canonical(const Product& a, uint32_t compute_units, bool split, P
     plan->workgroups = plan->tiles * chunks;
 }
 
+// The combine of a split product's range sums (every output of every token).
+hipError_t launch_combine_ranges(const Product& a, const float* range_sums, hipStream_t stream) {
+    const uint64_t outputs = static_cast<uint64_t>(a.tokens) * a.rows;
+    hipLaunchKernelGGL(combine_ranges, dim3(static_cast<uint32_t>((outputs + 255) / 256)), dim3(256), 0, stream, a,
+                       range_sums);
+    return hipGetLastError();
+}
+
 // The tiled form; with `range_sums` (room for 32 x tokens x rows floats), the
 // split form and its combine.
 hipError_t launch_gemm_canonical(const Product& a, uint32_t format, const Plan& plan, float* range_sums,
@@ -301,11 +309,7 @@ hipError_t launch_gemm_canonical(const Product& a, uint32_t format, const Plan& 
         case kBF16: go_format<kBF16>(a, plan, range_sums, stream); break;
         default: return hipErrorInvalidValue;
     }
-    if (range_sums) {
-        const uint64_t outputs = static_cast<uint64_t>(a.tokens) * a.rows;
-        hipLaunchKernelGGL(combine_ranges, dim3(static_cast<uint32_t>((outputs + 255) / 256)), dim3(256), 0, stream, a,
-                           range_sums);
-    }
+    if (range_sums) return launch_combine_ranges(a, range_sums, stream);
     return hipGetLastError();
 }
 

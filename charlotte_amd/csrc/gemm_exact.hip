@@ -106,14 +106,27 @@ __device__ __forceinline__ void weights_of(const Raw<F>& r, float* w) {
     }
 }
 
-template <uint32_t F, uint32_t TT, bool FULL, bool CLIP>
-__global__ __launch_bounds__(256, 2) void gemm_exact(Product a, uint32_t token_tiles) {
+// SPLIT (the split along K, matmul.wgsl:592-695): `chunks` workgroups a tile,
+// chunk c taking ranges [32c / chunks, 32(c + 1) / chunks) and writing each
+// range's sum to range_sums ([32][tokens][rows], range first) instead of
+// adding it to a total; combine_ranges (gemm.hip) then adds a row's sums in
+// order. The range sums are the VALU split's bits, so the outputs are too.
+// `quads`: rows a multiple of 4 and range_sums 16-byte aligned, so a lane's
+// four registers of consecutive rows go out as one 16-byte store (C6's split
+// 20.9 -> 18.3 us against a store a register).
+template <uint32_t F, uint32_t TT, bool FULL, bool CLIP, bool SPLIT = false>
+__global__ __launch_bounds__(256, 2) void gemm_exact(Product a, uint32_t token_tiles, uint32_t row_tiles,
+                                                     uint32_t chunks, float* range_sums, bool quads) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t tile_t = blockIdx.x % token_tiles, tile_r = blockIdx.x / token_tiles;
+    const uint32_t tile_t = blockIdx.x % token_tiles, tile_r = (blockIdx.x / token_tiles) % row_tiles;
+    const uint32_t chunk = blockIdx.x / (token_tiles * row_tiles);
     const uint32_t T = tile_t * TT, R = (tile_r * kWaves + wave) * kWaveRows;
     if (R >= a.rows) return;  // the whole wave: no barrier follows
     const uint32_t G = a.groups;
     const uint64_t K = static_cast<uint64_t>(G) * 32;
+    const uint32_t r_begin = 32 * chunk / chunks, r_end = 32 * (chunk + 1) / chunks;
+    const uint32_t g_begin = range_lo(r_begin, G), g_end = range_lo(r_end, G);
+    if (g_begin >= g_end) return;  // a chunk of empty ranges (G < 32): nothing to write
 
     // Rows and tokens past the product read its last row or token; their
     // outputs are never stored.
@@ -136,8 +149,8 @@ __global__ __launch_bounds__(256, 2) void gemm_exact(Product a, uint32_t token_t
 
     // The range that ends after group g is the one before `next_r`'s first
     // group; ranges with no groups (G < 32) hold zero and add nothing.
-    uint32_t next_r = 1;
-    while (next_r < 32 && range_lo(next_r, G) == 0) ++next_r;
+    uint32_t next_r = r_begin + 1;
+    while (next_r < r_end && range_lo(next_r, G) <= g_begin) ++next_r;
 
     // A group's bytes and inputs are loaded a whole group ahead, into one of
     // two buffers (the loop takes groups in pairs, so each buffer keeps its
@@ -200,16 +213,50 @@ __global__ __launch_bounds__(256, 2) void gemm_exact(Product a, uint32_t token_t
         }
         fresh = g + 1 == range_lo(next_r, G);
         if (fresh) {  // range next_r - 1 ends
+            if constexpr (SPLIT) {
 #pragma unroll
-            for (int v = 0; v < 32; ++v) {
-                const float a0 = s0[v];
-                t[0][v] = t[0][v] + a0;
-                if constexpr (S == 2) {
-                    const float a1 = s1[v];
-                    t[S - 1][v] = t[S - 1][v] + a1;
+                for (int v = 0; v < 32; v += 4) {
+                    const uint32_t in_block = 8 * ((v & 15) / 4) + 4 * (lane >> 5);  // rows in_block .. + 3
+                    uint32_t token, p;
+                    if constexpr (TT == 64) {
+                        token = T + 32 * (v / 16) + (lane & 31u), p = R + in_block;
+                    } else {
+                        token = T + (lane & 31u), p = R + 32 * (v / 16) + in_block;
+                    }
+                    if (token >= a.tokens) continue;
+                    float* at = range_sums + (static_cast<uint64_t>(next_r - 1) * a.tokens + token) * a.rows + p;
+                    float q0[4] = {s0[v], s0[v + 1], s0[v + 2], s0[v + 3]};
+                    if (quads) {
+                        if (p < a.rows) *reinterpret_cast<float4*>(at) = make_float4(q0[0], q0[1], q0[2], q0[3]);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (p + i < a.rows) at[i] = q0[i];
+                    }
+                    if constexpr (S == 2) {
+                        float q1[4] = {s1[v], s1[v + 1], s1[v + 2], s1[v + 3]};
+                        if (quads) {
+                            if (p + 32 < a.rows)
+                                *reinterpret_cast<float4*>(at + 32) = make_float4(q1[0], q1[1], q1[2], q1[3]);
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                if (p + 32 + i < a.rows) at[32 + i] = q1[i];
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < 32; ++v) {
+                    const float a0 = s0[v];
+                    t[0][v] = t[0][v] + a0;
+                    if constexpr (S == 2) {
+                        const float a1 = s1[v];
+                        t[S - 1][v] = t[S - 1][v] + a1;
+                    }
                 }
             }
-            while (next_r < 32 && range_lo(next_r, G) <= g + 1) ++next_r;
+            while (next_r < r_end && range_lo(next_r, G) <= g + 1) ++next_r;
         }
     };
 
@@ -218,14 +265,15 @@ __global__ __launch_bounds__(256, 2) void gemm_exact(Product a, uint32_t token_t
     // is the same on every path: a wait for one buffer never waits for the
     // other's loads.
     Buffer A, B;
-    fetch(A, 0);
-    for (uint32_t g = 0; g < G; g += 2) {
-        fetch(B, min(g + 1, G - 1));
+    fetch(A, g_begin);
+    for (uint32_t g = g_begin; g < g_end; g += 2) {
+        fetch(B, min(g + 1, g_end - 1));
         group(A, g);
-        if (g + 1 >= G) break;
-        fetch(A, min(g + 2, G - 1));
+        if (g + 1 >= g_end) break;
+        fetch(A, min(g + 2, g_end - 1));
         group(B, g + 1);
     }
+    if constexpr (SPLIT) return;
 
 #pragma unroll
     for (int v = 0; v < 32; ++v) {
@@ -244,22 +292,28 @@ __global__ __launch_bounds__(256, 2) void gemm_exact(Product a, uint32_t token_t
 }
 
 template <uint32_t F, uint32_t TT>
-void go_exact_tile(const Product& a, const Plan& plan, hipStream_t stream) {
-    const dim3 grid(static_cast<uint32_t>(plan.workgroups));
-    if (plain_epilogue(a))
-        hipLaunchKernelGGL((gemm_exact<F, TT, false, false>), grid, dim3(64 * kWaves), 0, stream, a, plan.token_tiles);
-    else if (!clipped(a))
-        hipLaunchKernelGGL((gemm_exact<F, TT, true, false>), grid, dim3(64 * kWaves), 0, stream, a, plan.token_tiles);
-    else
-        hipLaunchKernelGGL((gemm_exact<F, TT, true, true>), grid, dim3(64 * kWaves), 0, stream, a, plan.token_tiles);
+void go_exact_tile(const Product& a, const Plan& plan, float* range_sums, hipStream_t stream) {
+    const dim3 grid(static_cast<uint32_t>(plan.workgroups)), block(64 * kWaves);
+    const uint32_t tt = plan.token_tiles, rt = plan.row_tiles, ch = plan.chunks;
+    if (range_sums) {  // a split product has no options and is not gated
+        const bool quads = a.rows % 4 == 0 && reinterpret_cast<uintptr_t>(range_sums) % 16 == 0;
+        hipLaunchKernelGGL((gemm_exact<F, TT, false, false, true>), grid, block, 0, stream, a, tt, rt, ch, range_sums,
+                           quads);
+    } else if (plain_epilogue(a)) {
+        hipLaunchKernelGGL((gemm_exact<F, TT, false, false>), grid, block, 0, stream, a, tt, rt, 1u, nullptr, false);
+    } else if (!clipped(a)) {
+        hipLaunchKernelGGL((gemm_exact<F, TT, true, false>), grid, block, 0, stream, a, tt, rt, 1u, nullptr, false);
+    } else {
+        hipLaunchKernelGGL((gemm_exact<F, TT, true, true>), grid, block, 0, stream, a, tt, rt, 1u, nullptr, false);
+    }
 }
 
 template <uint32_t F>
-void go_exact(const Product& a, const Plan& plan, hipStream_t stream) {
+void go_exact(const Product& a, const Plan& plan, float* range_sums, hipStream_t stream) {
     if constexpr (F != kF32) {
-        if (plan.tile_tokens == 64) return go_exact_tile<F, 64>(a, plan, stream);
+        if (plan.tile_tokens == 64) return go_exact_tile<F, 64>(a, plan, range_sums, stream);
     }
-    go_exact_tile<F, 32>(a, plan, stream);
+    go_exact_tile<F, 32>(a, plan, range_sums, stream);
 }
 
 }  // namespace
@@ -274,37 +328,49 @@ void go_exact(const Product& a, const Plan& plan, hipStream_t stream) {
 // 32 — Llama 3.2 1B's QKV at 2,048 tokens: 1,536 waves of 64 x 64 on 1,024
 // SIMDs are two rounds, 3,072 of 64 x 32 one and a half. F32 always by 32 (its
 // 32 dwords a group beside 64 tokens' sums would not fit two waves' registers).
-void plan_gemm_exact(const Product& a, uint32_t format, uint32_t compute_units, Plan* plan) {
+void plan_gemm_exact(const Product& a, uint32_t format, uint32_t compute_units, bool split, Plan* plan) {
     *plan = Plan{};
     const uint64_t wave_rows = (a.rows + kWaveRows - 1) / kWaveRows;
     const uint64_t simds = 4ull * compute_units;
     const uint64_t rounds64 = (wave_rows * ((a.tokens + 63) / 64) + simds - 1) / simds;
     const uint64_t rounds32 = (wave_rows * ((a.tokens + 31) / 32) + simds - 1) / simds;  // half-length rounds
-    const uint32_t tt = format != kF32 && rounds32 >= 2 * rounds64 ? 64 : 32;
-    plan->kernel = kGemmExact;
-    plan->launches = 1;
+    uint32_t tt = format != kF32 && rounds32 >= 2 * rounds64 ? 64 : 32;
+    if (split) tt = format != kF32 && a.tokens > 32 ? 64 : 32;
+    plan->kernel = split ? kGemmExactSplit : kGemmExact;
+    plan->launches = split ? 2 : 1;
     plan->tile_tokens = tt;
     plan->tile_rows = kWaves * kWaveRows;
     plan->token_tiles = (a.tokens + tt - 1) / tt;
     plan->row_tiles = (a.rows + plan->tile_rows - 1) / plan->tile_rows;
-    plan->chunks = 1;
     plan->wave_rows = kWaveRows / 32;
     plan->wave_tokens = tt / 32;
     plan->tiles = static_cast<uint64_t>(plan->token_tiles) * plan->row_tiles;
-    plan->workgroups = plan->tiles;
+    // Split: the ranges cut into as few chunks (a power of two, at most 32)
+    // as still give every compute unit two workgroups where 32 can.
+    uint32_t chunks = 1;
+    if (split) {
+        chunks = 2;
+        while (chunks < 32 && plan->tiles * chunks < 2ull * compute_units) chunks *= 2;
+    }
+    plan->chunks = chunks;
+    plan->workgroups = plan->tiles * chunks;
 }
 
-hipError_t launch_gemm_exact(const Product& a, uint32_t format, const Plan& plan, hipStream_t stream) {
+// The tile; with `range_sums` (the split plan: room for 32 x tokens x rows
+// floats), the split form and then combine_ranges.
+hipError_t launch_gemm_exact(const Product& a, uint32_t format, const Plan& plan, float* range_sums,
+                             hipStream_t stream) {
     switch (format) {
-        case kQ4_0: go_exact<kQ4_0>(a, plan, stream); break;
-        case kQ4_1: go_exact<kQ4_1>(a, plan, stream); break;
-        case kQ8_0: go_exact<kQ8_0>(a, plan, stream); break;
-        case kQ6_K: go_exact<kQ6_K>(a, plan, stream); break;
-        case kF32: go_exact<kF32>(a, plan, stream); break;
-        case kF16: go_exact<kF16>(a, plan, stream); break;
-        case kBF16: go_exact<kBF16>(a, plan, stream); break;
+        case kQ4_0: go_exact<kQ4_0>(a, plan, range_sums, stream); break;
+        case kQ4_1: go_exact<kQ4_1>(a, plan, range_sums, stream); break;
+        case kQ8_0: go_exact<kQ8_0>(a, plan, range_sums, stream); break;
+        case kQ6_K: go_exact<kQ6_K>(a, plan, range_sums, stream); break;
+        case kF32: go_exact<kF32>(a, plan, range_sums, stream); break;
+        case kF16: go_exact<kF16>(a, plan, range_sums, stream); break;
+        case kBF16: go_exact<kBF16>(a, plan, range_sums, stream); break;
         default: return hipErrorInvalidValue;
     }
+    if (range_sums) return launch_combine_ranges(a, range_sums, stream);
     return hipGetLastError();
 }
 

@@ -29,6 +29,7 @@ enum Kernel : uint32_t {
     kGemmMfma = 18,     // prefill on the matrix cores, x split into two f16 parts
     kGemmShort = 19,    // prefill of a short step: 16 or 8 rows x 32 tokens, K split among the waves
     kGemmExact = 20,    // prefill on the matrix cores' K = 1 f32 instruction, the canonical order
+    kGemmExactSplit = 21,  // the same split along K, then the ordered combine
 };
 
 struct Plan {
@@ -69,6 +70,8 @@ uint64_t gemv_wide_workgroups(uint32_t compute_units, uint64_t steps);
 void plan_gemm_canonical(const Product& a, uint32_t compute_units, bool split, Plan* plan);
 hipError_t launch_gemm_canonical(const Product& a, uint32_t format, const Plan& plan, float* range_sums,
                                  hipStream_t stream);
+// The split form's ordered combine of range sums (gemm.hip).
+hipError_t launch_combine_ranges(const Product& a, const float* range_sums, hipStream_t stream);
 
 // Prefill of a short step (gemm_short.hip): a step that does not split and
 // whose 128-row tiles would leave compute units idle.
@@ -77,8 +80,9 @@ hipError_t launch_gemm_short(const Product& a, uint32_t format, const Plan& plan
 
 // Prefill on the matrix cores in the canonical order (gemm_exact.hip):
 // every format, every epilogue, the VALU tile's bits.
-void plan_gemm_exact(const Product& a, uint32_t format, uint32_t compute_units, Plan* plan);
-hipError_t launch_gemm_exact(const Product& a, uint32_t format, const Plan& plan, hipStream_t stream);
+void plan_gemm_exact(const Product& a, uint32_t format, uint32_t compute_units, bool split, Plan* plan);
+hipError_t launch_gemm_exact(const Product& a, uint32_t format, const Plan& plan, float* range_sums,
+                             hipStream_t stream);
 
 // Prefill on the matrix cores, x split into two f16 parts.
 bool mfma_reads(uint32_t format);

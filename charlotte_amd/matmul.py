@@ -102,6 +102,7 @@ class Kernel(enum.IntEnum):
     GEMM_MFMA = 18
     GEMM_SHORT = 19
     GEMM_EXACT = 20
+    GEMM_EXACT_SPLIT = 21
 
 
 class GemvPath(enum.IntEnum):

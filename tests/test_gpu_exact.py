@@ -9,7 +9,8 @@ EXACT_MFMA too); here the two tiles meet where the oracle would take too long:
 the BASELINE prefill shapes in full (C4; C5's QKV, gated gate/up and down at
 2,048 tokens), Q6_K products, K past the ranges' count (K = 14,336) and
 below it (K = 64: 30 empty ranges), ragged rows and tokens, every epilogue,
-on both of its tiles (64 tokens a wave for large steps, 32 for the rest).
+on both of its tiles (64 tokens a wave for large steps, 32 for the rest);
+and its split along K (GEMM_EXACT_SPLIT) against the VALU's (GEMM_SPLIT).
 The reference's own check of the same property: a token's outputs the same
 whatever the step (tests/gpu/matmul_test.cpp:257-267).
 """
@@ -17,11 +18,9 @@ whatever the step (tests/gpu/matmul_test.cpp:257-267).
 import numpy as np
 import pytest
 
-from tests.support.oracle_lib import Q4_0, Q6_K
+from tests.support.oracle_lib import F32, Q4_0, Q4_1, Q6_K, Q8_0
 
 pytestmark = pytest.mark.gpu
-
-Q8_0, Q4_1 = 8, 3
 
 
 @pytest.fixture(scope="module")
@@ -164,3 +163,61 @@ def test_every_epilogue_and_option_same_bits(ctxs, activation):
 
     got, want = _both(ctxs, opts, x, tokens, [300], clip=clip, bias=bias, activated=True, activation=activation)
     _same(got, want, f"write with options act={activation}")
+
+
+@pytest.mark.parametrize("gtype,rows,columns,tokens", [
+    (Q4_0, 2048, 8192, 32),      # C6: 8 tiles x 32 chunks
+    (Q4_0, 2048, 8192, 64),      # 64-token tiles
+    (Q6_K, 3072, 1152, 9),
+    (Q4_0, 1000, 14336, 33),     # 448 groups: 14 a range; 64-token tiles, 31 tokens past the step
+    (Q4_0, 333, 64, 20),         # 2 groups: 30 empty ranges, chunks holding none
+    (Q8_0, 700, 2048, 17),
+    (Q4_1, 520, 1024, 5),
+    (F32, 300, 1024, 12),
+])
+def test_split_same_bits_as_the_valu_split(ctxs, gtype, rows, columns, tokens):
+    """The split along K (GEMM_EXACT_SPLIT against GEMM_SPLIT): each chunk's
+    range sums the VALU split's bits, so the combine's outputs are too."""
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+
+    rng = np.random.default_rng(rows + columns + tokens + 7)
+    if gtype == F32:
+        stored = (rng.standard_normal((rows, columns)).astype(np.float32) * np.float32(0.05)).tobytes()
+    else:
+        stored = synthetic.weight(rng, gtype, rows, columns)
+    x = synthetic.activations(rng, tokens, columns)
+    sums = 4 * mm.range_sum_floats(mm.Epilogue.Write, rows, columns, mm.kAlways)
+    shape = [mm.Member(mm.Weight.shape(gtype, rows, columns))]
+    for path, kernel in ((mm.GemmPath.EXACT_MFMA, mm.Kernel.GEMM_EXACT_SPLIT), (mm.GemmPath.CANONICAL,
+                                                                                 mm.Kernel.GEMM_SPLIT)):
+        assert mm.plan_launch(mm.MatmulLaunch(shape, 16, [16]), tokens, mm.Target(gemm_path=path), gate=mm.kAlways,
+                              range_sums_bytes=sums).kernel == kernel
+
+    def members(ctx):
+        w = _weight(ctx, gtype, rows, columns, stored)
+        return [mm.Member(w)], [w]
+
+    got, want = _both(ctxs, members, x, tokens, [rows], gate=mm.kAlways, sums_bytes=sums)
+    _same(got, want, f"split type {gtype} {rows}x{columns} tokens={tokens}")
+
+
+def test_split_qkv_same_bits_as_the_valu_split(ctxs):
+    """A fused QKV step split along K: the combine routes each row to its
+    member's output."""
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+
+    rng = np.random.default_rng(8)
+    tokens, columns = 24, 2048
+    x = synthetic.activations(rng, tokens, columns)
+    parts = [synthetic.weight(rng, Q4_0, r, columns) for r in (2048, 512, 512)]
+    sums = 4 * mm.range_sum_floats(mm.Epilogue.QKV, 3072, columns, mm.kAlways)
+
+    def qkv_members(ctx):
+        ws = [_weight(ctx, Q4_0, r, columns, s) for r, s in zip((2048, 512, 512), parts)]
+        return [mm.Member(w) for w in ws], ws
+
+    got, want = _both(ctxs, qkv_members, x, tokens, [2048, 512, 512], epilogue=mm.Epilogue.QKV, gate=mm.kAlways,
+                      sums_bytes=sums)
+    _same(got, want, "qkv split")

@@ -142,7 +142,7 @@ def test_epilogues_over_float_weights(oracle, run, gtype):
         w.free()
 
 
-@pytest.mark.parametrize("gtype", [F16, BF16])
+@pytest.mark.parametrize("gtype", [F16, BF16, F32])
 def test_split_along_k_gives_the_tiled_bits(oracle, run, gtype):
     from charlotte_amd import matmul as mm
 
@@ -152,7 +152,7 @@ def test_split_along_k_gives_the_tiled_bits(oracle, run, gtype):
     want = oracle.matmul_f32(gtype, stored, rows, columns, x, threads=16)
     sums = 4 * mm.range_sum_floats(mm.Epilogue.Write, rows, columns, mm.kAlways)
     assert mm.plan_launch(mm.MatmulLaunch([mm.Member(w)], 16, [16]), 32, gate=mm.kAlways,
-                          range_sums_bytes=sums).kernel == mm.Kernel.GEMM_SPLIT
+                          range_sums_bytes=sums).kernel == mm.Kernel.GEMM_EXACT_SPLIT  # AUTO's plan
     _check(run.write(w, x, 32, gate=mm.kAlways, sums_bytes=sums), want, "split")
     w.free()
 

@@ -106,7 +106,7 @@ def test_clip_takes_four_bound_words_or_none(shapes):
     assert "4-byte" in _refused(_write(w, clip=[span, span + 2, span + 8, span + 12]), 1)
     # An optioned product never splits (matmul.cpp:166-172), whatever the gate.
     assert mm.plan_launch(_write(w, clip=apart), 32, gate=mm.kAlways, range_sums_bytes=1 << 24).kernel == K.GEMM_SHORT
-    assert mm.plan_launch(_write(w), 32, gate=mm.kAlways, range_sums_bytes=1 << 24).kernel == K.GEMM_SPLIT
+    assert mm.plan_launch(_write(w), 32, gate=mm.kAlways, range_sums_bytes=1 << 24).kernel == K.GEMM_EXACT_SPLIT
 
 
 # ---- the kernel each shape runs --------------------------------------------------
@@ -267,10 +267,27 @@ def test_the_matrix_cores_refuse_the_float_formats(shapes):
 
 
 def test_short_steps_split_along_k_when_the_gate_and_range_sums_allow(shapes):
+    """AUTO splits on the matrix cores' fused multiply-add (GEMM_EXACT_SPLIT),
+    CANONICAL on the VALU tile (GEMM_SPLIT): the same range sums, the same
+    combine. The exact split cuts the 32 ranges into the fewest chunks (a
+    power of two) that give every compute unit two workgroups: 8,192 rows at
+    32 tokens are 32 tiles of 256 rows, 16 chunks."""
     w = shapes(Q4_0, 8192, 2048)
     sums = 4 * mm.range_sum_floats(mm.Epilogue.Write, 8192, 2048, mm.kAlways)
     p = mm.plan_launch(_write(w), 32, gate=mm.kAlways, range_sums_bytes=sums)
+    assert (p.kernel, p.launches, p.canonical, p.tile_tokens, p.tile_rows) == (K.GEMM_EXACT_SPLIT, 2, True, 32, 256)
+    assert (p.tiles, p.chunks, p.workgroups) == (32, 16, 512)
+    p = mm.plan_launch(_write(w), 32, mm.Target(256, mm.GemmPath.CANONICAL), gate=mm.kAlways, range_sums_bytes=sums)
     assert (p.kernel, p.launches, p.canonical, p.tile_tokens) == (K.GEMM_SPLIT, 2, True, 32) and p.chunks >= 2
+    # C6: 2,048 x 8,192 at 32 tokens: 8 tiles, the most chunks (32); 64 tokens by 64
+    down = shapes(Q4_0, 2048, 8192)
+    sums = 4 * mm.range_sum_floats(mm.Epilogue.Write, 2048, 8192, mm.kAlways)
+    p = mm.plan_launch(_write(down), 32, gate=mm.kAlways, range_sums_bytes=sums)
+    assert (p.kernel, p.tiles, p.chunks, p.workgroups) == (K.GEMM_EXACT_SPLIT, 8, 32, 256)
+    p = mm.plan_launch(_write(down), 64, gate=mm.kAlways, range_sums_bytes=2 * sums)
+    assert (p.kernel, p.tile_tokens, p.tiles, p.chunks) == (K.GEMM_EXACT_SPLIT, 64, 8, 32)
+    assert mm.plan_launch(_write(down), 64, mm.Target(128), gate=mm.kAlways, range_sums_bytes=2 * sums).chunks == 32
+    assert mm.plan_launch(_write(down), 64, mm.Target(16), gate=mm.kAlways, range_sums_bytes=2 * sums).chunks == 4
     # Range sums too small for the step, no gate, options or a gated product: a
     # tile (the short-step tile under AUTO, the 128-row tile under CANONICAL).
     canonical = mm.Target(256, mm.GemmPath.CANONICAL)
@@ -319,7 +336,7 @@ def test_exact_mfma_path_takes_every_unsplit_prefill_step(shapes):
     cores' f32 fused multiply-add (GEMM_EXACT, the canonical order): tiles of
     256 rows by 64 tokens where 64 x 64 waves take no more rounds of the 1,024
     SIMDs than 64 x 32 waves take half-length rounds, else by 32 tokens; decode
-    and the split are unchanged."""
+    are unchanged, and the split runs on the matrix cores as under AUTO."""
     w = shapes(Q4_0, 2048, 8192)
     exact = mm.Target(256, mm.GemmPath.EXACT_MFMA)
     for tokens in (2, 31, 32, 64, 511, 2048, 4096):
@@ -337,7 +354,8 @@ def test_exact_mfma_path_takes_every_unsplit_prefill_step(shapes):
     assert mm.plan_launch(_write(shapes(Q4_0, 3072, 2048)), 2048, exact).tile_tokens == 32
     assert mm.plan_launch(_write(w), 1, exact).kernel == mm.plan_launch(_write(w), 1).kernel == K.GEMV_RANGES
     sums = 4 * mm.range_sum_floats(mm.Epilogue.Write, 2048, 8192, mm.kSplitGate)
-    assert mm.plan_launch(_write(w), 32, exact, gate=mm.kSplitGate, range_sums_bytes=sums).kernel == K.GEMM_SPLIT
+    assert mm.plan_launch(_write(w), 32, exact, gate=mm.kSplitGate, range_sums_bytes=sums).kernel == \
+        K.GEMM_EXACT_SPLIT
     g = mm.MatmulLaunch([mm.Member(w), mm.Member(w)], X, [Y0], epilogue=mm.Epilogue.GatedActivation)
     assert mm.plan_launch(g, 32, exact).kernel == K.GEMM_EXACT
     f = shapes(F16, 300, 1024)

@@ -65,11 +65,11 @@ def test_static_launch_matches_the_launch_on_two_calls_the_second_smaller(ctx, o
 
     print("no-alloc: call 1, Q4_0 2048 x 2048, 32 tokens, split", flush=True)
     plan, a, b, want = _both(ctx, Q4_0, 2048, 2048, 32, 1, oracle)
-    assert plan.kernel == mm.Kernel.GEMM_SPLIT
+    assert plan.kernel == mm.Kernel.GEMM_EXACT_SPLIT
     assert _same(a, want) and _same(b, a)
     print("no-alloc: call 2, Q6_K 512 x 1024, 9 tokens, split", flush=True)
     plan, a, b, want = _both(ctx, Q6_K, 512, 1024, 9, 2, oracle)
-    assert plan.kernel == mm.Kernel.GEMM_SPLIT
+    assert plan.kernel == mm.Kernel.GEMM_EXACT_SPLIT
     assert _same(a, want) and _same(b, a)
 
 
@@ -102,7 +102,7 @@ def test_static_launch_tiles_a_split_past_its_array(ctx, oracle):
     xb, yb = hx.Buffer.of(x), hx.Buffer(4 * tokens * rows)
     yb.fill(0xFF)
     m = mm.MatmulLaunch([mm.Member(w)], xb.ptr, [yb.ptr])
-    assert mm.plan_launch(m, tokens, gate=mm.kAlways, range_sums_bytes=1 << 40).kernel == mm.Kernel.GEMM_SPLIT
+    assert mm.plan_launch(m, tokens, gate=mm.kAlways, range_sums_bytes=1 << 40).kernel == mm.Kernel.GEMM_EXACT_SPLIT
     assert mm.plan_launch(m, tokens, gate=mm.kAlways,
                           range_sums_bytes=mm.STATIC_SCRATCH_BYTES).kernel == mm.Kernel.GEMM_SHORT
     mm.launch_static(ctx, m, tokens, mm.kAlways)
@@ -140,7 +140,7 @@ def test_static_launch_replays_from_a_graph_captured_in_global_mode(ctx, oracle)
     ms = [mm.MatmulLaunch([mm.Member(w)], x.ptr, [y.ptr]) for w, x, y in zip(ws, xs, ys)]
     other = mm.MatmulLaunch([mm.Member(other_w)], other_x.ptr, [other_y.ptr])
     assert mm.plan_launch(ms[0], 32, gate=mm.kAlways,
-                          range_sums_bytes=mm.STATIC_SCRATCH_BYTES).kernel == mm.Kernel.GEMM_SPLIT
+                          range_sums_bytes=mm.STATIC_SCRATCH_BYTES).kernel == mm.Kernel.GEMM_EXACT_SPLIT
     want = [[oracle.matmul_f32(g, s, r, c, i, threads=16) for i in ins]
             for (g, r, c, _), s, ins in zip(shapes, stored, inputs)]
 
