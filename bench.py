@@ -690,6 +690,35 @@ def c3_floors(S, launches, steps, warmup):
     return {"launch_us": round(launch_ms * 1e3, 1), "memory_us": round(memory_ms * 1e3, 1), "memory_bytes": total}
 
 
+def c3_cached(steps, warmup, settle_ms):
+    """c3's 112 layer launches (the step without its head) as graphs, with
+    every layer's own weights (235 MB, the step as it runs) and with the first
+    7, 3 and 1 layers' weights cycled through the same 112 launches (59, 25
+    and 8.4 MB: inside the MALL; the L2s' 32 MB; one layer's, L2-resident):
+    what a launch would save with its weights already cached. Two rounds,
+    us a step and a launch."""
+    S = Setup()
+    S.settle_ms = settle_ms
+    mm = S.mm
+    rng = np.random.default_rng(3)
+    out = {}
+    try:
+        launches, _, _, _ = build_products(S, rng, layer_plan(2048, 1024, 1024, 3072, True) * 28, 1)
+        cases = [("28 layers", launches), ("7 layers cycled", launches[:28] * 4),
+                 ("3 layers cycled", (launches[:12] * 10)[:112]), ("1 layer cycled", launches[:4] * 28)]
+        for rnd in range(2):
+            for name, ls in cases:
+                def body(ls=ls):
+                    for m in ls:
+                        mm.launch(S.ctx, m, 1, stream=S.stream.handle)
+                us = S.time_graph(body, steps, warmup) * 1e3
+                log(f"c3 cached, {name}: {us:.1f} us for {len(ls)} launches, {us / len(ls):.2f} us a launch")
+                out.setdefault(name, []).append({"us": round(us, 1), "us_a_launch": round(us / len(ls), 3)})
+    finally:
+        S.close()
+    return out
+
+
 def decode_matches_prefill(S, launches, xs, rng, tokens=4):
     """The step's token decoded alone (the outputs the timed launches wrote) against the same token
     prefilled as the last of `tokens`: every product, bit for bit (the consistency the reference tracks,
@@ -1006,6 +1035,8 @@ def main():
                         "optionally a comma list of probe shape numbers (0-8)")
     p.add_argument("--read-sweep", action="store_true",
                    help="time every pure-read form over C2's bytes (the read ceiling) and exit")
+    p.add_argument("--c3-cached", action="store_true",
+                   help="time c3's 112 layer launches with 28, 7, 3 and 1 layers' weights (cycled) and exit")
     args = p.parse_args()
     if args.cpu_table:
         print(json.dumps(cpu_table(min(os.cpu_count() or 1, 16))), flush=True)
@@ -1016,6 +1047,9 @@ def main():
         return
     if args.read_sweep:
         print(json.dumps(read_sweep(max(args.steps, 20), args.warmup, args.settle_ms)), flush=True)
+        return
+    if args.c3_cached:
+        print(json.dumps(c3_cached(args.steps, args.warmup, args.settle_ms)), flush=True)
         return
     if args.decode:
         print(json.dumps(time_decode_shapes(args.decode, args.steps, args.warmup, args.settle_ms, args.limbs)),
