@@ -232,26 +232,33 @@ __global__ __launch_bounds__(256) void mfma_rate_kernel(uint32_t iters, uint32_t
     if (fold == kNever) sink[static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = fold;
 }
 
-// Whether the K = 1 f32 matrix instruction (32x32x1, two blocks) rounds as
-// one fused multiply-add. Pair p gives a and b to every lane, and the wave's
-// 2,048 accumulator values c[p][64 v + lane] (v < 32); every element of the
-// result is then c + a b whatever its place in the blocks, so no layout is
-// assumed: lane l compares its result v with fmaf(a, b, c) bit for bit (two
-// NaNs agree). out: [0] elements differing, [1] elements compared, then for
-// the first 64 differing: pair, element, the instruction's bits, fmaf's bits.
+// Whether a K = 1 f32 matrix instruction rounds as one fused multiply-add:
+// S 5 the 32x32x1 (two blocks, 32 registers), 6 the 16x16x1 (four blocks, 16
+// registers). Pair p gives a and b to every lane, and the wave's accumulator
+// values c[p][64 v + lane] (v < the shape's registers; 2,048 floats a pair);
+// every element of the result is then c + a b whatever its place in the
+// blocks, so no layout is assumed: lane l compares its result v with fmaf(a,
+// b, c) bit for bit (two NaNs agree). out: [0] elements differing, [1]
+// elements compared, then for the first 64 differing: pair, element, the
+// instruction's bits, fmaf's bits.
+template <int S>
 __global__ __launch_bounds__(64) void mfma_fma_check_kernel(const float* ab, const float* c, uint32_t pairs,
                                                             uint32_t* out) {
+    constexpr int R = S == 5 ? 32 : 16;
+    using Acc = std::conditional_t<R == 32, mf32, mf16>;
     const uint32_t lane = threadIdx.x;
-    uint32_t differing = 0, compared = 0;
+    uint32_t compared = 0;
     for (uint32_t p = blockIdx.x; p < pairs; p += gridDim.x) {
         const float a = ab[2 * p], b = ab[2 * p + 1];
         const float* cp = c + static_cast<uint64_t>(p) * 2048;
-        mf32 acc;
+        Acc acc;
 #pragma unroll
-        for (int v = 0; v < 32; ++v) acc[v] = cp[64 * v + lane];
-        const mf32 d = __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, acc, 0, 0, 0);
+        for (int v = 0; v < R; ++v) acc[v] = cp[64 * v + lane];
+        Acc d;
+        if constexpr (S == 5) d = __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, acc, 0, 0, 0);
+        else d = __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, acc, 0, 0, 0);
 #pragma unroll
-        for (int v = 0; v < 32; ++v) {
+        for (int v = 0; v < R; ++v) {
             // the element copied out first: this compiler lowers a bit cast of
             // a vector's element d[v] to element 0 whatever v is
             const float dv = d[v];
@@ -267,11 +274,9 @@ __global__ __launch_bounds__(64) void mfma_fma_check_kernel(const float* ab, con
                     out[4 + 4 * at] = db;
                     out[5 + 4 * at] = rb;
                 }
-                ++differing;
             }
         }
     }
-    (void)differing;
     atomicAdd(out + 1, compared);
 }
 
@@ -347,19 +352,29 @@ __global__ __launch_bounds__(64) void mfma_c_probe_kernel(const float* c, float*
     for (int v = 0; v < R; ++v) out[64 * v + lane] = d[v];
 }
 
-// The K = 1 f32 instruction's lane layout: with C = 0, a = lane + 1 and b = 1
-// each result names the lane whose a it took (its row); with a = 1 and b =
-// lane + 1, the lane whose b it took (its column). out: 2 x 64 lanes x 32.
+// A K = 1 f32 instruction's lane layout (S 5 the 32x32x1, 6 the 16x16x1):
+// with C = 0, a = lane + 1 and b = 1 each result names the lane whose a it
+// took (its row); with a = 1 and b = lane + 1, the lane whose b it took (its
+// column). out: 2 x 64 lanes x the shape's registers, [64 v + lane].
+template <int S>
 __global__ __launch_bounds__(64) void mfma_layout_kernel(float* out) {
+    constexpr int R = S == 5 ? 32 : 16;
+    using Acc = std::conditional_t<R == 32, mf32, mf16>;
     const uint32_t lane = threadIdx.x;
-    const mf32 zero = {};
+    const Acc zero = {};
     const float id = static_cast<float>(lane + 1);
-    const mf32 rows = __builtin_amdgcn_mfma_f32_32x32x1f32(id, 1.0f, zero, 0, 0, 0);
-    const mf32 cols = __builtin_amdgcn_mfma_f32_32x32x1f32(1.0f, id, zero, 0, 0, 0);
+    Acc rows, cols;
+    if constexpr (S == 5) {
+        rows = __builtin_amdgcn_mfma_f32_32x32x1f32(id, 1.0f, zero, 0, 0, 0);
+        cols = __builtin_amdgcn_mfma_f32_32x32x1f32(1.0f, id, zero, 0, 0, 0);
+    } else {
+        rows = __builtin_amdgcn_mfma_f32_16x16x1f32(id, 1.0f, zero, 0, 0, 0);
+        cols = __builtin_amdgcn_mfma_f32_16x16x1f32(1.0f, id, zero, 0, 0, 0);
+    }
 #pragma unroll
-    for (int v = 0; v < 32; ++v) {
+    for (int v = 0; v < R; ++v) {
         out[64 * v + lane] = rows[v];
-        out[2048 + 64 * v + lane] = cols[v];
+        out[64 * R + 64 * v + lane] = cols[v];
     }
 }
 
@@ -599,16 +614,22 @@ int chx_mfma_rate(int shape, int chains, uint32_t blocks, uint32_t iters, void* 
     return hipGetLastError();
 }
 
-// mfma_fma_check_kernel over `pairs` pairs (ab: 2 floats a pair; c: 2,048
-// floats a pair), `blocks` one-wave workgroups; out: 2 + 4 x 64 words,
-// cleared here.
-int chx_mfma_fma_check(const void* ab, const void* c, uint32_t pairs, uint32_t blocks, void* out, void* s) {
-    if (pairs == 0 || blocks == 0) return hipErrorInvalidValue;
+// mfma_fma_check_kernel<shape> (5 or 6) over `pairs` pairs (ab: 2 floats a
+// pair; c: 2,048 floats a pair), `blocks` one-wave workgroups; out: 2 + 4 x
+// 64 words, cleared here.
+int chx_mfma_fma_check(int shape, const void* ab, const void* c, uint32_t pairs, uint32_t blocks, void* out,
+                       void* s) {
+    if (pairs == 0 || blocks == 0 || (shape != 5 && shape != 6)) return hipErrorInvalidValue;
     const auto stream = static_cast<hipStream_t>(s);
     hipError_t e = hipMemsetAsync(out, 0, (2 + 4 * 64) * 4, stream);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(mfma_fma_check_kernel, dim3(blocks), dim3(64), 0, stream, static_cast<const float*>(ab),
-                       static_cast<const float*>(c), pairs, static_cast<uint32_t*>(out));
+    const auto* abf = static_cast<const float*>(ab);
+    const auto* cf = static_cast<const float*>(c);
+    auto* o = static_cast<uint32_t*>(out);
+    if (shape == 5)
+        hipLaunchKernelGGL(mfma_fma_check_kernel<5>, dim3(blocks), dim3(64), 0, stream, abf, cf, pairs, o);
+    else
+        hipLaunchKernelGGL(mfma_fma_check_kernel<6>, dim3(blocks), dim3(64), 0, stream, abf, cf, pairs, o);
     return hipGetLastError();
 }
 
@@ -647,9 +668,13 @@ int chx_mfma_chain_check(int k, const void* ab, const void* c, uint32_t pairs, u
     return hipGetLastError();
 }
 
-// mfma_layout_kernel: out holds 2 x 2,048 floats.
-int chx_mfma_layout(void* out, void* s) {
-    hipLaunchKernelGGL(mfma_layout_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(s), static_cast<float*>(out));
+// mfma_layout_kernel<shape> (5 or 6): out holds 2 x 2,048 floats.
+int chx_mfma_layout(int shape, void* out, void* s) {
+    const auto stream = static_cast<hipStream_t>(s);
+    if (shape == 5) hipLaunchKernelGGL(mfma_layout_kernel<5>, dim3(1), dim3(64), 0, stream, static_cast<float*>(out));
+    else if (shape == 6)
+        hipLaunchKernelGGL(mfma_layout_kernel<6>, dim3(1), dim3(64), 0, stream, static_cast<float*>(out));
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

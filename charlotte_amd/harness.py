@@ -47,8 +47,9 @@ _SIGS = {
     "chx_mfma_rate": (_c.c_int, [_c.c_int, _c.c_int, _c.c_uint32, _c.c_uint32, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
     "chx_read_sweep": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_uint32, _c.c_uint32, _c.c_void_p,
                                   _c.c_uint64, _c.c_void_p, _c.c_uint64, _c.c_void_p]),
-    "chx_mfma_fma_check": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_uint32, _c.c_uint32, _c.c_void_p, _c.c_void_p]),
-    "chx_mfma_layout": (_c.c_int, [_c.c_void_p, _c.c_void_p]),
+    "chx_mfma_fma_check": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_void_p, _c.c_uint32, _c.c_uint32, _c.c_void_p,
+                                      _c.c_void_p]),
+    "chx_mfma_layout": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_void_p]),
     "chx_mfma_c_probe": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_void_p, _c.c_void_p]),
     "chx_mfma_chain_check": (_c.c_int, [_c.c_int, _c.c_void_p, _c.c_void_p, _c.c_uint32, _c.c_uint32, _c.c_void_p,
                                         _c.c_void_p]),
@@ -228,10 +229,11 @@ def mfma_rate(shape, chains, blocks, iters, sink_ptr, sink_bytes, stream=None):
                             stream.handle if isinstance(stream, Stream) else stream), "mfma rate")
 
 
-def mfma_fma_check(ab_ptr, c_ptr, pairs, blocks, out_ptr, stream=None):
-    """chx_mfma_fma_check: the K = 1 f32 matrix instruction against fmaf, bit for bit; out (2 + 256 words):
-    differing, compared, then (pair, element, instruction bits, fmaf bits) for the first 64 differing."""
-    check(lib.chx_mfma_fma_check(ab_ptr, c_ptr, pairs, blocks, out_ptr,
+def mfma_fma_check(ab_ptr, c_ptr, pairs, blocks, out_ptr, stream=None, shape=5):
+    """chx_mfma_fma_check: a K = 1 f32 matrix instruction (shape 5 the 32x32x1 two-block, 6 the 16x16x1
+    four-block) against fmaf, bit for bit; out (2 + 256 words): differing, compared, then (pair, element,
+    instruction bits, fmaf bits) for the first 64 differing."""
+    check(lib.chx_mfma_fma_check(shape, ab_ptr, c_ptr, pairs, blocks, out_ptr,
                                  stream.handle if isinstance(stream, Stream) else stream), "mfma fma check")
 
 
@@ -242,9 +244,11 @@ def mfma_chain_check(k, ab_ptr, c_ptr, pairs, blocks, out_ptr, stream=None):
                                    stream.handle if isinstance(stream, Stream) else stream), "mfma chain check")
 
 
-def mfma_layout(out_ptr, stream=None):
-    """chx_mfma_layout: 2 x 2,048 floats, the lane (+1) each 32x32x1 result took its a from, then its b."""
-    check(lib.chx_mfma_layout(out_ptr, stream.handle if isinstance(stream, Stream) else stream), "mfma layout")
+def mfma_layout(out_ptr, stream=None, shape=5):
+    """chx_mfma_layout: the lane (+1) each result of a K = 1 f32 shape (5 the 32x32x1, 32 registers; 6 the
+    16x16x1, 16) took its a from, then its b: 2 x 64 x registers floats, [64 v + lane]."""
+    check(lib.chx_mfma_layout(shape, out_ptr, stream.handle if isinstance(stream, Stream) else stream),
+          "mfma layout")
 
 
 def mfma_c_probe(shape, c_ptr, out_ptr, stream=None):

@@ -1,6 +1,7 @@
-"""The matrix-core instruction the canonical-order prefill tile (GEMM_EXACT)
-is built on: v_mfma_f32_32x32x1_2b_f32 is, element by element, one fused
-multiply-add, d = fmaf(a, b, c), bit for bit.
+"""The matrix-core instructions the canonical-order prefill tiles (GEMM_EXACT)
+are built on: v_mfma_f32_32x32x1_2b_f32 and v_mfma_f32_16x16x1_4b_f32 are,
+element by element, one fused multiply-add, d = fmaf(a, b, c), bit for bit;
+and their lane layouts.
 
 GEMM_EXACT's outputs are the reference order's bits only because of that, so
 the property itself is held here, on the harness's probes (harness.hip):
@@ -81,9 +82,11 @@ def _classes(rng):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("shape,registers", [(5, 32), (6, 16)])
 @pytest.mark.parametrize("name", ["random", "cancel", "halfway", "denormal", "denormal_operand", "special",
                                   "overflow"])
-def test_k1_f32_instruction_is_fmaf_bit_for_bit(name):
+def test_k1_f32_instruction_is_fmaf_bit_for_bit(name, shape, registers):
+    """Shape 5: v_mfma_f32_32x32x1_2b_f32; 6: v_mfma_f32_16x16x1_4b_f32."""
     from charlotte_amd import harness as hx
 
     a, b, c = _classes(np.random.default_rng(sum(map(ord, name))))[name]()
@@ -92,10 +95,10 @@ def test_k1_f32_instruction_is_fmaf_bit_for_bit(name):
     out = hx.Buffer(nbytes=(2 + 256) * 4)
     s = hx.Stream()
     try:
-        hx.mfma_fma_check(ab.ptr, cb.ptr, PAIRS, 1024, out.ptr, s)
+        hx.mfma_fma_check(ab.ptr, cb.ptr, PAIRS, 1024, out.ptr, s, shape=shape)
         s.sync()
         o = out.read(np.uint32)
-        assert o[1] == PAIRS * 2048, "every element compared"
+        assert o[1] == PAIRS * 64 * registers, "every element compared"
         assert o[0] == 0, f"{name}: {o[0]} of {o[1]} differ; first (pair, element, mfma, fmaf): {o[2:6].tolist()}"
     finally:
         for buf in (ab, cb, out):
@@ -122,6 +125,39 @@ def test_accumulators_come_back_in_their_places(shape, registers):
         cb.free()
         ob.free()
         s.destroy()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [5, 6])
+def test_k1_f32_instruction_layout(shape):
+    """The places the exact prefill tiles read results from. 32x32x1 (two
+    blocks, 32 registers): register v of lane l is block v / 16, its row 8
+    ((v % 16) / 4) + 4 (l / 32) + v % 4 (a from lane 32 (v / 16) + that row),
+    its column l % 32 (b from lane 32 (v / 16) + l % 32). 16x16x1 (four
+    blocks, 16 registers): block v / 4, row 4 (l / 16) + v % 4, column l % 16,
+    a and b from lanes 16 (v / 4) + row and + column."""
+    from charlotte_amd import harness as hx
+
+    registers = 32 if shape == 5 else 16
+    out = hx.Buffer(nbytes=2 * 64 * registers * 4)
+    s = hx.Stream()
+    try:
+        hx.mfma_layout(out.ptr, s, shape=shape)
+        s.sync()
+        got = out.read(np.float32).reshape(2, registers, 64)
+    finally:
+        out.free()
+        s.destroy()
+    v = np.arange(registers)[:, None]
+    lane = np.arange(64)[None, :]
+    if shape == 5:
+        block, row, col = v // 16, 8 * ((v % 16) // 4) + 4 * (lane // 32) + v % 4, lane % 32
+        width = 32
+    else:
+        block, row, col = v // 4, 4 * (lane // 16) + v % 4, lane % 16
+        width = 16
+    assert (got[0] == width * block + row + 1).all(), "rows"
+    assert (got[1] == width * block + col + 1).all(), "columns"
 
 
 def _mixed(rng, n, k, registers):
