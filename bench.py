@@ -20,7 +20,9 @@ A step is one pass of the hot path over one batch of synthetic input:
   c5_tile128.
   c6  a short prefill step, 32 tokens through Llama-3.2-1B's down projection
       (2048x8192 Q4_0): split along K on the matrix cores' fused multiply-add
-      (c6_split, AUTO) and on the VALU (c6_split128), tiled (c6_tiled), matrix cores
+      (c6_split, AUTO) and on the VALU (c6_split128); unsplit on the matrix-core
+      short-step tile (c6_tiled, AUTO) and the VALU one (c6_tiled_valu); the
+      split-f16 matrix cores
   c7  the embedding gather from Qwen3-0.6B's Q6_K table (151936x1024): a
       512-token step and a decode step
   c8  large Q4_0 decodes: a Q4_0 LM head 151936x1024 and a 32768x8192 product
@@ -816,7 +818,7 @@ def gemm_roofline(tflops, path, name, kernels):
                 "frac": round(tflops / F16_PEAK_TFLOPS, 4), "useful_peak": F16_PEAK_TFLOPS / 2,
                 "frac_of_useful": round(tflops / (F16_PEAK_TFLOPS / 2), 4)}
         kind = "mfma"
-    elif "GEMM_EXACT" in kernels or "GEMM_EXACT_SPLIT" in kernels:
+    elif any(k.startswith("GEMM_EXACT") for k in kernels):
         roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(tflops / FP32_PEAK_TFLOPS, 4)}
         kind = "exact"
@@ -1138,26 +1140,26 @@ def main():
             # projection: split along K (the reference's measured gate, 2/1 up
             # to 64 workgroups) as AUTO runs it, on the matrix cores' fused
             # multiply-add, and on the VALU tile; unsplit, as a product with
-            # options or without range sums runs, on the short-step tile AUTO
-            # takes (8 rows x 32 tokens, K split among a workgroup's waves: 256
-            # workgroups) and on the 128-row tile (16 workgroups); on the
+            # options or without range sums runs, on the matrix-core short-step
+            # tile AUTO takes (32 rows x 32 tokens, K split among a workgroup's
+            # eight waves: 64 workgroups) and on the VALU short-step tile
+            # CANONICAL takes (8 rows x 32 tokens: 256 workgroups); on the
             # split-f16 matrix cores. Then the same step's gated gate/up
-            # product, which never splits: the short-step tile and the 128-row
-            # tile.
+            # product, which never splits, on both short-step tiles.
             plan = [("write", [(2048, 8192)])]
             out["c6_split"] = run_gemm(S, "c6_split", plan, 32, args.steps, args.warmup, rng,
                                        S.mm.GemmPath.AUTO, gate=S.mm.kSplitGate)
             out["c6_split128"] = run_gemm(S, "c6_split128", plan, 32, args.steps, args.warmup, rng,
                                           S.mm.GemmPath.CANONICAL, gate=S.mm.kSplitGate)
             out["c6_tiled"] = run_gemm(S, "c6_tiled", plan, 32, args.steps, args.warmup, rng, S.mm.GemmPath.AUTO)
-            out["c6_tiled128"] = run_gemm(S, "c6_tiled128", plan, 32, args.steps, args.warmup, rng,
-                                          S.mm.GemmPath.CANONICAL)
+            out["c6_tiled_valu"] = run_gemm(S, "c6_tiled_valu", plan, 32, args.steps, args.warmup, rng,
+                                            S.mm.GemmPath.CANONICAL)
             out["c6_mfma"] = run_gemm(S, "c6_mfma", plan, 32, args.steps, args.warmup, rng,
                                       S.mm.GemmPath.SPLIT_F16_MFMA)
             gated = [("gated", [(8192, 2048), (8192, 2048)])]
             out["c6_gated"] = run_gemm(S, "c6_gated", gated, 32, args.steps, args.warmup, rng, S.mm.GemmPath.AUTO)
-            out["c6_gated128"] = run_gemm(S, "c6_gated128", gated, 32, args.steps, args.warmup, rng,
-                                          S.mm.GemmPath.CANONICAL)
+            out["c6_gated_valu"] = run_gemm(S, "c6_gated_valu", gated, 32, args.steps, args.warmup, rng,
+                                            S.mm.GemmPath.CANONICAL)
         if "c7" in only:
             # The embedding gather of Qwen3 0.6B's tied Q6_K table: a
             # 512-token prefill step and a decode step.

@@ -230,9 +230,10 @@ Verdict describe(const charlotte_hip_matmul_desc* desc, uint32_t tokens, const c
 // token or the head's last; else the split along K when the gate allows the
 // step and its range sums fit `range_sums_bytes` (a product with options, or
 // gated, never splits: matmul.cpp:166-172, 233-241); else a tile in the
-// canonical order (the matrix cores' fused multiply-add, the short-step tile
-// or the 128-row VALU tile), or the split-f16 matrix cores when the target
-// asks for them.
+// canonical order (AUTO and EXACT_MFMA: the matrix cores' fused multiply-add,
+// whole or split in the workgroup for a short step; CANONICAL: the 128-row
+// VALU tile or the VALU short-step tile), or the split-f16 matrix cores when
+// the target asks for them.
 Verdict plan_product(const chm::Product& a, uint32_t format, const Target& t, charlotte_hip_matmul_split_gate gate,
                      uint64_t range_sums_bytes, chm::Plan* plan) {
     *plan = chm::Plan{};
@@ -262,7 +263,12 @@ Verdict plan_product(const chm::Product& a, uint32_t format, const Target& t, ch
         split = a.tokens <= most;
     }
     chm::plan_gemm_canonical(a, t.compute_units, split, plan);
-    if (t.gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_CANONICAL) return {};
+    if (t.gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_CANONICAL) {
+        // the VALU tiles: the short-step tile where the 128-row tiles would
+        // be fewer than the compute units
+        if (!split && plan->tiles < t.compute_units) chm::plan_gemm_short(a, t.compute_units, plan);
+        return {};
+    }
     if (split) {
         // the split on the matrix cores' fused multiply-add: the same range
         // sums, the same combine
@@ -273,15 +279,16 @@ Verdict plan_product(const chm::Product& a, uint32_t format, const Target& t, ch
     chm::plan_gemm_exact(a, format, t.compute_units, false, &exact);
     // AUTO: the matrix cores' fused multiply-add tile where the step gives it
     // at least two waves a compute unit (below that each of its waves' walk
-    // through K is the step's time: measured slower than the short-step tile
-    // at 256 waves, faster at 512); else, a step the 128-row tile leaves short
-    // of one workgroup a compute unit: the short-step tile, K split among its
-    // waves. The same bits whichever runs.
+    // through K is the step's time: measured slower than the short-step
+    // tiles at 256 waves, faster at 512); else the short-step form on the
+    // matrix cores, K split among a workgroup's waves (measured faster than
+    // the VALU short-step tile at every short step tried). The same bits
+    // whichever runs.
     const uint64_t exact_waves = uint64_t{(a.rows + 63) / 64} * exact.token_tiles;
     if (t.gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_EXACT_MFMA || exact_waves >= 2ull * t.compute_units)
         *plan = exact;
-    else if (plan->tiles < t.compute_units)
-        chm::plan_gemm_short(a, t.compute_units, plan);
+    else
+        chm::plan_gemm_exact_short(a, plan);
     return {};
 }
 
@@ -548,6 +555,7 @@ static Status run_plan(charlotte_hip_matmul_context* ctx, const chm::Product& a,
         case chm::kGemmShort: e = chm::launch_gemm_short(a, format, plan, s); break;
         case chm::kGemmExact: e = chm::launch_gemm_exact(a, format, plan, nullptr, s); break;
         case chm::kGemmExactSplit: e = chm::launch_gemm_exact(a, format, plan, range_sums, s); break;
+        case chm::kGemmExactShort: e = chm::launch_gemm_exact_short(a, format, plan, s); break;
         case chm::kGemmSplit: e = chm::launch_gemm_canonical(a, format, plan, range_sums, s); break;
         default: e = chm::launch_gemv(a, format, plan, ctx->compute_units, s); break;
     }

@@ -37,6 +37,7 @@ namespace chm {
 namespace {
 
 typedef float f32x32 __attribute__((ext_vector_type(32)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kWaveRows = 64;   // rows a wave
 constexpr uint32_t kWaves = 4;       // waves a workgroup, each its own 64 rows
@@ -291,6 +292,138 @@ __global__ __launch_bounds__(256, 2) void gemm_exact(Product a, uint32_t token_t
     }
 }
 
+
+// gemm_exact_short — a short step on the matrix cores: the canonical order
+// with K split among a workgroup's waves, as gemm_short splits it on the
+// VALU. A step of few tokens gives gemm_exact few waves, each walking all of
+// K as one chain of dependent matrix instructions (C6's 2,048 x 8,192 at 32
+// tokens: 32 waves); here a workgroup takes 32 rows x 32 tokens and its
+// eight waves four of the 32 ranges each, every range's chain on
+// v_mfma_f32_16x16x1_4b_f32 (K = 1, four 16 x 16 blocks, one fused
+// multiply-add an element: checked as the two-block instruction is): block b
+// rows R + 16 (b % 2) .. + 15 against tokens T + 16 (b / 2) .. + 15; lane l
+// supplies row R + l % 32 as A and token T + 16 (l / 32) + l % 16 as B, and
+// register v holds block v / 4's row 4 (l / 16) + v % 4, column l % 16. Each
+// range's sums go to LDS ([range][register][lane]: 128 KB, one workgroup a
+// CU), and after the barrier thread (wave w, lane l) adds registers 2w and
+// 2w + 1 of lane l — rows p, p + 1 of one token — over the 32 ranges in
+// order from zero, skipping empty ones (G < 32): gemm_canonical's order, its
+// bits; a gated pair's totals meet in the thread.
+constexpr uint32_t kShortWaves = 8;  // waves a workgroup, four ranges each
+constexpr uint32_t kShortTile = 32;  // rows, and tokens, a workgroup
+
+template <uint32_t F, bool FULL, bool CLIP>
+__global__ __launch_bounds__(64 * kShortWaves, 1) void gemm_exact_short(Product a, uint32_t token_tiles) {
+    __shared__ float sums[32 * 16 * 64];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t T = (blockIdx.x % token_tiles) * kShortTile, R = (blockIdx.x / token_tiles) * kShortTile;
+    const uint32_t G = a.groups;
+    const uint64_t K = static_cast<uint64_t>(G) * 32;
+    const uint32_t r_begin = 4 * wave, r_end = r_begin + 4;
+    const uint32_t g_begin = range_lo(r_begin, G), g_end = range_lo(r_end, G);
+
+    if (g_begin < g_end) {
+        // Rows and tokens past the product read its last row or token; their
+        // outputs are never stored.
+        const Piece pc = piece_of(a, min(R + (lane & 31u), a.rows - 1));
+        const uint64_t row0 = static_cast<uint64_t>(pc.row) * G;
+        const uint32_t my_token = T + 16 * (lane >> 5) + (lane & 15u);
+        const float4* xrow =
+            reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(min(my_token, a.tokens - 1)) * K);
+        float lo = 0.0f, hi = 0.0f;
+        if constexpr (CLIP) lo = *a.clip[0], hi = *a.clip[1];
+        uint32_t next_r = r_begin + 1;
+        while (next_r < r_end && range_lo(next_r, G) <= g_begin) ++next_r;
+        struct Buffer {
+            Raw<F> raw;
+            float4 xq[8];
+        };
+        auto fetch = [&](Buffer& b, uint32_t g) {
+            b.raw.load(pc.piece, pc.blocks, row0 + g);
+#pragma unroll
+            for (int v = 0; v < 8; ++v) b.xq[v] = xrow[8 * g + v];
+        };
+        f32x16 s = {};
+        bool fresh = true;
+        auto group = [&](const Buffer& b, uint32_t g) {
+            float w[32], x[32];
+            weights_of(b.raw, w);
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+                float4 q = b.xq[v];
+                if constexpr (CLIP) {
+                    q.x = clamp_to(q.x, lo, hi);
+                    q.y = clamp_to(q.y, lo, hi);
+                    q.z = clamp_to(q.z, lo, hi);
+                    q.w = clamp_to(q.w, lo, hi);
+                }
+                x[4 * v] = q.x;
+                x[4 * v + 1] = q.y;
+                x[4 * v + 2] = q.z;
+                x[4 * v + 3] = q.w;
+            }
+            // a range's first product takes +0 as its accumulator
+            if (fresh) {
+                const f32x16 zero = {};
+                s = __builtin_amdgcn_mfma_f32_16x16x1f32(w[0], x[0], zero, 0, 0, 0);
+            } else {
+                s = __builtin_amdgcn_mfma_f32_16x16x1f32(w[0], x[0], s, 0, 0, 0);
+            }
+#pragma unroll
+            for (int k = 1; k < 32; ++k) s = __builtin_amdgcn_mfma_f32_16x16x1f32(w[k], x[k], s, 0, 0, 0);
+            fresh = g + 1 == range_lo(next_r, G);
+            if (fresh) {  // range next_r - 1 ends: its sums to LDS
+                float* slot = sums + (next_r - 1) * 1024 + lane;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const float e = s[v];
+                    slot[64 * v] = e;
+                }
+                while (next_r < r_end && range_lo(next_r, G) <= g + 1) ++next_r;
+            }
+        };
+        Buffer A, B;
+        fetch(A, g_begin);
+        for (uint32_t g = g_begin; g < g_end; g += 2) {
+            fetch(B, min(g + 1, g_end - 1));
+            group(A, g);
+            if (g + 1 >= g_end) break;
+            fetch(A, min(g + 2, g_end - 1));
+            group(B, g + 1);
+        }
+    }
+    __syncthreads();
+
+    // The ordered combine: registers 2 wave and 2 wave + 1 of `lane`.
+    const uint32_t v0 = 2 * wave;
+    float ta = 0.0f, tb = 0.0f;
+#pragma unroll
+    for (uint32_t r = 0; r < 32; ++r) {
+        if (range_lo(r, G) < range_lo(r + 1, G)) {
+            ta = ta + sums[r * 1024 + 64 * v0 + lane];
+            tb = tb + sums[r * 1024 + 64 * (v0 + 1) + lane];
+        }
+    }
+    const uint32_t token = T + 16 * (v0 / 8) + (lane & 15u);
+    const uint32_t p = R + 16 * ((v0 / 4) & 1) + 4 * (lane >> 4) + (v0 & 3);
+    if (token < a.tokens) {
+        if (p < a.rows) emit<FULL>(a, p, token, token, ta, tb);
+        if (p + 1 < a.rows) emit<FULL>(a, p + 1, token, token, tb, 0.0f);
+    }
+}
+
+template <uint32_t F>
+void go_exact_short(const Product& a, const Plan& plan, hipStream_t stream) {
+    const dim3 grid(static_cast<uint32_t>(plan.workgroups)), block(64 * kShortWaves);
+    const uint32_t tt = plan.token_tiles;
+    if (plain_epilogue(a))
+        hipLaunchKernelGGL((gemm_exact_short<F, false, false>), grid, block, 0, stream, a, tt);
+    else if (!clipped(a))
+        hipLaunchKernelGGL((gemm_exact_short<F, true, false>), grid, block, 0, stream, a, tt);
+    else
+        hipLaunchKernelGGL((gemm_exact_short<F, true, true>), grid, block, 0, stream, a, tt);
+}
+
 template <uint32_t F, uint32_t TT>
 void go_exact_tile(const Product& a, const Plan& plan, float* range_sums, hipStream_t stream) {
     const dim3 grid(static_cast<uint32_t>(plan.workgroups)), block(64 * kWaves);
@@ -354,6 +487,35 @@ void plan_gemm_exact(const Product& a, uint32_t format, uint32_t compute_units, 
     }
     plan->chunks = chunks;
     plan->workgroups = plan->tiles * chunks;
+}
+
+// The short-step form: workgroups of 32 rows x 32 tokens, token tile first.
+void plan_gemm_exact_short(const Product& a, Plan* plan) {
+    *plan = Plan{};
+    plan->kernel = kGemmExactShort;
+    plan->launches = 1;
+    plan->tile_tokens = kShortTile;
+    plan->tile_rows = kShortTile;
+    plan->token_tiles = (a.tokens + kShortTile - 1) / kShortTile;
+    plan->row_tiles = (a.rows + kShortTile - 1) / kShortTile;
+    plan->wave_rows = 1;
+    plan->wave_tokens = 1;
+    plan->tiles = static_cast<uint64_t>(plan->token_tiles) * plan->row_tiles;
+    plan->workgroups = plan->tiles;
+}
+
+hipError_t launch_gemm_exact_short(const Product& a, uint32_t format, const Plan& plan, hipStream_t stream) {
+    switch (format) {
+        case kQ4_0: go_exact_short<kQ4_0>(a, plan, stream); break;
+        case kQ4_1: go_exact_short<kQ4_1>(a, plan, stream); break;
+        case kQ8_0: go_exact_short<kQ8_0>(a, plan, stream); break;
+        case kQ6_K: go_exact_short<kQ6_K>(a, plan, stream); break;
+        case kF32: go_exact_short<kF32>(a, plan, stream); break;
+        case kF16: go_exact_short<kF16>(a, plan, stream); break;
+        case kBF16: go_exact_short<kBF16>(a, plan, stream); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 // The tile; with `range_sums` (the split plan: room for 32 x tokens x rows

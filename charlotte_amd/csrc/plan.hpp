@@ -30,6 +30,7 @@ enum Kernel : uint32_t {
     kGemmShort = 19,    // prefill of a short step: 16 or 8 rows x 32 tokens, K split among the waves
     kGemmExact = 20,    // prefill on the matrix cores' K = 1 f32 instruction, the canonical order
     kGemmExactSplit = 21,  // the same split along K, then the ordered combine
+    kGemmExactShort = 22,  // a short step on the matrix cores: 32 x 32, K split among 8 waves
 };
 
 struct Plan {
@@ -81,6 +82,8 @@ hipError_t launch_gemm_short(const Product& a, uint32_t format, const Plan& plan
 // Prefill on the matrix cores in the canonical order (gemm_exact.hip):
 // every format, every epilogue, the VALU tile's bits.
 void plan_gemm_exact(const Product& a, uint32_t format, uint32_t compute_units, bool split, Plan* plan);
+void plan_gemm_exact_short(const Product& a, Plan* plan);
+hipError_t launch_gemm_exact_short(const Product& a, uint32_t format, const Plan& plan, hipStream_t stream);
 hipError_t launch_gemm_exact(const Product& a, uint32_t format, const Plan& plan, float* range_sums,
                              hipStream_t stream);
 

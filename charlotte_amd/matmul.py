@@ -73,12 +73,14 @@ class Rows(enum.IntEnum):
 
 
 class GemmPath(enum.IntEnum):
-    """The prefill kernel: AUTO (the default) and CANONICAL are bit-exact —
-    AUTO takes the short-step tile (GEMM_SHORT) where the 128-row tile would
-    leave compute units idle, CANONICAL always the 128-row tile; EXACT_MFMA runs
-    every step that does not split on the matrix cores' f32 fused multiply-add
-    (GEMM_EXACT), the same bits; SPLIT_F16_MFMA, only when asked for, the matrix
-    cores within 1e-5."""
+    """The prefill kernel: AUTO (the default), CANONICAL and EXACT_MFMA are
+    bit-exact — AUTO runs the matrix cores' f32 fused multiply-add, whole
+    (GEMM_EXACT) from two waves a compute unit, else split in the workgroup
+    (GEMM_EXACT_SHORT), and its split along K (GEMM_EXACT_SPLIT); CANONICAL
+    keeps to the VALU (the 128-row tile, the short-step tile GEMM_SHORT where
+    the 128-row tiles would leave compute units idle, GEMM_SPLIT); EXACT_MFMA
+    runs every step that does not split on GEMM_EXACT; SPLIT_F16_MFMA, only
+    when asked for, the matrix cores within 1e-5."""
 
     AUTO = 0
     CANONICAL = 1
@@ -103,6 +105,7 @@ class Kernel(enum.IntEnum):
     GEMM_SHORT = 19
     GEMM_EXACT = 20
     GEMM_EXACT_SPLIT = 21
+    GEMM_EXACT_SHORT = 22
 
 
 class GemvPath(enum.IntEnum):

@@ -121,14 +121,16 @@ typedef enum {
  * step that does not split, AUTO takes the matrix cores' K = 1 f32
  * instruction (GEMM_EXACT: each range's chain one fused multiply-add a k, as
  * the VALU tile adds it, on 64-row waves) where the step gives it at least
- * two waves a compute unit; else the short-step tile (GEMM_SHORT: 16 or 8
- * rows by 32 tokens, K split among a workgroup's waves) where the 128-row
- * tiles would number fewer than the compute units; else the 128-row VALU
- * tile. A step that splits runs its chunks of ranges on the same matrix-core
- * chains under AUTO and EXACT_MFMA (GEMM_EXACT_SPLIT), on the 128-row VALU
- * tile under CANONICAL (GEMM_SPLIT); the same range sums, the same combine.
- * CANONICAL always takes the 128-row tile; EXACT_MFMA always GEMM_EXACT.
- * All three give the same bits.
+ * two waves a compute unit; else the same chains split among a workgroup's
+ * waves (GEMM_EXACT_SHORT: 32 rows by 32 tokens, eight waves of four ranges,
+ * the range sums combined in LDS). A step that splits runs its chunks of
+ * ranges on the matrix-core chains under AUTO and EXACT_MFMA
+ * (GEMM_EXACT_SPLIT), on the 128-row VALU tile under CANONICAL (GEMM_SPLIT);
+ * the same range sums, the same combine. CANONICAL keeps to the VALU: the
+ * 128-row tile, or the short-step tile (GEMM_SHORT: 16 or 8 rows by 32
+ * tokens, K split among a workgroup's waves) where the 128-row tiles would
+ * number fewer than the compute units. EXACT_MFMA always GEMM_EXACT. All
+ * three give the same bits.
  * SPLIT_F16_MFMA, only when asked for, runs the products on the matrix cores
  * with x split into two f16 parts, within the tolerance max|err| / max|y| <=
  * 1e-5 but not bit-exact and not batch-invariant with decode; it needs a
@@ -316,7 +318,8 @@ typedef enum {
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_MFMA = 18,    /* prefill on the matrix cores (x split into two f16 parts) */
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_SHORT = 19,   /* prefill of a short step: 16 or 8 rows x 32 tokens, K split in the workgroup */
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_EXACT = 20,   /* prefill on the matrix cores' f32 fused multiply-add, the canonical order */
-    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_EXACT_SPLIT = 21 /* the same split along K, then the ordered combine */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_EXACT_SPLIT = 21, /* the same split along K, then the ordered combine */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_EXACT_SHORT = 22  /* a short step on the matrix cores: 32 x 32, K split in the workgroup */
 } charlotte_hip_matmul_kernel;
 
 /* What a plan is made for: the device's compute units (256 on MI355X) and

@@ -127,7 +127,7 @@ def test_write_clamped_biased_activated_in_place(oracle, ctx, span, source):
     m = mm.MatmulLaunch([mm.Member(w)], 0x10000, [0x20000], clip=ptrs, bias=buf.ptr + bias_t.offset, activated=True,
                         activation=mm.Activation.SiLU)
     plan = mm.plan_launch(m, 33, gate=mm.kAlways, range_sums_bytes=1 << 24)
-    assert plan.kernel == mm.Kernel.GEMM_SHORT
+    assert plan.kernel == mm.Kernel.GEMM_EXACT_SHORT
     _check(_run(ctx, m, x, 33, 48, gate=mm.kAlways, sums_bytes=1 << 24), want, "prefilled")
     _check(_run(ctx, m, x[7:8], 1, 48)[0], want[7], "token 7 decoded")
     w.free()

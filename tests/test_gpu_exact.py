@@ -221,3 +221,100 @@ def test_split_qkv_same_bits_as_the_valu_split(ctxs):
     got, want = _both(ctxs, qkv_members, x, tokens, [2048, 512, 512], epilogue=mm.Epilogue.QKV, gate=mm.kAlways,
                       sums_bytes=sums)
     _same(got, want, "qkv split")
+
+
+@pytest.fixture(scope="module")
+def short_ctxs():
+    """AUTO (the matrix-core short-step tile for short steps) and CANONICAL
+    (the VALU short-step tile)."""
+    from charlotte_amd import matmul as mm
+
+    auto, tile = mm.Context(0), mm.Context(0)
+    tile.set_gemm_path(mm.GemmPath.CANONICAL)
+    yield auto, tile
+    auto.close()
+    tile.close()
+
+
+@pytest.mark.parametrize("gtype,rows,columns,tokens", [
+    (Q4_0, 2048, 8192, 32),      # C6's down projection, unsplit: 64 workgroups
+    (Q4_0, 1001, 2048, 45),      # ragged rows and tokens
+    (Q6_K, 3072, 1152, 9),
+    (Q4_0, 1000, 14336, 33),     # 448 groups: 56 a wave
+    (Q4_0, 333, 64, 20),         # 2 groups: 30 empty ranges, waves holding none
+    (Q8_0, 700, 2048, 17),
+    (Q4_1, 520, 1024, 5),
+    (F32, 300, 1024, 12),
+])
+def test_short_step_tile_same_bits_as_the_valu_short_tile(short_ctxs, gtype, rows, columns, tokens):
+    """GEMM_EXACT_SHORT (each wave four of a 32 x 32 tile's ranges on the
+    16x16x1 four-block instruction, the sums combined in LDS) against the
+    VALU short-step tile, bit for bit."""
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+
+    rng = np.random.default_rng(rows + columns + tokens + 11)
+    if gtype == F32:
+        stored = (rng.standard_normal((rows, columns)).astype(np.float32) * np.float32(0.05)).tobytes()
+    else:
+        stored = synthetic.weight(rng, gtype, rows, columns)
+    x = synthetic.activations(rng, tokens, columns)
+    shape = mm.MatmulLaunch([mm.Member(mm.Weight.shape(gtype, rows, columns))], 16, [16])
+    assert mm.plan_launch(shape, tokens).kernel == mm.Kernel.GEMM_EXACT_SHORT
+
+    def members(ctx):
+        w = _weight(ctx, gtype, rows, columns, stored)
+        return [mm.Member(w)], [w]
+
+    got, want = _both(short_ctxs, members, x, tokens, [rows])
+    _same(got, want, f"short type {gtype} {rows}x{columns} tokens={tokens}")
+
+
+@pytest.mark.parametrize("activation", [0, 1])
+def test_short_step_tile_epilogues_same_bits(short_ctxs, activation):
+    """A gated gate/up pair (Llama 3.2 1B's, 32 tokens), a fused QKV, a Write
+    with clip, bias and activation, and GatedByInput, on both short tiles."""
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+
+    rng = np.random.default_rng(60 + activation)
+    tokens = 32
+    x = synthetic.activations(rng, tokens, 2048)
+    gate, up = (synthetic.weight(rng, Q4_0, 8192, 2048) for _ in range(2))
+
+    def gated(ctx):
+        ws = [_weight(ctx, Q4_0, 8192, 2048, s) for s in (gate, up)]
+        return [mm.Member(w) for w in ws], ws
+
+    got, want = _both(short_ctxs, gated, x, tokens, [8192], epilogue=mm.Epilogue.GatedActivation,
+                      activation=activation)
+    _same(got, want, f"gated act={activation}")
+    parts = [synthetic.weight(rng, Q4_0, r, 2048) for r in (2048, 512, 512)]
+
+    def qkv(ctx):
+        ws = [_weight(ctx, Q4_0, r, 2048, s) for r, s in zip((2048, 512, 512), parts)]
+        return [mm.Member(w) for w in ws], ws
+
+    got, want = _both(short_ctxs, qkv, x[:24], 24, [2048, 512, 512], epilogue=mm.Epilogue.QKV)
+    _same(got, want, "qkv")
+    tokens, columns = 77, 1024
+    x = synthetic.activations(rng, tokens, columns)
+    a_s = synthetic.weight(rng, Q4_0, 300, columns)
+    bias = rng.standard_normal(300).astype(np.float32)
+
+    def opts(ctx):
+        w = _weight(ctx, Q4_0, 300, columns, a_s)
+        return [mm.Member(w)], [w]
+
+    got, want = _both(short_ctxs, opts, x, tokens, [300], clip=[-1.5, 1.25, -3.0, 2.5], bias=bias, activated=True,
+                      activation=activation)
+    _same(got, want, f"write with options act={activation}")
+    u = rng.standard_normal((tokens, 500)).astype(np.float32)
+
+    def by_input(ctx):
+        w = _weight(ctx, Q4_0, 300, columns, a_s)
+        return [mm.Member(w, output_row=100)], [w]
+
+    got, want = _both(short_ctxs, by_input, x, tokens, [500], epilogue=mm.Epilogue.GatedByInput,
+                      activation=activation, out_width=500, gate_input=u, gate_input_stride=500, gate_input_column=50)
+    _same(got, want, f"gated by input act={activation}")

@@ -74,7 +74,7 @@ def test_output_rows_that_wrap_32_bits_are_refused(shapes):
     assert "out_width" in _refused(m, 1)
     # Inside: the member's last output is out_width - 1.
     m = mm.MatmulLaunch([mm.Member(w, output_row=100)], X, [Y0], out_width=164)
-    assert mm.plan_launch(m, 2).kernel == K.GEMM_SHORT
+    assert mm.plan_launch(m, 2).kernel == K.GEMM_EXACT_SHORT
     _refused(mm.MatmulLaunch([mm.Member(w, output_row=101)], X, [Y0], out_width=164), 2)
 
 
@@ -98,14 +98,15 @@ def test_clip_takes_four_bound_words_or_none(shapes):
     w = shapes(Q4_0, 64, 1024)
     span = 0x50000
     apart = [span + 32 * i for i in range(4)]
-    assert mm.plan_launch(_write(w, clip=apart), 33).kernel == K.GEMM_SHORT
+    assert mm.plan_launch(_write(w, clip=apart), 33).kernel == K.GEMM_EXACT_SHORT
     assert mm.plan_launch(_write(w, clip=apart[::-1]), 1).kernel != K.NONE
     assert mm.plan_launch(_write(w, clip=[span] * 4), 1).kernel != K.NONE
     for partial in ([span, 0, 0, 0], [span, span + 4, span + 8, 0], [0, 0, 0, span]):
         assert "four bounds or none" in _refused(_write(w, clip=partial), 1)
     assert "4-byte" in _refused(_write(w, clip=[span, span + 2, span + 8, span + 12]), 1)
     # An optioned product never splits (matmul.cpp:166-172), whatever the gate.
-    assert mm.plan_launch(_write(w, clip=apart), 32, gate=mm.kAlways, range_sums_bytes=1 << 24).kernel == K.GEMM_SHORT
+    assert mm.plan_launch(_write(w, clip=apart), 32, gate=mm.kAlways,
+                          range_sums_bytes=1 << 24).kernel == K.GEMM_EXACT_SHORT
     assert mm.plan_launch(_write(w), 32, gate=mm.kAlways, range_sums_bytes=1 << 24).kernel == K.GEMM_EXACT_SPLIT
 
 
@@ -263,7 +264,7 @@ def test_the_matrix_cores_refuse_the_float_formats(shapes):
     w = shapes(F16, 256, 1024)
     target = mm.Target(256, mm.GemmPath.SPLIT_F16_MFMA, workspace_bytes=1 << 30)
     _refused(_write(w), 64, mm.Status.UNSUPPORTED, target=target)
-    assert mm.plan_launch(_write(w), 64).kernel == K.GEMM_SHORT
+    assert mm.plan_launch(_write(w), 64).kernel == K.GEMM_EXACT_SHORT
 
 
 def test_short_steps_split_along_k_when_the_gate_and_range_sums_allow(shapes):
@@ -289,9 +290,9 @@ def test_short_steps_split_along_k_when_the_gate_and_range_sums_allow(shapes):
     assert mm.plan_launch(_write(down), 64, mm.Target(128), gate=mm.kAlways, range_sums_bytes=2 * sums).chunks == 32
     assert mm.plan_launch(_write(down), 64, mm.Target(16), gate=mm.kAlways, range_sums_bytes=2 * sums).chunks == 4
     # Range sums too small for the step, no gate, options or a gated product: a
-    # tile (the short-step tile under AUTO, the 128-row tile under CANONICAL).
+    # short-step tile (on the matrix cores under AUTO, the VALU under CANONICAL).
     canonical = mm.Target(256, mm.GemmPath.CANONICAL)
-    for target, kernel in ((MI355X, K.GEMM_SHORT), (canonical, K.GEMM_TILED)):
+    for target, kernel in ((MI355X, K.GEMM_EXACT_SHORT), (canonical, K.GEMM_SHORT)):
         assert mm.plan_launch(_write(w), 32, target, gate=mm.kAlways, range_sums_bytes=sums // 64).kernel == kernel
         assert mm.plan_launch(_write(w), 32, target, gate=mm.kNever, range_sums_bytes=sums).kernel == kernel
         assert mm.plan_launch(_write(w, bias=Y1), 32, target, gate=mm.kAlways, range_sums_bytes=sums).kernel == kernel
@@ -299,33 +300,45 @@ def test_short_steps_split_along_k_when_the_gate_and_range_sums_allow(shapes):
         assert mm.plan_launch(g, 32, target, gate=mm.kAlways, range_sums_bytes=2 * sums).kernel == kernel
 
 
-def test_short_steps_that_do_not_split_take_the_short_tile_while_the_128_row_tile_underfills(shapes):
-    """C6's 32 tokens through 2,048 x 8,192, unsplit: 16 tiles of 128 rows on
-    256 CUs, so 8-row short tiles, 256 workgroups. A 32-token gated gate/up of
-    Llama 3.2 1B (16,384 interleaved rows): 16-row tiles, 1,024 workgroups. C4
-    (512 x 8,192): 512 tiles of 128 rows, the 128-row tile."""
+def test_short_steps_that_do_not_split_take_a_short_step_tile(shapes):
+    """AUTO: a step that gives the whole-K matrix-core tile fewer than two
+    waves a compute unit runs GEMM_EXACT_SHORT, workgroups of 32 rows x 32
+    tokens whose eight waves split K's ranges: C6's 32 tokens through 2,048 x
+    8,192, 64 workgroups; a 32-token gated gate/up of Llama 3.2 1B (16,384
+    interleaved rows), 512. CANONICAL: the VALU short-step tile where the
+    128-row tiles would be fewer than the compute units (C6: 16 tiles of 128
+    rows on 256 CUs, so 8-row tiles, 256 workgroups; the gated pair 16-row
+    tiles, 1,024 workgroups), else the 128-row tile (C4: 512 tiles)."""
     down = shapes(Q4_0, 2048, 8192)
     p = mm.plan_launch(_write(down), 32)
+    assert (p.kernel, p.canonical, p.tile_rows, p.tile_tokens, p.workgroups) == (K.GEMM_EXACT_SHORT, True, 32, 32, 64)
+    canonical = mm.Target(256, mm.GemmPath.CANONICAL)
+    p = mm.plan_launch(_write(down), 32, canonical)
     assert (p.kernel, p.canonical, p.tile_rows, p.tile_tokens, p.workgroups) == (K.GEMM_SHORT, True, 8, 32, 256)
     gate, up = shapes(Q4_0, 8192, 2048), shapes(Q4_0, 8192, 2048)
     g = mm.MatmulLaunch([mm.Member(gate), mm.Member(up)], X, [Y0], epilogue=mm.Epilogue.GatedActivation)
     p = mm.plan_launch(g, 32)
+    assert (p.kernel, p.tile_rows, p.workgroups) == (K.GEMM_EXACT_SHORT, 32, 512)
+    p = mm.plan_launch(g, 32, canonical)
     assert (p.kernel, p.tile_rows, p.workgroups) == (K.GEMM_SHORT, 16, 1024)
-    assert mm.plan_launch(g, 32, mm.Target(256, mm.GemmPath.CANONICAL)).kernel == K.GEMM_TILED
     assert mm.plan_launch(_write(gate), 512).kernel == K.GEMM_EXACT
-    # 100 tokens over 2,048 rows: 32 tiles of 128 rows; short tiles of 16 rows, 4 x 128 workgroups.
+    assert mm.plan_launch(_write(gate), 512, canonical).kernel == K.GEMM_TILED
+    # 100 tokens over 2,048 rows: 64 x 4 workgroups on the matrix cores; on the
+    # VALU 32 tiles of 128 rows, so short tiles of 16 rows, 4 x 128 workgroups.
     p = mm.plan_launch(_write(down), 100)
+    assert (p.kernel, p.tiles) == (K.GEMM_EXACT_SHORT, 64 * 4)
+    p = mm.plan_launch(_write(down), 100, canonical)
     assert (p.kernel, p.tiles, p.tile_rows) == (K.GEMM_SHORT, 4 * 128, 16)
 
 
 def test_auto_takes_the_exact_matrix_core_tile_from_two_waves_a_compute_unit(shapes):
     """AUTO: GEMM_EXACT where its waves (64 rows by 64 or 32 tokens) number at
-    least 2 x the compute units, else the short-step tile: 2,048 x 2,048 at
-    512 tokens is 512 waves of 64 x 32, at 256 tokens 256 (the measured
-    crossing: 98 against 130 us at 512, 97 against 67 at 256)."""
+    least 2 x the compute units, else the matrix-core short-step tile: 2,048 x
+    2,048 at 512 tokens is 512 waves of 64 x 32, at 256 tokens 256 (the
+    measured crossing: 89 against 46 us at 256 tokens)."""
     w = shapes(Q4_0, 2048, 2048)
     assert mm.plan_launch(_write(w), 512).kernel == K.GEMM_EXACT
-    assert mm.plan_launch(_write(w), 256).kernel == K.GEMM_SHORT
+    assert mm.plan_launch(_write(w), 256).kernel == K.GEMM_EXACT_SHORT
     assert mm.plan_launch(_write(w), 1024).kernel == K.GEMM_EXACT
     assert mm.plan_launch(_write(w), 512, mm.Target(128)).kernel == K.GEMM_EXACT  # 2 x 128 CUs: 256 waves
     assert mm.plan_launch(_write(w), 256, mm.Target(128)).kernel == K.GEMM_EXACT

@@ -81,7 +81,7 @@ def test_static_launch_decodes_and_tiles_as_the_launch(ctx, oracle):
     assert plan.kernel == mm.Kernel.GEMV_RANGES and _same(a, want) and _same(b, a)
     print("no-alloc: tiled (no split gate), Q4_0 256 x 1024, 100 tokens", flush=True)
     plan, a, b, want = _both(ctx, Q4_0, 256, 1024, 100, 4, oracle, gate=mm.kNever)
-    assert plan.kernel == mm.Kernel.GEMM_SHORT and _same(a, want) and _same(b, a)
+    assert plan.kernel == mm.Kernel.GEMM_EXACT_SHORT and _same(a, want) and _same(b, a)
 
 
 def test_static_launch_tiles_a_split_past_its_array(ctx, oracle):
@@ -104,7 +104,7 @@ def test_static_launch_tiles_a_split_past_its_array(ctx, oracle):
     m = mm.MatmulLaunch([mm.Member(w)], xb.ptr, [yb.ptr])
     assert mm.plan_launch(m, tokens, gate=mm.kAlways, range_sums_bytes=1 << 40).kernel == mm.Kernel.GEMM_EXACT_SPLIT
     assert mm.plan_launch(m, tokens, gate=mm.kAlways,
-                          range_sums_bytes=mm.STATIC_SCRATCH_BYTES).kernel == mm.Kernel.GEMM_SHORT
+                          range_sums_bytes=mm.STATIC_SCRATCH_BYTES).kernel == mm.Kernel.GEMM_EXACT_SHORT
     mm.launch_static(ctx, m, tokens, mm.kAlways)
     hx.sync()
     got = yb.read(np.float32).reshape(tokens, rows)
