@@ -31,6 +31,7 @@
 #include "decode.hpp"
 #include "plan.hpp"
 #include "product.hpp"
+#include "stream.hpp"
 
 namespace chm {
 
@@ -303,65 +304,98 @@ __global__ __launch_bounds__(256, 2) void gemm_exact(Product a, uint32_t token_t
 // multiply-add an element: checked as the two-block instruction is): block b
 // rows R + 16 (b % 2) .. + 15 against tokens T + 16 (b / 2) .. + 15; lane l
 // supplies row R + l % 32 as A and token T + 16 (l / 32) + l % 16 as B, and
-// register v holds block v / 4's row 4 (l / 16) + v % 4, column l % 16. Each
-// range's sums go to LDS ([range][register][lane]: 128 KB, one workgroup a
-// CU), and after the barrier thread (wave w, lane l) adds registers 2w and
-// 2w + 1 of lane l — rows p, p + 1 of one token — over the 32 ranges in
-// order from zero, skipping empty ones (G < 32): gemm_canonical's order, its
-// bits; a gated pair's totals meet in the thread.
+// register v holds block v / 4's row 4 (l / 16) + v % 4, column l % 16.
+//
+// A group's inputs (32 tokens x 128 bytes) reach a wave's LDS stage by four
+// copies (global_load_lds, 1 KB each: 8 tokens' whole lines), where loading
+// them into registers took eight loads a group touching 32 lines each (the
+// kernel's bound: 76 -> 47 us at C6 without them); token t's 16-byte chunk c
+// lies at position c ^ (t % 8) of its 128 bytes, so a read of one chunk for
+// 32 tokens spreads over the banks. A wave keeps its four ranges' sums in
+// registers through K; then, after a barrier, the stages' LDS holds the
+// range sums ([range][register][lane]: 128 KB, one workgroup a CU), and
+// after a second each thread adds two registers' 32 range sums in order from
+// zero, skipping empty ones (G < 32) — rows p, p + 1 of one token, so a
+// gated pair's totals meet in the thread: gemm_canonical's order, its bits.
 constexpr uint32_t kShortWaves = 8;  // waves a workgroup, four ranges each
 constexpr uint32_t kShortTile = 32;  // rows, and tokens, a workgroup
 
 template <uint32_t F, bool FULL, bool CLIP>
 __global__ __launch_bounds__(64 * kShortWaves, 1) void gemm_exact_short(Product a, uint32_t token_tiles) {
-    __shared__ float sums[32 * 16 * 64];
+    __shared__ float4 lds[32 * 16 * 64 / 4];  // the stages (64 KB), then the range sums (128 KB)
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t T = (blockIdx.x % token_tiles) * kShortTile, R = (blockIdx.x / token_tiles) * kShortTile;
     const uint32_t G = a.groups;
     const uint64_t K = static_cast<uint64_t>(G) * 32;
     const uint32_t r_begin = 4 * wave, r_end = r_begin + 4;
     const uint32_t g_begin = range_lo(r_begin, G), g_end = range_lo(r_end, G);
+    f32x16 held[4] = {};  // the wave's range sums, range r_begin + q in held[q]
 
     if (g_begin < g_end) {
         // Rows and tokens past the product read its last row or token; their
         // outputs are never stored.
         const Piece pc = piece_of(a, min(R + (lane & 31u), a.rows - 1));
         const uint64_t row0 = static_cast<uint64_t>(pc.row) * G;
-        const uint32_t my_token = T + 16 * (lane >> 5) + (lane & 15u);
-        const float4* xrow =
-            reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(min(my_token, a.tokens - 1)) * K);
+        // copy i: token 8 i + lane / 8, its chunk (lane % 8) ^ (token % 8)
+        const float4* src[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t tok = 8 * i + (lane >> 3);
+            src[i] = reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(min(T + tok, a.tokens - 1)) * K) +
+                     ((lane & 7u) ^ (tok & 7u));
+        }
+        const uint32_t my_tok = 16 * (lane >> 5) + (lane & 15u);
+        float4* const stages = lds + wave * 512;  // two stages of 256 chunks
+        const uint32_t read_at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(stages)) + 128 * my_tok;
         float lo = 0.0f, hi = 0.0f;
         if constexpr (CLIP) lo = *a.clip[0], hi = *a.clip[1];
         uint32_t next_r = r_begin + 1;
         while (next_r < r_end && range_lo(next_r, G) <= g_begin) ++next_r;
-        struct Buffer {
-            Raw<F> raw;
-            float4 xq[8];
-        };
-        auto fetch = [&](Buffer& b, uint32_t g) {
-            b.raw.load(pc.piece, pc.blocks, row0 + g);
+        // A group's copies go out before its weights' loads (and nothing may
+        // move between them); its weights are waited for (the compiler's
+        // wait) before the next group's loads go out, so that wait covers the
+        // copies too and leaves the next group's loads in flight.
+        auto fetch = [&](Raw<F>& raw, uint32_t stage, uint32_t g) {
 #pragma unroll
-            for (int v = 0; v < 8; ++v) b.xq[v] = xrow[8 * g + v];
+            for (int i = 0; i < 4; ++i)
+                __builtin_amdgcn_global_load_lds(src[i] + 8 * g, (lds_void)(stages + 256 * stage + 64 * i), 16, 0, 0);
+            __asm__ __volatile__("" ::: "memory");
+            raw.load(pc.piece, pc.blocks, row0 + g);
         };
         f32x16 s = {};
         bool fresh = true;
-        auto group = [&](const Buffer& b, uint32_t g) {
+        auto group = [&](const Raw<F>& raw, uint32_t stage, uint32_t g, auto&& next) {
             float w[32], x[32];
-            weights_of(b.raw, w);
+            weights_of(raw, w);
+            // the stage's reads, after the weights (whose loads were waited
+            // for): the last weight is an input the reads do not use
+            u32x4s_t q[8];
+            const uint32_t at = read_at + 4096 * stage;
+            const uint32_t sw = my_tok & 7u;
 #pragma unroll
-            for (int v = 0; v < 8; ++v) {
-                float4 q = b.xq[v];
-                if constexpr (CLIP) {
-                    q.x = clamp_to(q.x, lo, hi);
-                    q.y = clamp_to(q.y, lo, hi);
-                    q.z = clamp_to(q.z, lo, hi);
-                    q.w = clamp_to(q.w, lo, hi);
-                }
-                x[4 * v] = q.x;
-                x[4 * v + 1] = q.y;
-                x[4 * v + 2] = q.z;
-                x[4 * v + 3] = q.w;
+            for (int c = 0; c < 8; ++c) {
+                const uint32_t addr = at + 16 * (c ^ sw);
+                __asm__ __volatile__("ds_read_b128 %0, %1" : "=v"(q[c]) : "v"(addr), "v"(w[31]));
             }
+            __asm__ __volatile__("s_waitcnt lgkmcnt(0)"
+                                 : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(q[4]), "+v"(q[5]),
+                                   "+v"(q[6]), "+v"(q[7]));
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                float4 v = make_float4(__uint_as_float(q[c][0]), __uint_as_float(q[c][1]),
+                                       __uint_as_float(q[c][2]), __uint_as_float(q[c][3]));
+                if constexpr (CLIP) {
+                    v.x = clamp_to(v.x, lo, hi);
+                    v.y = clamp_to(v.y, lo, hi);
+                    v.z = clamp_to(v.z, lo, hi);
+                    v.w = clamp_to(v.w, lo, hi);
+                }
+                x[4 * c] = v.x;
+                x[4 * c + 1] = v.y;
+                x[4 * c + 2] = v.z;
+                x[4 * c + 3] = v.w;
+            }
+            next();  // the next group's loads, in flight under this chain
             // a range's first product takes +0 as its accumulator
             if (fresh) {
                 const f32x16 zero = {};
@@ -372,24 +406,39 @@ __global__ __launch_bounds__(64 * kShortWaves, 1) void gemm_exact_short(Product 
 #pragma unroll
             for (int k = 1; k < 32; ++k) s = __builtin_amdgcn_mfma_f32_16x16x1f32(w[k], x[k], s, 0, 0, 0);
             fresh = g + 1 == range_lo(next_r, G);
-            if (fresh) {  // range next_r - 1 ends: its sums to LDS
-                float* slot = sums + (next_r - 1) * 1024 + lane;
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const float e = s[v];
-                    slot[64 * v] = e;
-                }
+            if (fresh) {  // range next_r - 1 ends: its sums held
+                const uint32_t q_range = next_r - 1 - r_begin;
+                if (q_range == 0) held[0] = s;
+                else if (q_range == 1) held[1] = s;
+                else if (q_range == 2) held[2] = s;
+                else held[3] = s;
                 while (next_r < r_end && range_lo(next_r, G) <= g + 1) ++next_r;
             }
         };
-        Buffer A, B;
-        fetch(A, g_begin);
+        Raw<F> A, B;
+        fetch(A, 0, g_begin);
         for (uint32_t g = g_begin; g < g_end; g += 2) {
-            fetch(B, min(g + 1, g_end - 1));
-            group(A, g);
+            group(A, 0, g, [&] {
+                if (g + 1 < g_end) fetch(B, 1, g + 1);
+            });
             if (g + 1 >= g_end) break;
-            fetch(A, min(g + 2, g_end - 1));
-            group(B, g + 1);
+            group(B, 1, g + 1, [&] {
+                if (g + 2 < g_end) fetch(A, 0, g + 2);
+            });
+        }
+    }
+    // Every copy has landed (each wave waited for its last group's weights,
+    // loaded after its copies, and loads nothing past it) and every stage
+    // read: the LDS takes the range sums, [range][register][lane].
+    __syncthreads();
+    float* const sums = reinterpret_cast<float*>(lds);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float* slot = sums + (r_begin + q) * 1024 + lane;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const float e = held[q][v];
+            slot[64 * v] = e;
         }
     }
     __syncthreads();
