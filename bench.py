@@ -255,22 +255,27 @@ def time_decode_shapes(spec, steps, warmup, settle_ms, limbs=False):
     return out
 
 
+PREFILL_TYPES = {"f32": 0, "f16": 1, "q4_0": 2, "q4_1": 3, "q8_0": 8, "q6_k": 14, "bf16": 30}
+
+
 def time_prefill_shapes(spec, steps, warmup, settle_ms):
-    """One Q4_0 prefill product a shape ROWSxKxTOKENS, timed as the configs
-    are, on each bit-exact path (CANONICAL: the 128-row tile; AUTO; EXACT_MFMA:
-    the matrix cores' fused multiply-add): {"ROWSxKxTOKENS": {path: {us,
-    TFLOP/s, kernel}}}. The figures that choose AUTO's kernel."""
+    """One prefill product a shape [TYPE:]ROWSxKxTOKENS (TYPE a key of
+    PREFILL_TYPES, Q4_0 when absent), timed as the configs are, on each
+    bit-exact path (CANONICAL: the 128-row tile; AUTO; EXACT_MFMA: the matrix
+    cores' fused multiply-add): {"[TYPE:]ROWSxKxTOKENS": {path: {us, TFLOP/s,
+    kernel}}}. The figures that choose AUTO's kernel."""
     S = Setup()
     S.settle_ms = settle_ms
     rng = np.random.default_rng(2)
     out = {}
     try:
         for item in spec.split(","):
-            rows, columns, tokens = (int(v) for v in item.lower().split("x"))
+            kind, _, dims = item.lower().rpartition(":")
+            rows, columns, tokens = (int(v) for v in dims.split("x"))
             row = {}
             for path in (S.mm.GemmPath.CANONICAL, S.mm.GemmPath.AUTO, S.mm.GemmPath.EXACT_MFMA):
                 r = run_gemm(S, f"{item} {path.name}", [("write", [(rows, columns)])], tokens, steps, warmup, rng,
-                             path)
+                             path, gtype=PREFILL_TYPES[kind or "q4_0"])
                 row[path.name] = {"us": round(r["ms_per_step"] * 1e3, 2), "TFLOP/s": round(r["TFLOP/s"], 1),
                                   "kernel": r["kernels"][0]}
             out[item] = row
@@ -756,8 +761,8 @@ def decode_matches_prefill(S, launches, xs, rng, tokens=4):
     return {"decode_prefill_outputs_compared": compared, "decode_prefill_bits_equal": differing == 0}
 
 
-def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=None, breakdown=False):
-    """plan: products (build_products) over `tokens` tokens, on prefill path `path`; with `gate`, the
+def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=None, breakdown=False, gtype=2):
+    """plan: products (build_products, weights of GGUF type `gtype`) over `tokens` tokens, on prefill path `path`; with `gate`, the
     split along K where the gate takes the step (range sums sized for the largest product). With
     `breakdown`, a step of layers of four products and a head: each kind timed in place."""
     from charlotte_amd import synthetic
@@ -765,7 +770,7 @@ def run_gemm(S, name, plan, tokens, steps, warmup, rng, path, head=None, gate=No
     mm = S.mm
     t0 = time.time()
     S.ctx.set_gemm_path(path)
-    launches, xs, _, flops = build_products(S, rng, plan, tokens)
+    launches, xs, _, flops = build_products(S, rng, plan, tokens, gtype)
     launches = [(m, tokens) for m in launches]
     gate = gate or mm.kNever
     sums, sums_bytes = 0, 0
@@ -1031,7 +1036,8 @@ def main():
                         "TYPE a GGUF type number (2 Q4_0, default; 3 Q4_1; 8 Q8_0; 14 Q6_K, repacked)")
     p.add_argument("--limbs", action="store_true", help="with --decode: the INT8_LIMBS decode path")
     p.add_argument("--prefill", metavar="SHAPES",
-                   help="time Q4_0 prefill products ROWSxKxTOKENS (a comma list) on each bit-exact path and exit")
+                   help="time prefill products [TYPE:]ROWSxKxTOKENS (a comma list; TYPE f32, f16, bf16, q4_0 (the "
+                        "default), q4_1, q8_0 or q6_k) on each bit-exact path and exit")
     p.add_argument("--mfma-rate", nargs="?", const="all", default=None,
                    help="time each matrix-core instruction shape's sustained rate (a probe) and exit; "
                         "optionally a comma list of probe shape numbers (0-8)")

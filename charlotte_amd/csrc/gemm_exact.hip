@@ -299,44 +299,53 @@ __global__ __launch_bounds__(256, 2) void gemm_exact(Product a, uint32_t token_t
 // VALU. A step of few tokens gives gemm_exact few waves, each walking all of
 // K as one chain of dependent matrix instructions (C6's 2,048 x 8,192 at 32
 // tokens: 32 waves); here a workgroup takes 32 rows x 32 tokens and its
-// eight waves four of the 32 ranges each, every range's chain on
-// v_mfma_f32_16x16x1_4b_f32 (K = 1, four 16 x 16 blocks, one fused
-// multiply-add an element: checked as the two-block instruction is): block b
-// rows R + 16 (b % 2) .. + 15 against tokens T + 16 (b / 2) .. + 15; lane l
-// supplies row R + l % 32 as A and token T + 16 (l / 32) + l % 16 as B, and
-// register v holds block v / 4's row 4 (l / 16) + v % 4, column l % 16.
+// eight waves four of the 32 ranges each, as two pairs. A pair's two chains
+// run in one v_mfma_f32_32x32x1_2b_f32 (K = 1, two 32 x 32 blocks, one fused
+// multiply-add an element): block b is range r_begin + 2 p + b, its A (row R
+// + l % 32) and B (token T + l % 32) from lanes 32 b .. 32 b + 31, each lane
+// decoding its own range's group, and register v holds block v / 16's row 8
+// ((v % 16) / 4) + 4 (l / 32) + v % 4, column l % 32. Step j of a pair is
+// group j of both ranges; where one range is a group shorter than the other
+// (the two differ by at most one), its block's lanes take -0 and +0 at the
+// pair's last step: fma(-0, +0, acc) is acc for every acc (acc + -0 = acc).
 //
-// A group's inputs (32 tokens x 128 bytes) reach a wave's LDS stage by four
-// copies (global_load_lds, 1 KB each: 8 tokens' whole lines), where loading
-// them into registers took eight loads a group touching 32 lines each (the
-// kernel's bound: 76 -> 47 us at C6 without them); token t's 16-byte chunk c
-// lies at position c ^ (t % 8) of its 128 bytes, so a read of one chunk for
-// 32 tokens spreads over the banks. A wave keeps its four ranges' sums in
-// registers through K; then, after a barrier, the stages' LDS holds the
-// range sums ([range][register][lane]: 128 KB, one workgroup a CU), and
-// after a second each thread adds two registers' 32 range sums in order from
-// zero, skipping empty ones (G < 32) — rows p, p + 1 of one token, so a
-// gated pair's totals meet in the thread: gemm_canonical's order, its bits.
-constexpr uint32_t kShortWaves = 8;  // waves a workgroup, four ranges each
+// A step's inputs (two groups x 32 tokens x 128 bytes) reach the wave's LDS
+// stage by eight copies (global_load_lds, 1 KB each: 8 tokens' whole lines of
+// one group), where loading them into registers took eight loads a group
+// touching 32 lines each; token t's 16-byte chunk c lies at position c ^ (t %
+// 8) of its 128 bytes, so a read of one chunk for 32 tokens spreads over the
+// banks. Two stages a wave: a step's loads are waited for (the compiler's
+// wait, which covers its copies, issued before them) before the next step's
+// go out, in flight under this step's chain. The pairs' sums stay in
+// registers through K; then, after a barrier, the stages' LDS holds the range
+// sums ([range][register][lane]: 128 KB, one workgroup a CU), and after a
+// second each thread adds two registers' 32 range sums in order from zero,
+// skipping empty ones (G < 32) — rows p, p + 1 of one token, so a gated pair's
+// totals meet in the thread: gemm_canonical's order, its bits.
+constexpr uint32_t kShortWaves = 8;  // waves a workgroup, two pairs of ranges each
 constexpr uint32_t kShortTile = 32;  // rows, and tokens, a workgroup
 
 template <uint32_t F, bool FULL, bool CLIP>
 __global__ __launch_bounds__(64 * kShortWaves, 1) void gemm_exact_short(Product a, uint32_t token_tiles) {
-    __shared__ float4 lds[32 * 16 * 64 / 4];  // the stages (64 KB), then the range sums (128 KB)
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    __shared__ float4 lds[32 * 16 * 64 / 4];  // the stages (16 KB a wave), then the range sums (128 KB)
+    static_assert(kShortWaves * 2 * 512 == 32 * 16 * 64 / 4, "two stages of 8 KB a wave fill the range sums' LDS");
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, half = lane >> 5;
     const uint32_t T = (blockIdx.x % token_tiles) * kShortTile, R = (blockIdx.x / token_tiles) * kShortTile;
     const uint32_t G = a.groups;
     const uint64_t K = static_cast<uint64_t>(G) * 32;
-    const uint32_t r_begin = 4 * wave, r_end = r_begin + 4;
-    const uint32_t g_begin = range_lo(r_begin, G), g_end = range_lo(r_end, G);
-    f32x16 held[4] = {};  // the wave's range sums, range r_begin + q in held[q]
+    const uint32_t r_begin = 4 * wave;
+    // pair p's steps: its longer range's groups
+    const uint32_t l0 = range_lo(r_begin, G), l1 = range_lo(r_begin + 1, G), l2 = range_lo(r_begin + 2, G),
+                   l3 = range_lo(r_begin + 3, G), l4 = range_lo(r_begin + 4, G);
+    const uint32_t n0 = max(l1 - l0, l2 - l1), steps = n0 + max(l3 - l2, l4 - l3);
+    f32x32 held0 = {}, held1 = {};  // pair 0's sums, pair 1's
 
-    if (g_begin < g_end) {
+    if (steps) {
         // Rows and tokens past the product read its last row or token; their
         // outputs are never stored.
         const Piece pc = piece_of(a, min(R + (lane & 31u), a.rows - 1));
         const uint64_t row0 = static_cast<uint64_t>(pc.row) * G;
-        // copy i: token 8 i + lane / 8, its chunk (lane % 8) ^ (token % 8)
+        // copy i of a group: token 8 i + lane / 8, its chunk (lane % 8) ^ (token % 8)
         const float4* src[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -344,33 +353,44 @@ __global__ __launch_bounds__(64 * kShortWaves, 1) void gemm_exact_short(Product 
             src[i] = reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(min(T + tok, a.tokens - 1)) * K) +
                      ((lane & 7u) ^ (tok & 7u));
         }
-        const uint32_t my_tok = 16 * (lane >> 5) + (lane & 15u);
-        float4* const stages = lds + wave * 512;  // two stages of 256 chunks
-        const uint32_t read_at = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(stages)) + 128 * my_tok;
+        const uint32_t my_tok = lane & 31u;
+        float4* const stages = lds + wave * 1024;  // two stages of 2 x 256 chunks, [block][token][chunk]
+        const uint32_t read_at =
+            static_cast<uint32_t>(reinterpret_cast<uintptr_t>(stages)) + 4096 * half + 128 * my_tok;
         float lo = 0.0f, hi = 0.0f;
         if constexpr (CLIP) lo = *a.clip[0], hi = *a.clip[1];
-        uint32_t next_r = r_begin + 1;
-        while (next_r < r_end && range_lo(next_r, G) <= g_begin) ++next_r;
-        // A group's copies go out before its weights' loads (and nothing may
-        // move between them); its weights are waited for (the compiler's
-        // wait) before the next group's loads go out, so that wait covers the
-        // copies too and leaves the next group's loads in flight.
-        auto fetch = [&](Raw<F>& raw, uint32_t stage, uint32_t g) {
+        // Step t's group for block b, clamped into the product; `live` false
+        // past the end of the block's range.
+        auto group_of = [&](uint32_t t, uint32_t b, bool& live) {
+            const bool second = t >= n0;
+            const uint32_t j = second ? t - n0 : t;
+            const uint32_t first = second ? (b ? l3 : l2) : (b ? l1 : l0), end = second ? (b ? l4 : l3) : (b ? l2 : l1);
+            live = first + j < end;
+            return min(first + j, G - 1);
+        };
+        // A step's copies go out before its weights' loads (and nothing may
+        // move between them), so the wait for its weights covers its copies.
+        auto fetch = [&](Raw<F>& raw, uint32_t stage, uint32_t t) {
+            bool live;
+            const uint32_t g0 = group_of(t, 0, live), g1 = group_of(t, 1, live);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                __builtin_amdgcn_global_load_lds(src[i] + 8 * g, (lds_void)(stages + 256 * stage + 64 * i), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(src[i] + 8 * g0, (lds_void)(stages + 512 * stage + 64 * i), 16, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                __builtin_amdgcn_global_load_lds(src[i] + 8 * g1, (lds_void)(stages + 512 * stage + 256 + 64 * i), 16,
+                                                 0, 0);
             __asm__ __volatile__("" ::: "memory");
-            raw.load(pc.piece, pc.blocks, row0 + g);
+            raw.load(pc.piece, pc.blocks, row0 + (half ? g1 : g0));
         };
-        f32x16 s = {};
-        bool fresh = true;
-        auto group = [&](const Raw<F>& raw, uint32_t stage, uint32_t g, auto&& next) {
+        f32x32 s = {};  // +0 at each pair's start: its first products are fma(w, x, +0)
+        auto step = [&](const Raw<F>& raw, uint32_t stage, uint32_t t, auto&& next) {
             float w[32], x[32];
             weights_of(raw, w);
             // the stage's reads, after the weights (whose loads were waited
             // for): the last weight is an input the reads do not use
             u32x4s_t q[8];
-            const uint32_t at = read_at + 4096 * stage;
+            const uint32_t at = read_at + 8192 * stage;
             const uint32_t sw = my_tok & 7u;
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
@@ -395,55 +415,48 @@ __global__ __launch_bounds__(64 * kShortWaves, 1) void gemm_exact_short(Product 
                 x[4 * c + 2] = v.z;
                 x[4 * c + 3] = v.w;
             }
-            next();  // the next group's loads, in flight under this chain
-            // a range's first product takes +0 as its accumulator
-            if (fresh) {
-                const f32x16 zero = {};
-                s = __builtin_amdgcn_mfma_f32_16x16x1f32(w[0], x[0], zero, 0, 0, 0);
-            } else {
-                s = __builtin_amdgcn_mfma_f32_16x16x1f32(w[0], x[0], s, 0, 0, 0);
-            }
+            bool live0, live1;
+            group_of(t, 0, live0);
+            group_of(t, 1, live1);
+            if (!(half ? live1 : live0)) {  // past this block's range: products of -0 and +0
 #pragma unroll
-            for (int k = 1; k < 32; ++k) s = __builtin_amdgcn_mfma_f32_16x16x1f32(w[k], x[k], s, 0, 0, 0);
-            fresh = g + 1 == range_lo(next_r, G);
-            if (fresh) {  // range next_r - 1 ends: its sums held
-                const uint32_t q_range = next_r - 1 - r_begin;
-                if (q_range == 0) held[0] = s;
-                else if (q_range == 1) held[1] = s;
-                else if (q_range == 2) held[2] = s;
-                else held[3] = s;
-                while (next_r < r_end && range_lo(next_r, G) <= g + 1) ++next_r;
+                for (int k = 0; k < 32; ++k) w[k] = -0.0f, x[k] = 0.0f;
+            }
+            next();  // the next step's loads, in flight under this chain
+#pragma unroll
+            for (int k = 0; k < 32; ++k) s = __builtin_amdgcn_mfma_f32_32x32x1f32(w[k], x[k], s, 0, 0, 0);
+            if (t + 1 == n0) {  // pair 0 ends
+                held0 = s;
+                s = f32x32{};
             }
         };
         Raw<F> A, B;
-        fetch(A, 0, g_begin);
-        for (uint32_t g = g_begin; g < g_end; g += 2) {
-            group(A, 0, g, [&] {
-                if (g + 1 < g_end) fetch(B, 1, g + 1);
+        fetch(A, 0, 0);
+        for (uint32_t t = 0; t < steps; t += 2) {
+            step(A, 0, t, [&] {
+                if (t + 1 < steps) fetch(B, 1, t + 1);
             });
-            if (g + 1 >= g_end) break;
-            group(B, 1, g + 1, [&] {
-                if (g + 2 < g_end) fetch(A, 0, g + 2);
+            if (t + 1 >= steps) break;
+            step(B, 1, t + 1, [&] {
+                if (t + 2 < steps) fetch(A, 0, t + 2);
             });
         }
+        held1 = s;
     }
-    // Every copy has landed (each wave waited for its last group's weights,
+    // Every copy has landed (each wave waited for its last step's weights,
     // loaded after its copies, and loads nothing past it) and every stage
     // read: the LDS takes the range sums, [range][register][lane].
     __syncthreads();
     float* const sums = reinterpret_cast<float*>(lds);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        float* slot = sums + (r_begin + q) * 1024 + lane;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const float e = held[q][v];
-            slot[64 * v] = e;
-        }
+    for (int v = 0; v < 32; ++v) {
+        const uint32_t r = r_begin + (v / 16);
+        sums[r * 1024 + 64 * (v % 16) + lane] = held0[v];
+        sums[(r + 2) * 1024 + 64 * (v % 16) + lane] = held1[v];
     }
     __syncthreads();
 
-    // The ordered combine: registers 2 wave and 2 wave + 1 of `lane`.
+    // The ordered combine: registers 2 wave and 2 wave + 1 of a block, for `lane`.
     const uint32_t v0 = 2 * wave;
     float ta = 0.0f, tb = 0.0f;
 #pragma unroll
@@ -453,8 +466,8 @@ __global__ __launch_bounds__(64 * kShortWaves, 1) void gemm_exact_short(Product 
             tb = tb + sums[r * 1024 + 64 * (v0 + 1) + lane];
         }
     }
-    const uint32_t token = T + 16 * (v0 / 8) + (lane & 15u);
-    const uint32_t p = R + 16 * ((v0 / 4) & 1) + 4 * (lane >> 4) + (v0 & 3);
+    const uint32_t token = T + (lane & 31u);
+    const uint32_t p = R + 8 * (v0 / 4) + 4 * (lane >> 5) + (v0 & 3);
     if (token < a.tokens) {
         if (p < a.rows) emit<FULL>(a, p, token, token, ta, tb);
         if (p + 1 < a.rows) emit<FULL>(a, p + 1, token, token, tb, 0.0f);

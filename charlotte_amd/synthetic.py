@@ -74,8 +74,21 @@ def q8_0(rng: np.random.Generator, rows: int, columns: int) -> bytes:
     return blocks.tobytes()
 
 
-_MAKERS = {2: q4_0, 3: q4_1, 8: q8_0, 14: q6_k}
-_BLOCKS = {2: (32, 18), 3: (32, 20), 8: (32, 34), 14: (256, 210)}
+def f32(rng: np.random.Generator, rows: int, columns: int) -> bytes:
+    return (rng.standard_normal((rows, columns)).astype(np.float32) * np.float32(0.05)).tobytes()
+
+
+def f16(rng: np.random.Generator, rows: int, columns: int) -> bytes:
+    return (rng.standard_normal((rows, columns)) * 0.05).astype(np.float16).tobytes()
+
+
+def bf16(rng: np.random.Generator, rows: int, columns: int) -> bytes:
+    bits = (rng.standard_normal((rows, columns)).astype(np.float32) * np.float32(0.05)).view(np.uint32)
+    return (bits >> 16).astype(np.uint16).tobytes()  # the upper halves: bf16 by truncation
+
+
+_MAKERS = {0: f32, 1: f16, 2: q4_0, 3: q4_1, 8: q8_0, 14: q6_k, 30: bf16}
+_BLOCKS = {0: (1, 4), 1: (1, 2), 2: (32, 18), 3: (32, 20), 8: (32, 34), 14: (256, 210), 30: (1, 2)}
 
 
 def weight(rng, gguf_type: int, rows: int, columns: int) -> bytes:

@@ -245,10 +245,13 @@ def short_ctxs():
     (Q8_0, 700, 2048, 17),
     (Q4_1, 520, 1024, 5),
     (F32, 300, 1024, 12),
+    (Q4_0, 640, 1440, 24),       # 45 groups: ranges of 1 and 2, a pair's shorter one padded
+    (Q6_K, 512, 2816, 16),       # 88 groups: ranges of 2 and 3
+    (F32, 200, 1440, 7),
 ])
 def test_short_step_tile_same_bits_as_the_valu_short_tile(short_ctxs, gtype, rows, columns, tokens):
-    """GEMM_EXACT_SHORT (each wave four of a 32 x 32 tile's ranges on the
-    16x16x1 four-block instruction, the sums combined in LDS) against the
+    """GEMM_EXACT_SHORT (each wave four of a 32 x 32 tile's ranges, two a
+    32x32x1 two-block instruction, the sums combined in LDS) against the
     VALU short-step tile, bit for bit."""
     from charlotte_amd import matmul as mm
     from charlotte_amd import synthetic

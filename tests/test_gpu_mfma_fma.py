@@ -1,7 +1,8 @@
-"""The matrix-core instructions the canonical-order prefill tiles (GEMM_EXACT)
-are built on: v_mfma_f32_32x32x1_2b_f32 and v_mfma_f32_16x16x1_4b_f32 are,
-element by element, one fused multiply-add, d = fmaf(a, b, c), bit for bit;
-and their lane layouts.
+"""The matrix-core instruction the canonical-order prefill tiles (GEMM_EXACT,
+GEMM_EXACT_SHORT, GEMM_EXACT_SPLIT) are built on, v_mfma_f32_32x32x1_2b_f32,
+and its four-block K = 1 sibling v_mfma_f32_16x16x1_4b_f32 are, element by
+element, one fused multiply-add, d = fmaf(a, b, c), bit for bit; and their
+lane layouts.
 
 GEMM_EXACT's outputs are the reference order's bits only because of that, so
 the property itself is held here, on the harness's probes (harness.hip):
