@@ -284,18 +284,23 @@ __device__ __forceinline__ void group_product(float4_t (&tot)[R][T], const half8
 #pragma unroll
                     for (int k = 0; k < 4; ++k) tot[r][t][k] = __builtin_fmaf(m[r], sum[t][k], tot[r][t][k]);
         }
+        // every block's hi multiplies, then every lo, then the scales: each
+        // scale waits behind R T independent multiplies, not T
+        float4_t p[R][T];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float4_t p[T];
+        for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int t = 0; t < T; ++t) p[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[t], b[r], z, 0, 0, 0);
+            for (int t = 0; t < T; ++t) p[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[t], b[r], z, 0, 0, 0);
 #pragma unroll
-            for (int t = 0; t < T; ++t) p[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[t], b[r], p[t], 0, 0, 0);
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int t = 0; t < T; ++t) p[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[t], b[r], p[r][t], 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int t = 0; t < T; ++t)
 #pragma unroll
-                for (int k = 0; k < 4; ++k) tot[r][t][k] = __builtin_fmaf(s[r], p[t][k], tot[r][t][k]);
-        }
+                for (int k = 0; k < 4; ++k) tot[r][t][k] = __builtin_fmaf(s[r], p[r][t][k], tot[r][t][k]);
     } else {
         // Codes of weights 4q .. 4q+3 (half 0) and 16+4q .. 16+4q+3 (half
         // 1): low nibbles from lo, high pairs from hi.
