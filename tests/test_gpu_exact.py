@@ -248,6 +248,9 @@ def short_ctxs():
     (Q4_0, 640, 1440, 24),       # 45 groups: ranges of 1 and 2, a pair's shorter one padded
     (Q6_K, 512, 2816, 16),       # 88 groups: ranges of 2 and 3
     (F32, 200, 1440, 7),
+    (Q4_0, 100, 32, 7),          # one group: range 31 alone, beside an empty range
+    (Q8_0, 70, 96, 40),          # three groups
+    (Q4_0, 33, 2080, 3),         # 65 groups: ranges of 2 and 3
 ])
 def test_short_step_tile_same_bits_as_the_valu_short_tile(short_ctxs, gtype, rows, columns, tokens):
     """GEMM_EXACT_SHORT (each wave four of a 32 x 32 tile's ranges, two a
@@ -271,6 +274,38 @@ def test_short_step_tile_same_bits_as_the_valu_short_tile(short_ctxs, gtype, row
 
     got, want = _both(short_ctxs, members, x, tokens, [rows])
     _same(got, want, f"short type {gtype} {rows}x{columns} tokens={tokens}")
+
+
+def test_short_step_tile_special_inputs_as_the_valu_short_tile(short_ctxs):
+    """Infinite, NaN, huge, subnormal and signed-zero inputs through pairs of
+    ranges of unequal length (45 groups, the shorter range of each pair
+    multiplying -0 by +0 at the pair's last step): NaN where the VALU short
+    tile has NaN, every other output bit for bit."""
+    from charlotte_amd import matmul as mm
+    from charlotte_amd import synthetic
+
+    rows, columns, tokens = 640, 1440, 5
+    rng = np.random.default_rng(45)
+    stored = synthetic.weight(rng, Q4_0, rows, columns)
+    x = rng.standard_normal((tokens, columns), dtype=np.float32)
+    x[0, 3], x[0, 40], x[0, 41], x[0, columns - 1] = 1e28, 1e-40, -1e-42, -0.0
+    x[0, 77::97] = np.float32(-1e28)
+    x[1, columns // 2] = np.inf
+    x[2, 5] = np.nan
+    x[3] = (x[3].astype(np.float64) * 1e-39).astype(np.float32)
+    x[4, 1400:] = -0.0  # the last groups' inputs all -0: range sums of zero products
+    shape = mm.MatmulLaunch([mm.Member(mm.Weight.shape(Q4_0, rows, columns))], 16, [16])
+    assert mm.plan_launch(shape, tokens).kernel == mm.Kernel.GEMM_EXACT_SHORT
+
+    def members(ctx):
+        w = _weight(ctx, Q4_0, rows, columns, stored)
+        return [mm.Member(w)], [w]
+
+    (got,), (want,) = _both(short_ctxs, members, x, tokens, [rows])
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    nan_g, nan_w = np.isnan(got), np.isnan(want)
+    assert nan_w.any() and (nan_g == nan_w).all(), "NaN where the VALU tile has NaN"
+    assert (got[~nan_w].view(np.uint32) == want[~nan_w].view(np.uint32)).all()
 
 
 @pytest.mark.parametrize("activation", [0, 1])
