@@ -278,15 +278,15 @@ Verdict plan_product(const chm::Product& a, uint32_t format, const Target& t, ch
     chm::Plan exact;
     chm::plan_gemm_exact(a, format, t.compute_units, false, &exact);
     // AUTO: the matrix cores' fused multiply-add tile where the step gives it
-    // more than two waves a compute unit (at fewer each of its waves' walk
+    // at least three waves a compute unit (at fewer each of its waves' walk
     // through K is the step's time: measured slower than the short-step tile
-    // at 512 waves on 256 compute units, 91 against 71 us at 8,192 x 2,048 x
-    // 128 tokens, faster at 768, 54 against 70 us at 3,072 x 1,024 x 512);
+    // at 640 waves on 256 compute units, 91 against 79 us at 2,560 x 2,048 x
+    // 512 tokens, faster at 768, 53 against 58 us at 3,072 x 1,024 x 512);
     // else the short-step form on the matrix cores, K split among a
     // workgroup's waves (measured faster than the VALU short-step tile at
     // every short step tried). The same bits whichever runs.
     const uint64_t exact_waves = uint64_t{(a.rows + 63) / 64} * exact.token_tiles;
-    if (t.gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_EXACT_MFMA || exact_waves > 2ull * t.compute_units)
+    if (t.gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_EXACT_MFMA || exact_waves >= 3ull * t.compute_units)
         *plan = exact;
     else
         chm::plan_gemm_exact_short(a, plan);

@@ -75,7 +75,7 @@ class Rows(enum.IntEnum):
 class GemmPath(enum.IntEnum):
     """The prefill kernel: AUTO (the default), CANONICAL and EXACT_MFMA are
     bit-exact — AUTO runs the matrix cores' f32 fused multiply-add, whole
-    (GEMM_EXACT) above two waves a compute unit, else split in the workgroup
+    (GEMM_EXACT) from three waves a compute unit, else split in the workgroup
     (GEMM_EXACT_SHORT), and its split along K (GEMM_EXACT_SPLIT); CANONICAL
     keeps to the VALU (the 128-row tile, the short-step tile GEMM_SHORT where
     the 128-row tiles would leave compute units idle, GEMM_SPLIT); EXACT_MFMA

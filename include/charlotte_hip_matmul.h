@@ -120,8 +120,8 @@ typedef enum {
  * reference's decode = prefill guarantee whatever workspace it sets. For a
  * step that does not split, AUTO takes the matrix cores' K = 1 f32
  * instruction (GEMM_EXACT: each range's chain one fused multiply-add a k, as
- * the VALU tile adds it, on 64-row waves) where the step gives it more than
- * two waves a compute unit; else the same chains split among a workgroup's
+ * the VALU tile adds it, on 64-row waves) where the step gives it at least
+ * three waves a compute unit; else the same chains split among a workgroup's
  * waves (GEMM_EXACT_SHORT: 32 rows by 32 tokens, eight waves of four ranges,
  * the range sums combined in LDS). A step that splits runs its chunks of
  * ranges on the matrix-core chains under AUTO and EXACT_MFMA

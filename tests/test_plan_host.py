@@ -331,17 +331,18 @@ def test_short_steps_that_do_not_split_take_a_short_step_tile(shapes):
     assert (p.kernel, p.tiles, p.tile_rows) == (K.GEMM_SHORT, 4 * 128, 16)
 
 
-def test_auto_takes_the_exact_matrix_core_tile_above_two_waves_a_compute_unit(shapes):
-    """AUTO: GEMM_EXACT where its waves (64 rows by 64 or 32 tokens) number more
-    than 2 x the compute units, else the matrix-core short-step tile: 2,048 x
-    2,048 at 1,024 tokens is 1,024 waves of 64 x 32, at 512 tokens 512 (the
-    measured crossing: 90 against 69 us at 512 tokens); 3,072 x 1,024 at 512
-    tokens, 768 (54 against 70 us)."""
+def test_auto_takes_the_exact_matrix_core_tile_from_three_waves_a_compute_unit(shapes):
+    """AUTO: GEMM_EXACT where its waves (64 rows by 64 or 32 tokens) number at
+    least 3 x the compute units, else the matrix-core short-step tile: 2,048 x
+    2,048 at 1,024 tokens is 1,024 waves of 64 x 32, at 512 tokens 512; 2,560
+    x 2,048 at 512 tokens 640 (the measured crossing: 91 against 79 us);
+    3,072 x 1,024 at 512 tokens 768 (53 against 58 us)."""
     w = shapes(Q4_0, 2048, 2048)
     assert mm.plan_launch(_write(w), 1024).kernel == K.GEMM_EXACT
     assert mm.plan_launch(_write(w), 512).kernel == K.GEMM_EXACT_SHORT
     assert mm.plan_launch(_write(w), 256).kernel == K.GEMM_EXACT_SHORT
-    assert mm.plan_launch(_write(shapes(Q4_0, 3072, 1024)), 512).kernel == K.GEMM_EXACT
+    assert mm.plan_launch(_write(shapes(Q4_0, 2560, 2048)), 512).kernel == K.GEMM_EXACT_SHORT  # 640 waves
+    assert mm.plan_launch(_write(shapes(Q4_0, 3072, 1024)), 512).kernel == K.GEMM_EXACT  # 768
     assert mm.plan_launch(_write(shapes(Q4_0, 8192, 2048)), 128).kernel == K.GEMM_EXACT_SHORT  # 512 waves
     assert mm.plan_launch(_write(w), 512, mm.Target(128)).kernel == K.GEMM_EXACT  # 512 waves on 128 CUs
     assert mm.plan_launch(_write(w), 256, mm.Target(128)).kernel == K.GEMM_EXACT_SHORT  # 256 of them
