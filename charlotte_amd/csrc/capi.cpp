@@ -289,7 +289,7 @@ Verdict plan_product(const chm::Product& a, uint32_t format, const Target& t, ch
     if (t.gemm_path == CHARLOTTE_HIP_MATMUL_GEMM_EXACT_MFMA || exact_waves >= 3ull * t.compute_units)
         *plan = exact;
     else
-        chm::plan_gemm_exact_short(a, plan);
+        chm::plan_gemm_exact_short(a, t.compute_units, plan);
     return {};
 }
 

@@ -474,10 +474,169 @@ __global__ __launch_bounds__(64 * kShortWaves, 1) void gemm_exact_short(Product 
     }
 }
 
+// gemm_exact_quad — the short-step tile for a step whose 32 x 32 tiles would
+// leave compute units idle (C6's 2,048 x 8,192 at 32 tokens: 64 of them):
+// 16 rows x 16 tokens a workgroup, four times the workgroups (at the cost of
+// twice the decode a product: each instruction does half the products). Each of its
+// eight waves takes four of the 32 ranges as the four blocks of one
+// v_mfma_f32_16x16x1_4b_f32 (K = 1, one fused multiply-add an element): block
+// b is range r_begin + b, its A (row R + l % 16) and B (token T + l % 16) from
+// lanes 16 b .. 16 b + 15, each lane decoding its own range's group; register
+// v holds block v / 4's row 4 (l / 16) + v % 4, column l % 16. Step j is group
+// j of the four ranges; a range a group shorter than the wave's longest takes
+// -0 and +0 at the last step (fma(-0, +0, acc) = acc for every acc). A
+// step's inputs, four groups x 16 tokens x 128 bytes, reach the wave's LDS
+// stage by eight whole-line copies as gemm_exact_short's do, two stages a
+// wave; the accumulator ends as the wave's four range sums, which a barrier
+// later the LDS holds ([range][register][lane]), and 128 threads add a
+// token's rows p, p + 1 over the 32 ranges in order from zero: the bits of
+// every other canonical tile.
+constexpr uint32_t kQuadTile = 16;  // rows, and tokens, a workgroup
+
+template <uint32_t F, bool FULL, bool CLIP>
+__global__ __launch_bounds__(64 * kShortWaves, 1) void gemm_exact_quad(Product a, uint32_t token_tiles) {
+    __shared__ float4 lds[kShortWaves * 2 * 512];  // the stages (16 KB a wave), then the range sums (32 KB)
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, blk = lane >> 4, my_i = lane & 15u;
+    const uint32_t T = (blockIdx.x % token_tiles) * kQuadTile, R = (blockIdx.x / token_tiles) * kQuadTile;
+    const uint32_t G = a.groups;
+    const uint64_t K = static_cast<uint64_t>(G) * 32;
+    const uint32_t r_begin = 4 * wave;
+    uint32_t lo_r[5];
+#pragma unroll
+    for (int b = 0; b < 5; ++b) lo_r[b] = range_lo(r_begin + b, G);
+    uint32_t steps = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) steps = max(steps, lo_r[b + 1] - lo_r[b]);
+    // this lane's range: its first group and its end
+    const uint32_t my_first = blk == 0 ? lo_r[0] : blk == 1 ? lo_r[1] : blk == 2 ? lo_r[2] : lo_r[3];
+    const uint32_t my_end = blk == 0 ? lo_r[1] : blk == 1 ? lo_r[2] : blk == 2 ? lo_r[3] : lo_r[4];
+    f32x16 s = {};  // +0: each range's first product is fma(w, x, +0)
+
+    if (steps) {
+        // Rows and tokens past the product read its last row or token; their
+        // outputs are never stored.
+        const Piece pc = piece_of(a, min(R + my_i, a.rows - 1));
+        const uint64_t row0 = static_cast<uint64_t>(pc.row) * G;
+        // copy (b, h): block b's tokens 8 h + lane / 8, chunk (lane % 8) ^ (token % 8)
+        const float4* src[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t tok = 8 * h + (lane >> 3);
+            src[h] = reinterpret_cast<const float4*>(a.x + static_cast<uint64_t>(min(T + tok, a.tokens - 1)) * K) +
+                     ((lane & 7u) ^ (tok & 7u));
+        }
+        float4* const stages = lds + wave * 1024;  // two stages of 4 x 128 chunks, [block][token][chunk]
+        const uint32_t read_at =
+            static_cast<uint32_t>(reinterpret_cast<uintptr_t>(stages)) + 2048 * blk + 128 * my_i;
+        float lo = 0.0f, hi = 0.0f;
+        if constexpr (CLIP) lo = *a.clip[0], hi = *a.clip[1];
+        // A step's copies go out before its weights' loads (and nothing may
+        // move between them), so the wait for its weights covers its copies.
+        auto fetch = [&](Raw<F>& raw, uint32_t stage, uint32_t j) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t g = min(lo_r[b] + j, G - 1);
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    __builtin_amdgcn_global_load_lds(src[h] + 8 * g, (lds_void)(stages + 512 * stage + 128 * b + 64 * h),
+                                                     16, 0, 0);
+            }
+            __asm__ __volatile__("" ::: "memory");
+            raw.load(pc.piece, pc.blocks, row0 + min(my_first + j, G - 1));
+        };
+        auto step = [&](const Raw<F>& raw, uint32_t stage, uint32_t j, auto&& next) {
+            float w[32], x[32];
+            weights_of(raw, w);
+            // the stage's reads, after the weights (whose loads were waited
+            // for): the last weight is an input the reads do not use
+            u32x4s_t q[8];
+            const uint32_t at = read_at + 8192 * stage;
+            const uint32_t sw = my_i & 7u;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const uint32_t addr = at + 16 * (c ^ sw);
+                __asm__ __volatile__("ds_read_b128 %0, %1" : "=v"(q[c]) : "v"(addr), "v"(w[31]));
+            }
+            __asm__ __volatile__("s_waitcnt lgkmcnt(0)"
+                                 : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(q[4]), "+v"(q[5]),
+                                   "+v"(q[6]), "+v"(q[7]));
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                float4 v = make_float4(__uint_as_float(q[c][0]), __uint_as_float(q[c][1]),
+                                       __uint_as_float(q[c][2]), __uint_as_float(q[c][3]));
+                if constexpr (CLIP) {
+                    v.x = clamp_to(v.x, lo, hi);
+                    v.y = clamp_to(v.y, lo, hi);
+                    v.z = clamp_to(v.z, lo, hi);
+                    v.w = clamp_to(v.w, lo, hi);
+                }
+                x[4 * c] = v.x;
+                x[4 * c + 1] = v.y;
+                x[4 * c + 2] = v.z;
+                x[4 * c + 3] = v.w;
+            }
+            if (my_first + j >= my_end) {  // past this block's range: products of -0 and +0
+#pragma unroll
+                for (int k = 0; k < 32; ++k) w[k] = -0.0f, x[k] = 0.0f;
+            }
+            next();  // the next step's loads, in flight under this chain
+#pragma unroll
+            for (int k = 0; k < 32; ++k) s = __builtin_amdgcn_mfma_f32_16x16x1f32(w[k], x[k], s, 0, 0, 0);
+        };
+        Raw<F> A, B;
+        fetch(A, 0, 0);
+        for (uint32_t j = 0; j < steps; j += 2) {
+            step(A, 0, j, [&] {
+                if (j + 1 < steps) fetch(B, 1, j + 1);
+            });
+            if (j + 1 >= steps) break;
+            step(B, 1, j + 1, [&] {
+                if (j + 2 < steps) fetch(A, 0, j + 2);
+            });
+        }
+    }
+    // Every copy has landed (each wave waited for its last step's weights,
+    // loaded after its copies, and loads nothing past it) and every stage
+    // read: the LDS takes the range sums, [range][register][lane].
+    __syncthreads();
+    float* const sums = reinterpret_cast<float*>(lds);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sums[(r_begin + v / 4) * 256 + 64 * (v % 4) + lane] = s[v];
+    __syncthreads();
+
+    // The ordered combine: registers 2 h and 2 h + 1 of a block, for lane `l`.
+    if (threadIdx.x < 128) {
+        const uint32_t l = threadIdx.x & 63u, h = threadIdx.x >> 6;
+        float ta = 0.0f, tb = 0.0f;
+#pragma unroll
+        for (uint32_t r = 0; r < 32; ++r) {
+            if (range_lo(r, G) < range_lo(r + 1, G)) {
+                ta = ta + sums[r * 256 + 64 * (2 * h) + l];
+                tb = tb + sums[r * 256 + 64 * (2 * h + 1) + l];
+            }
+        }
+        const uint32_t token = T + (l & 15u);
+        const uint32_t p = R + 4 * (l >> 4) + 2 * h;
+        if (token < a.tokens) {
+            if (p < a.rows) emit<FULL>(a, p, token, token, ta, tb);
+            if (p + 1 < a.rows) emit<FULL>(a, p + 1, token, token, tb, 0.0f);
+        }
+    }
+}
+
 template <uint32_t F>
 void go_exact_short(const Product& a, const Plan& plan, hipStream_t stream) {
     const dim3 grid(static_cast<uint32_t>(plan.workgroups)), block(64 * kShortWaves);
     const uint32_t tt = plan.token_tiles;
+    if (plan.tile_rows == kQuadTile) {
+        if (plain_epilogue(a))
+            hipLaunchKernelGGL((gemm_exact_quad<F, false, false>), grid, block, 0, stream, a, tt);
+        else if (!clipped(a))
+            hipLaunchKernelGGL((gemm_exact_quad<F, true, false>), grid, block, 0, stream, a, tt);
+        else
+            hipLaunchKernelGGL((gemm_exact_quad<F, true, true>), grid, block, 0, stream, a, tt);
+        return;
+    }
     if (plain_epilogue(a))
         hipLaunchKernelGGL((gemm_exact_short<F, false, false>), grid, block, 0, stream, a, tt);
     else if (!clipped(a))
@@ -552,14 +711,21 @@ void plan_gemm_exact(const Product& a, uint32_t format, uint32_t compute_units, 
 }
 
 // The short-step form: workgroups of 32 rows x 32 tokens, token tile first.
-void plan_gemm_exact_short(const Product& a, Plan* plan) {
+void plan_gemm_exact_short(const Product& a, uint32_t compute_units, Plan* plan) {
     *plan = Plan{};
     plan->kernel = kGemmExactShort;
     plan->launches = 1;
-    plan->tile_tokens = kShortTile;
-    plan->tile_rows = kShortTile;
-    plan->token_tiles = (a.tokens + kShortTile - 1) / kShortTile;
-    plan->row_tiles = (a.rows + kShortTile - 1) / kShortTile;
+    // 16 x 16 tiles (gemm_exact_quad) where they number at most two a
+    // compute unit, else 32 x 32 (gemm_exact_short), a quarter as many:
+    // measured on 256 compute units, 2,048 x 2,048 x 32 tokens (256 of 16 x
+    // 16) 7.5 against 17.2 us, 4,096 x 2,048 x 32 (512) 13.6 against 17.8,
+    // 6,144 x 2,048 x 32 (768) 19.8 against 18.0
+    const uint64_t quads = uint64_t{(a.tokens + kQuadTile - 1) / kQuadTile} * ((a.rows + kQuadTile - 1) / kQuadTile);
+    const uint32_t tile = quads <= 2ull * compute_units ? kQuadTile : kShortTile;
+    plan->tile_tokens = tile;
+    plan->tile_rows = tile;
+    plan->token_tiles = (a.tokens + tile - 1) / tile;
+    plan->row_tiles = (a.rows + tile - 1) / tile;
     plan->wave_rows = 1;
     plan->wave_tokens = 1;
     plan->tiles = static_cast<uint64_t>(plan->token_tiles) * plan->row_tiles;

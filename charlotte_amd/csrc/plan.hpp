@@ -82,7 +82,7 @@ hipError_t launch_gemm_short(const Product& a, uint32_t format, const Plan& plan
 // Prefill on the matrix cores in the canonical order (gemm_exact.hip):
 // every format, every epilogue, the VALU tile's bits.
 void plan_gemm_exact(const Product& a, uint32_t format, uint32_t compute_units, bool split, Plan* plan);
-void plan_gemm_exact_short(const Product& a, Plan* plan);
+void plan_gemm_exact_short(const Product& a, uint32_t compute_units, Plan* plan);
 hipError_t launch_gemm_exact_short(const Product& a, uint32_t format, const Plan& plan, hipStream_t stream);
 hipError_t launch_gemm_exact(const Product& a, uint32_t format, const Plan& plan, float* range_sums,
                              hipStream_t stream);

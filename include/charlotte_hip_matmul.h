@@ -122,8 +122,9 @@ typedef enum {
  * instruction (GEMM_EXACT: each range's chain one fused multiply-add a k, as
  * the VALU tile adds it, on 64-row waves) where the step gives it at least
  * three waves a compute unit; else the same chains split among a workgroup's
- * waves (GEMM_EXACT_SHORT: 32 rows by 32 tokens, eight waves of four ranges,
- * the range sums combined in LDS). A step that splits runs its chunks of
+ * waves (GEMM_EXACT_SHORT: 32 rows by 32 tokens, or 16 by 16 where the larger
+ * tiles would leave compute units idle, eight waves of four ranges, the range
+ * sums combined in LDS). A step that splits runs its chunks of
  * ranges on the matrix-core chains under AUTO and EXACT_MFMA
  * (GEMM_EXACT_SPLIT), on the 128-row VALU tile under CANONICAL (GEMM_SPLIT);
  * the same range sums, the same combine. CANONICAL keeps to the VALU: the
@@ -319,7 +320,7 @@ typedef enum {
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_SHORT = 19,   /* prefill of a short step: 16 or 8 rows x 32 tokens, K split in the workgroup */
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_EXACT = 20,   /* prefill on the matrix cores' f32 fused multiply-add, the canonical order */
     CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_EXACT_SPLIT = 21, /* the same split along K, then the ordered combine */
-    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_EXACT_SHORT = 22  /* a short step on the matrix cores: 32 x 32, K split in the workgroup */
+    CHARLOTTE_HIP_MATMUL_KERNEL_GEMM_EXACT_SHORT = 22  /* a short step on the matrix cores: 32 x 32 or 16 x 16 tiles, K split in the workgroup */
 } charlotte_hip_matmul_kernel;
 
 /* What a plan is made for: the device's compute units (256 on MI355X) and

@@ -236,26 +236,32 @@ def short_ctxs():
     tile.close()
 
 
-@pytest.mark.parametrize("gtype,rows,columns,tokens", [
-    (Q4_0, 2048, 8192, 32),      # C6's down projection, unsplit: 64 workgroups
-    (Q4_0, 1001, 2048, 45),      # ragged rows and tokens
-    (Q6_K, 3072, 1152, 9),
-    (Q4_0, 1000, 14336, 33),     # 448 groups: 56 a wave
-    (Q4_0, 333, 64, 20),         # 2 groups: 30 empty ranges, waves holding none
-    (Q8_0, 700, 2048, 17),
-    (Q4_1, 520, 1024, 5),
-    (F32, 300, 1024, 12),
-    (Q4_0, 640, 1440, 24),       # 45 groups: ranges of 1 and 2, a pair's shorter one padded
-    (Q6_K, 512, 2816, 16),       # 88 groups: ranges of 2 and 3
-    (F32, 200, 1440, 7),
-    (Q4_0, 100, 32, 7),          # one group: range 31 alone, beside an empty range
-    (Q8_0, 70, 96, 40),          # three groups
-    (Q4_0, 33, 2080, 3),         # 65 groups: ranges of 2 and 3
+@pytest.mark.parametrize("gtype,rows,columns,tokens,tile", [
+    (Q4_0, 2048, 8192, 32, 16),  # C6's down projection, unsplit: 64 tiles of 32 x 32, so 256 of 16 x 16
+    (Q4_0, 1001, 2048, 45, 16),  # ragged rows and tokens
+    (Q6_K, 3072, 1152, 9, 16),
+    (Q4_0, 1000, 14336, 33, 16),  # 448 groups: 56 a wave
+    (Q4_0, 333, 64, 20, 16),     # 2 groups: 30 empty ranges, waves holding none
+    (Q8_0, 700, 2048, 17, 16),
+    (Q4_1, 520, 1024, 5, 16),
+    (F32, 300, 1024, 12, 16),
+    (Q4_0, 640, 1440, 24, 16),   # 45 groups: ranges of 1 and 2, the shorter padded
+    (Q6_K, 512, 2816, 16, 16),   # 88 groups: ranges of 2 and 3
+    (F32, 200, 1440, 7, 16),
+    (Q4_0, 100, 32, 7, 16),      # one group: range 31 alone
+    (Q8_0, 70, 96, 40, 16),      # three groups
+    (Q4_0, 33, 2080, 3, 16),     # 65 groups: ranges of 2 and 3
+    (Q4_0, 8192, 1440, 32, 32),  # 256 tiles of 32 x 32: pairs of unequal ranges
+    (Q6_K, 4096, 2816, 64, 32),
+    (F32, 8192, 1024, 40, 32),
+    (Q4_1, 8200, 2048, 33, 32),  # ragged rows and tokens
+    (Q8_0, 8192, 64, 32, 32),    # 2 groups: pairs with an empty range
 ])
-def test_short_step_tile_same_bits_as_the_valu_short_tile(short_ctxs, gtype, rows, columns, tokens):
-    """GEMM_EXACT_SHORT (each wave four of a 32 x 32 tile's ranges, two a
-    32x32x1 two-block instruction, the sums combined in LDS) against the
-    VALU short-step tile, bit for bit."""
+def test_short_step_tile_same_bits_as_the_valu_short_tile(short_ctxs, gtype, rows, columns, tokens, tile):
+    """GEMM_EXACT_SHORT against the VALU short-step tile, bit for bit: 32 x 32
+    tiles (each wave four of the ranges, two a 32x32x1 two-block instruction)
+    where they give every compute unit one, else 16 x 16 (four ranges a
+    16x16x1 four-block instruction); the sums combined in LDS."""
     from charlotte_amd import matmul as mm
     from charlotte_amd import synthetic
 
@@ -266,7 +272,8 @@ def test_short_step_tile_same_bits_as_the_valu_short_tile(short_ctxs, gtype, row
         stored = synthetic.weight(rng, gtype, rows, columns)
     x = synthetic.activations(rng, tokens, columns)
     shape = mm.MatmulLaunch([mm.Member(mm.Weight.shape(gtype, rows, columns))], 16, [16])
-    assert mm.plan_launch(shape, tokens).kernel == mm.Kernel.GEMM_EXACT_SHORT
+    p = mm.plan_launch(shape, tokens)
+    assert (p.kernel, p.tile_rows, p.tile_tokens) == (mm.Kernel.GEMM_EXACT_SHORT, tile, tile)
 
     def members(ctx):
         w = _weight(ctx, gtype, rows, columns, stored)
@@ -276,15 +283,16 @@ def test_short_step_tile_same_bits_as_the_valu_short_tile(short_ctxs, gtype, row
     _same(got, want, f"short type {gtype} {rows}x{columns} tokens={tokens}")
 
 
-def test_short_step_tile_special_inputs_as_the_valu_short_tile(short_ctxs):
-    """Infinite, NaN, huge, subnormal and signed-zero inputs through pairs of
-    ranges of unequal length (45 groups, the shorter range of each pair
-    multiplying -0 by +0 at the pair's last step): NaN where the VALU short
-    tile has NaN, every other output bit for bit."""
+@pytest.mark.parametrize("rows,tile", [(640, 16), (12288, 32)])
+def test_short_step_tile_special_inputs_as_the_valu_short_tile(short_ctxs, rows, tile):
+    """Infinite, NaN, huge, subnormal and signed-zero inputs through ranges of
+    unequal length (45 groups, a shorter range multiplying -0 by +0 at its
+    last step), on both tile sizes: NaN where the VALU short tile has NaN,
+    every other output bit for bit."""
     from charlotte_amd import matmul as mm
     from charlotte_amd import synthetic
 
-    rows, columns, tokens = 640, 1440, 5
+    columns, tokens = 1440, 5
     rng = np.random.default_rng(45)
     stored = synthetic.weight(rng, Q4_0, rows, columns)
     x = rng.standard_normal((tokens, columns), dtype=np.float32)
@@ -295,7 +303,8 @@ def test_short_step_tile_special_inputs_as_the_valu_short_tile(short_ctxs):
     x[3] = (x[3].astype(np.float64) * 1e-39).astype(np.float32)
     x[4, 1400:] = -0.0  # the last groups' inputs all -0: range sums of zero products
     shape = mm.MatmulLaunch([mm.Member(mm.Weight.shape(Q4_0, rows, columns))], 16, [16])
-    assert mm.plan_launch(shape, tokens).kernel == mm.Kernel.GEMM_EXACT_SHORT
+    p = mm.plan_launch(shape, tokens)
+    assert (p.kernel, p.tile_rows) == (mm.Kernel.GEMM_EXACT_SHORT, tile)
 
     def members(ctx):
         w = _weight(ctx, Q4_0, rows, columns, stored)

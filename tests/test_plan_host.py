@@ -301,17 +301,19 @@ def test_short_steps_split_along_k_when_the_gate_and_range_sums_allow(shapes):
 
 
 def test_short_steps_that_do_not_split_take_a_short_step_tile(shapes):
-    """AUTO: a step that gives the whole-K matrix-core tile fewer than two
+    """AUTO: a step that gives the whole-K matrix-core tile fewer than three
     waves a compute unit runs GEMM_EXACT_SHORT, workgroups of 32 rows x 32
-    tokens whose eight waves split K's ranges: C6's 32 tokens through 2,048 x
-    8,192, 64 workgroups; a 32-token gated gate/up of Llama 3.2 1B (16,384
-    interleaved rows), 512. CANONICAL: the VALU short-step tile where the
+    tokens whose eight waves split K's ranges, or of 16 x 16 where those
+    number at most two a compute unit: C6's 32 tokens through 2,048 x 8,192,
+    256 of 16 x 16; a 32-token gated gate/up of Llama 3.2 1B (16,384
+    interleaved rows), 512 of 32 x 32 (2,048 of 16 x 16 would be eight a
+    compute unit). CANONICAL: the VALU short-step tile where the
     128-row tiles would be fewer than the compute units (C6: 16 tiles of 128
     rows on 256 CUs, so 8-row tiles, 256 workgroups; the gated pair 16-row
     tiles, 1,024 workgroups), else the 128-row tile (C4: 512 tiles)."""
     down = shapes(Q4_0, 2048, 8192)
     p = mm.plan_launch(_write(down), 32)
-    assert (p.kernel, p.canonical, p.tile_rows, p.tile_tokens, p.workgroups) == (K.GEMM_EXACT_SHORT, True, 32, 32, 64)
+    assert (p.kernel, p.canonical, p.tile_rows, p.tile_tokens, p.workgroups) == (K.GEMM_EXACT_SHORT, True, 16, 16, 256)
     canonical = mm.Target(256, mm.GemmPath.CANONICAL)
     p = mm.plan_launch(_write(down), 32, canonical)
     assert (p.kernel, p.canonical, p.tile_rows, p.tile_tokens, p.workgroups) == (K.GEMM_SHORT, True, 8, 32, 256)
