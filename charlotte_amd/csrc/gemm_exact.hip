@@ -476,8 +476,8 @@ __global__ __launch_bounds__(64 * kShortWaves, 1) void gemm_exact_short(Product 
 
 // gemm_exact_quad — the short-step tile for a step whose 32 x 32 tiles would
 // leave compute units idle (C6's 2,048 x 8,192 at 32 tokens: 64 of them):
-// 16 rows x 16 tokens a workgroup, four times the workgroups (at the cost of
-// twice the decode a product: each instruction does half the products). Each of its
+// 16 rows x 16 tokens a workgroup, four times the workgroups, at twice the
+// decode a product (each instruction does half the products). Each of its
 // eight waves takes four of the 32 ranges as the four blocks of one
 // v_mfma_f32_16x16x1_4b_f32 (K = 1, one fused multiply-add an element): block
 // b is range r_begin + b, its A (row R + l % 16) and B (token T + l % 16) from
