@@ -319,8 +319,9 @@ def test_short_step_tile_special_inputs_as_the_valu_short_tile(short_ctxs, rows,
 
 @pytest.mark.parametrize("activation", [0, 1])
 def test_short_step_tile_epilogues_same_bits(short_ctxs, activation):
-    """A gated gate/up pair (Llama 3.2 1B's, 32 tokens), a fused QKV, a Write
-    with clip, bias and activation, and GatedByInput, on both short tiles."""
+    """A gated gate/up pair (Llama 3.2 1B's, 32 tokens: the 32 x 32 tile; and a
+    small ragged one: the 16 x 16), a fused QKV, a Write with clip, bias and
+    activation, and GatedByInput, against the VALU short tile."""
     from charlotte_amd import matmul as mm
     from charlotte_amd import synthetic
 
@@ -336,6 +337,19 @@ def test_short_step_tile_epilogues_same_bits(short_ctxs, activation):
     got, want = _both(short_ctxs, gated, x, tokens, [8192], epilogue=mm.Epilogue.GatedActivation,
                       activation=activation)
     _same(got, want, f"gated act={activation}")
+    # a small gated pair, ragged (2 x 1,000 rows, 13 tokens): the 16 x 16 tile
+    small = [synthetic.weight(rng, Q4_0, 1000, 2048) for _ in range(2)]
+
+    def gated_small(ctx):
+        ws = [_weight(ctx, Q4_0, 1000, 2048, s) for s in small]
+        return [mm.Member(w) for w in ws], ws
+
+    shape = mm.MatmulLaunch([mm.Member(mm.Weight.shape(Q4_0, 1000, 2048))] * 2, 16, [16],
+                            epilogue=mm.Epilogue.GatedActivation)
+    assert mm.plan_launch(shape, 13).tile_rows == 16
+    got, want = _both(short_ctxs, gated_small, x[:13], 13, [1000], epilogue=mm.Epilogue.GatedActivation,
+                      activation=activation)
+    _same(got, want, f"small gated act={activation}")
     parts = [synthetic.weight(rng, Q4_0, r, 2048) for r in (2048, 512, 512)]
 
     def qkv(ctx):
