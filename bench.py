@@ -258,24 +258,39 @@ def time_decode_shapes(spec, steps, warmup, settle_ms, limbs=False):
 PREFILL_TYPES = {"f32": 0, "f16": 1, "q4_0": 2, "q4_1": 3, "q8_0": 8, "q6_k": 14, "bf16": 30}
 
 
+def parse_prefill_shapes(spec):
+    """--prefill's comma list of [TYPE:]ROWSxKxTOKENS as (item, GGUF type, rows,
+    K, tokens); SystemExit naming the item that does not parse."""
+    shapes = []
+    for item in spec.split(","):
+        kind, _, dims = item.strip().lower().rpartition(":")
+        if kind and kind not in PREFILL_TYPES:
+            raise SystemExit(f"--prefill {item}: the type is one of {', '.join(PREFILL_TYPES)}")
+        try:
+            rows, columns, tokens = (int(v) for v in dims.split("x"))
+        except ValueError:
+            raise SystemExit(f"--prefill {item}: not [TYPE:]ROWSxKxTOKENS") from None
+        shapes.append((item.strip(), PREFILL_TYPES[kind or "q4_0"], rows, columns, tokens))
+    return shapes
+
+
 def time_prefill_shapes(spec, steps, warmup, settle_ms):
     """One prefill product a shape [TYPE:]ROWSxKxTOKENS (TYPE a key of
     PREFILL_TYPES, Q4_0 when absent), timed as the configs are, on each
     bit-exact path (CANONICAL: the 128-row tile; AUTO; EXACT_MFMA: the matrix
     cores' fused multiply-add): {"[TYPE:]ROWSxKxTOKENS": {path: {us, TFLOP/s,
     kernel}}}. The figures that choose AUTO's kernel."""
+    shapes = parse_prefill_shapes(spec)
     S = Setup()
     S.settle_ms = settle_ms
     rng = np.random.default_rng(2)
     out = {}
     try:
-        for item in spec.split(","):
-            kind, _, dims = item.lower().rpartition(":")
-            rows, columns, tokens = (int(v) for v in dims.split("x"))
+        for item, gtype, rows, columns, tokens in shapes:
             row = {}
             for path in (S.mm.GemmPath.CANONICAL, S.mm.GemmPath.AUTO, S.mm.GemmPath.EXACT_MFMA):
                 r = run_gemm(S, f"{item} {path.name}", [("write", [(rows, columns)])], tokens, steps, warmup, rng,
-                             path, gtype=PREFILL_TYPES[kind or "q4_0"])
+                             path, gtype=gtype)
                 row[path.name] = {"us": round(r["ms_per_step"] * 1e3, 2), "TFLOP/s": round(r["TFLOP/s"], 1),
                                   "kernel": r["kernels"][0]}
             out[item] = row

@@ -87,3 +87,18 @@ def test_more_than_one_gpu_is_refused():
 def test_decode_shapes_parse_with_q4_0_by_default():
     assert bench.parse_shapes("4096x14336,151936x1024:14, 3072X1024:8") == [
         (4096, 14336, 2), (151936, 1024, 14), (3072, 1024, 8)]
+
+
+def test_prefill_shapes_parse_with_an_optional_weight_type():
+    """--prefill's list: Q4_0 where no type is given, the GGUF type where one
+    is; an unknown type or a malformed shape stops with the item named."""
+    assert bench.parse_prefill_shapes("2048x8192x32, f32:300x1024x12,q6_k:512x2816x16") == [
+        ("2048x8192x32", 2, 2048, 8192, 32), ("f32:300x1024x12", 0, 300, 1024, 12),
+        ("q6_k:512x2816x16", 14, 512, 2816, 16)]
+    for bad in ("q5_k:64x256x2", "64x256", "64xKx2"):
+        try:
+            bench.parse_prefill_shapes(bad)
+        except SystemExit as e:
+            assert bad in str(e)
+        else:
+            raise AssertionError(bad)
