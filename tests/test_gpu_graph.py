@@ -85,6 +85,9 @@ class Step:
                 sums=5 * 320 * 32 * 4)
         product(c, [mm.Member(weight(c, Q4_0, 256, 1024))], 1024, 8, [256])
         product(c, [mm.Member(weight(c, Q6_K, 256, 1152))], 1152, 32, [256])
+        # the short-step tile's 32 x 32 form, and the whole-K matrix-core tile
+        product(c, [mm.Member(weight(c, Q4_0, 8192, 1024))], 1024, 32, [8192])
+        product(c, [mm.Member(weight(c, Q4_0, 49152, 1024))], 1024, 32, [49152])
         table = weight(c, Q4_0, 64, 1024)
         ids = hx.Buffer.of(np.array([3, 0, 63, 3, 17], np.uint32))
         self.owned.append(ids)
