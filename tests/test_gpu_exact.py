@@ -379,3 +379,26 @@ def test_short_step_tile_epilogues_same_bits(short_ctxs, activation):
     got, want = _both(short_ctxs, by_input, x, tokens, [500], epilogue=mm.Epilogue.GatedByInput,
                       activation=activation, out_width=500, gate_input=u, gate_input_stride=500, gate_input_column=50)
     _same(got, want, f"gated by input act={activation}")
+    # the same options and GatedByInput on the 32 x 32 tile (8,200 ragged rows)
+    big = synthetic.weight(rng, Q4_0, 8200, columns)
+    shape = mm.MatmulLaunch([mm.Member(mm.Weight.shape(Q4_0, 8200, columns))], 16, [16])
+    assert mm.plan_launch(shape, tokens).tile_rows == 32
+    bias = rng.standard_normal(8200).astype(np.float32)
+
+    def opts_big(ctx):
+        w = _weight(ctx, Q4_0, 8200, columns, big)
+        return [mm.Member(w)], [w]
+
+    got, want = _both(short_ctxs, opts_big, x, tokens, [8200], clip=[-1.5, 1.25, -3.0, 2.5], bias=bias,
+                      activated=True, activation=activation)
+    _same(got, want, f"write with options, 32 x 32, act={activation}")
+    u = rng.standard_normal((tokens, 8400)).astype(np.float32)
+
+    def by_input_big(ctx):
+        w = _weight(ctx, Q4_0, 8200, columns, big)
+        return [mm.Member(w, output_row=100)], [w]
+
+    got, want = _both(short_ctxs, by_input_big, x, tokens, [8400], epilogue=mm.Epilogue.GatedByInput,
+                      activation=activation, out_width=8400, gate_input=u, gate_input_stride=8400,
+                      gate_input_column=50)
+    _same(got, want, f"gated by input, 32 x 32, act={activation}")
